@@ -1,0 +1,371 @@
+"""``bdh_hip_ext``: Python binding of the gfx950 C-ABI library ``libbdh_hip.so``.
+
+Counterpart of the reference's native module ``bdh_cuda_ext`` (pybind module of
+csrc/tril_attn_bind.cpp:25-40): same entry names (``tril_score_v``,
+``tril_decode`` and their ``*_hip`` device-specific spellings) plus the
+entries this build adds (fused RoPE forward/backward, analytic backward, RoPE
+apply).  Only ROCm device tensors are accepted; there is no CPU path in this
+module (``has_hip`` is the analogue of the reference's ``has_cuda``).
+
+The C ABI (``include/bdh_hip.h``) takes plain pointers, sizes and strides;
+PyTorch is used here only for device memory (outputs and workspaces come from
+its caching allocator) and for the current stream.
+
+Importing this module loads the library and fails loudly (ImportError) when it
+is missing or does not export the expected symbols.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+from typing import Optional, Sequence, Tuple
+
+import torch
+
+__all__ = [
+    "has_hip",
+    "lib_path",
+    "version",
+    "tril_score_v",
+    "tril_score_v_hip",
+    "tril_rope_score_v",
+    "tril_decode",
+    "tril_decode_hip",
+    "tril_score_v_bwd",
+    "tril_rope_score_v_bwd",
+    "rope_rotate",
+    "profile_enable",
+    "profile_collect",
+    "launch_count",
+    "EXPORTED_SYMBOLS",
+]
+
+BDH_F32 = 0
+BDH_BF16 = 1
+
+EXPORTED_SYMBOLS = (
+    "bdh_version",
+    "bdh_error_string",
+    "bdh_tril_score_v_workspace",
+    "bdh_tril_score_v",
+    "bdh_tril_rope_score_v",
+    "bdh_tril_decode_workspace",
+    "bdh_tril_decode",
+    "bdh_rope_rotate",
+    "bdh_tril_score_v_bwd_workspace",
+    "bdh_tril_score_v_bwd",
+    "bdh_tril_rope_score_v_bwd_workspace",
+    "bdh_tril_rope_score_v_bwd",
+    "bdh_profile_enable",
+    "bdh_profile_collect",
+)
+
+
+class Tensor4(ctypes.Structure):
+    _fields_ = [
+        ("data", ctypes.c_void_p),
+        ("size", ctypes.c_int64 * 4),
+        ("stride", ctypes.c_int64 * 4),
+        ("dtype", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
+    ]
+
+
+def _find_lib() -> Path:
+    env = os.environ.get("BDH_HIP_LIB")
+    if env:
+        return Path(env)
+    return Path(__file__).resolve().parent / "libbdh_hip.so"
+
+
+def _load():
+    path = _find_lib()
+    if not path.exists():
+        raise ImportError(
+            f"bdh_hip_ext: {path} not found; build it with "
+            "`python bdh-gpu-fast_amd/build.py` (or __graft_entry__.build())"
+        )
+    lib = ctypes.CDLL(str(path))
+    missing = [s for s in EXPORTED_SYMBOLS if not hasattr(lib, s)]
+    if missing:
+        raise ImportError(f"bdh_hip_ext: {path} lacks symbols {missing}")
+    P = ctypes.POINTER(Tensor4)
+    vp, i32, i64, sz = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_size_t
+    fp = ctypes.POINTER(ctypes.c_float)
+    sig = {
+        "bdh_version": (ctypes.c_char_p, []),
+        "bdh_error_string": (ctypes.c_char_p, [ctypes.c_int]),
+        "bdh_tril_score_v_workspace": (sz, [i64, i64, i64, i64, i64, i32]),
+        "bdh_tril_score_v": (ctypes.c_int, [P, P, P, P, vp, sz, vp]),
+        "bdh_tril_rope_score_v": (ctypes.c_int, [P, P, P, fp, i64, P, vp, sz, vp]),
+        "bdh_tril_decode_workspace": (sz, [i64, i64, i64, i64, i64, i64]),
+        "bdh_tril_decode": (ctypes.c_int, [P, P, P, P, vp, sz, vp]),
+        "bdh_rope_rotate": (ctypes.c_int, [P, P, P, P, i32, vp]),
+        "bdh_tril_score_v_bwd_workspace": (sz, [i64, i64, i64, i64, i64, i64, i32]),
+        "bdh_tril_score_v_bwd": (ctypes.c_int, [P, P, P, P, P, P, P, vp, sz, vp]),
+        "bdh_tril_rope_score_v_bwd_workspace": (sz, [i64, i64, i64, i64, i64, i64, i32]),
+        "bdh_tril_rope_score_v_bwd": (ctypes.c_int, [P, P, P, fp, i64, P, P, vp, sz, vp]),
+        "bdh_profile_enable": (None, [i32]),
+        "bdh_profile_collect": (ctypes.c_int, [ctypes.c_char_p, i32, fp, i32]),
+    }
+    for name, (res, args) in sig.items():
+        f = getattr(lib, name)
+        f.restype = res
+        f.argtypes = args
+    return lib, path
+
+
+_lib, _path = _load()
+has_hip = True
+lib_path = str(_path)
+_launches = 0
+
+
+def version() -> str:
+    return _lib.bdh_version().decode()
+
+
+def launch_count() -> int:
+    """Number of successful library entry-point calls made through this module."""
+    return _launches
+
+
+def _dtype_code(t: torch.Tensor) -> int:
+    if t.dtype == torch.float32:
+        return BDH_F32
+    if t.dtype == torch.bfloat16:
+        return BDH_BF16
+    raise TypeError(f"bdh_hip_ext supports float32 and bfloat16 tensors, got {t.dtype}")
+
+
+def _t4(t: torch.Tensor) -> Tensor4:
+    if t.dim() != 4:
+        raise ValueError(f"bdh_hip_ext expects 4-D tensors, got shape {tuple(t.shape)}")
+    s = Tensor4()
+    s.data = t.data_ptr() if t.numel() > 0 else None
+    for i in range(4):
+        s.size[i] = t.size(i)
+        s.stride[i] = t.stride(i)
+    s.dtype = _dtype_code(t)
+    return s
+
+
+def _require_device(*ts: Optional[torch.Tensor]) -> torch.device:
+    dev = None
+    for t in ts:
+        if t is None:
+            continue
+        if not t.is_cuda:
+            raise RuntimeError(
+                "bdh_hip_ext: tensors must live on a ROCm GPU (the HIP library has no CPU path); "
+                f"got a tensor on {t.device}"
+            )
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise RuntimeError(f"bdh_hip_ext: tensors on different devices ({dev} vs {t.device})")
+    assert dev is not None
+    return dev
+
+
+def _stream(dev: torch.device) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+
+
+def _check(rc: int, what: str) -> None:
+    global _launches
+    if rc != 0:
+        raise RuntimeError(f"bdh_hip_ext.{what} failed: {_lib.bdh_error_string(rc).decode()} (code {rc})")
+    _launches += 1
+
+
+def _workspace(nbytes: int, dev: torch.device) -> Tuple[Optional[torch.Tensor], int]:
+    if nbytes == 0:
+        return None, 0
+    return torch.empty(int(nbytes), dtype=torch.uint8, device=dev), int(nbytes)
+
+
+def _freqs_ptr(freqs: torch.Tensor, n: int, dev: torch.device):
+    if freqs.dtype != torch.float32:
+        raise TypeError(f"freqs must be float32, got {freqs.dtype}")
+    f = freqs.reshape(-1)
+    if f.numel() != n:
+        raise ValueError(f"freqs must hold {n} values (one per latent dim), got {f.numel()}")
+    if f.device != dev:
+        raise RuntimeError(f"freqs on {f.device}, tensors on {dev}")
+    f = f.contiguous()
+    return f, ctypes.cast(ctypes.c_void_p(f.data_ptr()), ctypes.POINTER(ctypes.c_float))
+
+
+# ------------------------------------------------------------------- forward
+def tril_score_v(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
+    """``tril(q @ k^T, -1) @ v`` (no softmax, no scale) on the GPU; out in q's dtype."""
+    dev = _require_device(q, k, v)
+    B, H, T, Dk = q.shape
+    out = torch.empty(B, H, T, v.size(-1), dtype=q.dtype, device=dev)
+    with torch.cuda.device(dev):
+        need = _lib.bdh_tril_score_v_workspace(B, H, T, Dk, v.size(-1), _dtype_code(q))
+        ws, nb = _workspace(need, dev)
+        rc = _lib.bdh_tril_score_v(
+            ctypes.byref(_t4(q)), ctypes.byref(_t4(k)), ctypes.byref(_t4(v)), ctypes.byref(_t4(out)),
+            ws.data_ptr() if ws is not None else None, nb, _stream(dev),
+        )
+    _check(rc, "tril_score_v")
+    return out
+
+
+tril_score_v_hip = tril_score_v
+
+
+def tril_rope_score_v(
+    x: torch.Tensor,
+    v: torch.Tensor,
+    freqs: torch.Tensor,
+    rope_start: int = 0,
+    qr_out: Optional[torch.Tensor] = None,
+    out: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """Cold BDH attention with RoPE fused into the loads: ``tril(R(x) R(x)^T, -1) v``.
+
+    ``freqs`` is the (N,) or (1,1,1,N) fp32 frequency buffer (pairs share a
+    value); positions are ``rope_start + t``.  ``qr_out`` optionally receives
+    ``R(x)`` (e.g. the KR cache slot).
+    """
+    dev = _require_device(x, v, qr_out, out)
+    B, H, T, N = x.shape
+    f, fptr = _freqs_ptr(freqs, N, dev)
+    if out is None:
+        out = torch.empty(B, H, T, v.size(-1), dtype=x.dtype, device=dev)
+    with torch.cuda.device(dev):
+        need = _lib.bdh_tril_score_v_workspace(B, H, T, N, v.size(-1), _dtype_code(x))
+        ws, nb = _workspace(need, dev)
+        rc = _lib.bdh_tril_rope_score_v(
+            ctypes.byref(_t4(x)), ctypes.byref(_t4(v)), ctypes.byref(_t4(out)), fptr, int(rope_start),
+            ctypes.byref(_t4(qr_out)) if qr_out is not None else None,
+            ws.data_ptr() if ws is not None else None, nb, _stream(dev),
+        )
+    _check(rc, "tril_rope_score_v")
+    return out
+
+
+# -------------------------------------------------------------------- decode
+def tril_decode(q: torch.Tensor, k_past: torch.Tensor, v_past: torch.Tensor) -> torch.Tensor:
+    """``(q @ k_past^T) @ v_past`` against the packed past (strided cache views OK)."""
+    dev = _require_device(q, k_past, v_past)
+    B, H, Tq, Dk = q.shape
+    S = k_past.size(2)
+    Dv = v_past.size(-1)
+    out = torch.empty(B, H, Tq, Dv, dtype=q.dtype, device=dev)
+    with torch.cuda.device(dev):
+        need = _lib.bdh_tril_decode_workspace(B, H, Tq, S, Dk, Dv)
+        ws, nb = _workspace(need, dev)
+        rc = _lib.bdh_tril_decode(
+            ctypes.byref(_t4(q)), ctypes.byref(_t4(k_past)), ctypes.byref(_t4(v_past)), ctypes.byref(_t4(out)),
+            ws.data_ptr() if ws is not None else None, nb, _stream(dev),
+        )
+    _check(rc, "tril_decode")
+    return out
+
+
+tril_decode_hip = tril_decode
+
+
+# ------------------------------------------------------------------ backward
+def tril_score_v_bwd(
+    q: torch.Tensor, k: Optional[torch.Tensor], v: torch.Tensor, dout: torch.Tensor
+) -> Tuple[torch.Tensor, Optional[torch.Tensor], torch.Tensor]:
+    """Analytic gradients of ``tril(q k^T, -1) v``.
+
+    ``k is None`` means self attention (k is q): returns ``(dq + dk, None, dv)``.
+    Otherwise ``(dq, dk, dv)``.  Gradients take their input's dtype.
+    """
+    dev = _require_device(q, k, v, dout)
+    B, H, T, N = q.shape
+    dq = torch.empty_like(q, memory_format=torch.contiguous_format)
+    dk = None if k is None else torch.empty_like(k, memory_format=torch.contiguous_format)
+    dv = torch.empty_like(v, memory_format=torch.contiguous_format)
+    with torch.cuda.device(dev):
+        need = _lib.bdh_tril_score_v_bwd_workspace(B, H, v.size(1), T, N, v.size(-1), _dtype_code(q))
+        ws, nb = _workspace(need, dev)
+        rc = _lib.bdh_tril_score_v_bwd(
+            ctypes.byref(_t4(q)), ctypes.byref(_t4(k)) if k is not None else None, ctypes.byref(_t4(v)),
+            ctypes.byref(_t4(dout)), ctypes.byref(_t4(dq)), ctypes.byref(_t4(dk)) if dk is not None else None,
+            ctypes.byref(_t4(dv)), ws.data_ptr() if ws is not None else None, nb, _stream(dev),
+        )
+    _check(rc, "tril_score_v_bwd")
+    return dq, dk, dv
+
+
+def tril_rope_score_v_bwd(
+    x: torch.Tensor, v: torch.Tensor, dout: torch.Tensor, freqs: torch.Tensor, rope_start: int = 0
+) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Gradients ``(dx, dv)`` of :func:`tril_rope_score_v`."""
+    dev = _require_device(x, v, dout)
+    B, H, T, N = x.shape
+    f, fptr = _freqs_ptr(freqs, N, dev)
+    dx = torch.empty_like(x, memory_format=torch.contiguous_format)
+    dv = torch.empty_like(v, memory_format=torch.contiguous_format)
+    with torch.cuda.device(dev):
+        need = _lib.bdh_tril_rope_score_v_bwd_workspace(B, H, v.size(1), T, N, v.size(-1), _dtype_code(x))
+        ws, nb = _workspace(need, dev)
+        rc = _lib.bdh_tril_rope_score_v_bwd(
+            ctypes.byref(_t4(x)), ctypes.byref(_t4(v)), ctypes.byref(_t4(dout)), fptr, int(rope_start),
+            ctypes.byref(_t4(dx)), ctypes.byref(_t4(dv)), ws.data_ptr() if ws is not None else None, nb,
+            _stream(dev),
+        )
+    _check(rc, "tril_rope_score_v_bwd")
+    return dx, dv
+
+
+# ---------------------------------------------------------------------- RoPE
+def rope_rotate(
+    v: torch.Tensor,
+    cos: torch.Tensor,
+    sin: torch.Tensor,
+    out: Optional[torch.Tensor] = None,
+    *,
+    backward: bool = False,
+) -> torch.Tensor:
+    """Adjacent-pair RoPE with caller tables; ``cos``/``sin`` broadcast to ``v``.
+
+    ``v`` may have 1 to 4 dims (leading dims are padded to 4); ``out`` defaults
+    to a fresh contiguous tensor of ``v``'s dtype.
+    """
+    dev = _require_device(v, cos, sin, out)
+    shape = tuple(v.shape)
+    pad = (1,) * (4 - v.dim())
+    if v.dim() > 4:
+        raise ValueError(f"rope_rotate supports up to 4 dims, got {v.dim()}")
+    v4 = v.reshape(pad + shape) if pad else v
+    c4 = cos.expand(shape).reshape(pad + shape) if pad else cos.expand(shape)
+    s4 = sin.expand(shape).reshape(pad + shape) if pad else sin.expand(shape)
+    if out is None:
+        out = torch.empty(shape, dtype=v.dtype, device=dev)
+    o4 = out.view(pad + shape) if pad else out
+    with torch.cuda.device(dev):
+        rc = _lib.bdh_rope_rotate(
+            ctypes.byref(_t4(v4)), ctypes.byref(_t4(c4)), ctypes.byref(_t4(s4)), ctypes.byref(_t4(o4)),
+            1 if backward else 0, _stream(dev),
+        )
+    _check(rc, "rope_rotate")
+    return out
+
+
+# ---------------------------------------------------------------- profiling
+def profile_enable(on: bool = True) -> None:
+    """Bracket every library kernel launch with HIP events (on its stream)."""
+    _lib.bdh_profile_enable(1 if on else 0)
+
+
+def profile_collect(max_records: int = 65536) -> Sequence[Tuple[str, float]]:
+    """Wait for and return ``(kernel_name, ms)`` for launches since the last collect."""
+    name_len = 64
+    names = ctypes.create_string_buffer(name_len * max_records)
+    ms = (ctypes.c_float * max_records)()
+    n = _lib.bdh_profile_collect(names, name_len, ms, max_records)
+    raw = names.raw
+    return [
+        (raw[i * name_len:(i + 1) * name_len].split(b"\0", 1)[0].decode(), float(ms[i])) for i in range(n)
+    ]

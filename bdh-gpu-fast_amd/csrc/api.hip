@@ -1,0 +1,85 @@
+// Library metadata, error names and optional per-kernel event timing.
+#include <string.h>
+
+#include <vector>
+
+#include "common.h"
+
+namespace bdh {
+
+namespace {
+struct ProfRec {
+  const char* name;
+  hipEvent_t start, stop;
+};
+bool g_prof_on = false;
+std::vector<ProfRec> g_recs;          // recorded, not yet collected
+std::vector<hipEvent_t> g_free;       // reusable events
+constexpr size_t kMaxRecs = 1 << 16;  // drop records beyond this until collected
+
+hipEvent_t take_event() {
+  if (!g_free.empty()) {
+    hipEvent_t e = g_free.back();
+    g_free.pop_back();
+    return e;
+  }
+  hipEvent_t e = nullptr;
+  if (hipEventCreate(&e) != hipSuccess) return nullptr;
+  return e;
+}
+}  // namespace
+
+int prof_begin(const char* name, hipStream_t s) {
+  if (!g_prof_on || g_recs.size() >= kMaxRecs) return -1;
+  ProfRec r{name, take_event(), take_event()};
+  if (!r.start || !r.stop) return -1;
+  if (hipEventRecord(r.start, s) != hipSuccess) return -1;
+  g_recs.push_back(r);
+  return int(g_recs.size()) - 1;
+}
+
+void prof_end(int slot, hipStream_t s) {
+  if (slot < 0 || size_t(slot) >= g_recs.size()) return;
+  (void)hipEventRecord(g_recs[slot].stop, s);
+}
+
+}  // namespace bdh
+
+extern "C" const char* bdh_version(void) { return "bdh-hip 0.1 gfx950"; }
+
+extern "C" const char* bdh_error_string(int code) {
+  switch (code) {
+    case BDH_OK: return "ok";
+    case BDH_ERR_SHAPE: return "inconsistent or unsupported shapes";
+    case BDH_ERR_DTYPE: return "unsupported dtype or dtype combination";
+    case BDH_ERR_STRIDE: return "last dimension must have unit stride";
+    case BDH_ERR_WORKSPACE: return "workspace missing or too small";
+    case BDH_ERR_LAUNCH: return "HIP kernel launch failed";
+    case BDH_ERR_ARG: return "invalid argument";
+    case BDH_ERR_ALIAS: return "output overlaps an input";
+    default: return "unknown error";
+  }
+}
+
+extern "C" void bdh_profile_enable(int32_t on) { bdh::g_prof_on = on != 0; }
+
+extern "C" int bdh_profile_collect(char* names, int32_t name_len, float* ms, int32_t max) {
+  using namespace bdh;
+  int n = 0;
+  for (auto& r : g_recs) {
+    if (n < max) {
+      float t = -1.f;
+      if (hipEventSynchronize(r.stop) == hipSuccess) (void)hipEventElapsedTime(&t, r.start, r.stop);
+      if (ms) ms[n] = t;
+      if (names && name_len > 0) {
+        strncpy(names + size_t(n) * name_len, r.name, size_t(name_len) - 1);
+        names[size_t(n) * name_len + name_len - 1] = 0;
+      }
+      ++n;
+    }
+    g_free.push_back(r.start);
+    g_free.push_back(r.stop);
+  }
+  g_recs.clear();
+  return n;
+}

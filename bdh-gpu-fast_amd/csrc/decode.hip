@@ -1,0 +1,192 @@
+// KV-cache decode step for gfx950: out = (q K_past^T) V_past.
+//
+// HBM-bound: every past key row (N = 8192 elements) is read exactly once per
+// query row.  Work is split over the past (chunks of kChunk keys per
+// workgroup) so a B*H = 256 row batch still fills the chip; partial outputs
+// over chunks are summed by a second small kernel (the op is linear in the
+// scores, so no renormalisation is needed).
+//
+// Per workgroup: the query row is staged in LDS as fp32; each wave64 streams
+// one key row at a time with 16-byte loads (each lane covers 8 bf16 / 4 fp32
+// elements per 512-element stride), reduces the dot product across the wave
+// with shuffles, and records the score in LDS; then all 256 threads form the
+// partial out[d] = sum_s score_s V[s,d] with coalesced V row reads.
+#include "common.h"
+
+namespace bdh {
+
+constexpr int kDecNT = 256;
+constexpr int kChunk = 32;  // keys per workgroup
+
+struct DecodeArgs {
+  View q, k, v;
+  int64_t H, Tq, S, Dk, Dv, Hv;
+  int vec_k;
+  float* part;    // [nchunk][rows][Dv]
+  int64_t rows;   // B*H*Tq
+};
+
+template <typename TK>
+__device__ __forceinline__ float dot_row(const float* qs, const TK* kp, int64_t Dk, int lane, bool vec) {
+  float acc = 0.f;
+  if (vec) {
+    constexpr int EK = 16 / sizeof(TK);
+    int64_t e0 = int64_t(lane) * EK;
+    constexpr int STEP = 64 * EK;
+    // four 16-byte loads in flight per lane per iteration
+    for (; e0 + 3 * STEP < Dk; e0 += 4 * STEP) {
+      u32x4 w[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) w[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(kp + e0 + u * STEP));
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const TK* x = reinterpret_cast<const TK*>(&w[u]);
+        const float* qq = qs + e0 + u * STEP;
+#pragma unroll
+        for (int e = 0; e < EK; ++e) acc += qq[e] * to_f(x[e]);
+      }
+    }
+    for (; e0 < Dk; e0 += STEP) {
+      u32x4 w = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(kp + e0));
+      const TK* x = reinterpret_cast<const TK*>(&w);
+#pragma unroll
+      for (int e = 0; e < EK; ++e) acc += qs[e0 + e] * to_f(x[e]);
+    }
+  } else {
+    for (int64_t e = lane; e < Dk; e += 64) acc += qs[e] * to_f(kp[e]);
+  }
+  return wave_sum(acc);
+}
+
+template <typename TQ, typename TK, typename TV>
+__global__ __launch_bounds__(kDecNT) void k_decode_partial(DecodeArgs a) {
+  extern __shared__ float smem[];
+  float* qs = smem;              // Dk
+  float* sc = smem + a.Dk;       // kChunk scores
+  const int64_t row = blockIdx.y;
+  const int64_t t = row % a.Tq, bh = row / a.Tq;
+  const int64_t h = bh % a.H, b = bh / a.H;
+  const int64_t hv = a.Hv == 1 ? 0 : h;
+
+  const TQ* qp = static_cast<const TQ*>(a.q.p) + b * a.q.s0 + h * a.q.s1 + t * a.q.s2;
+  for (int64_t e = threadIdx.x; e < a.Dk; e += kDecNT) qs[e] = to_f(qp[e]);
+  __syncthreads();
+
+  const int64_t s0 = int64_t(blockIdx.x) * kChunk;
+  const int64_t s1 = min(a.S, s0 + kChunk);
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const TK* kb = static_cast<const TK*>(a.k.p) + b * a.k.s0 + h * a.k.s1;
+  for (int64_t s = s0 + wave; s < s1; s += kDecNT / 64) {
+    const float d = dot_row<TK>(qs, kb + s * a.k.s2, a.Dk, lane, a.vec_k != 0);
+    if (lane == 0) sc[s - s0] = d;
+  }
+  __syncthreads();
+
+  const TV* vb = static_cast<const TV*>(a.v.p) + b * a.v.s0 + hv * a.v.s1;
+  float* out = a.part + (int64_t(blockIdx.x) * a.rows + row) * a.Dv;
+  for (int64_t d = threadIdx.x; d < a.Dv; d += kDecNT) {
+    float o = 0.f;
+    for (int64_t s = s0; s < s1; ++s) o += sc[s - s0] * to_f(vb[s * a.v.s2 + d]);
+    out[d] = o;
+  }
+}
+
+template <typename TO>
+__global__ __launch_bounds__(kDecNT) void k_decode_reduce(const float* part, int64_t nchunk, int64_t rows,
+                                                          int64_t Dv, View o, int64_t H, int64_t Tq) {
+  const int64_t idx = int64_t(blockIdx.x) * kDecNT + threadIdx.x;
+  if (idx >= rows * Dv) return;
+  const int64_t row = idx / Dv, d = idx % Dv;
+  float s = 0.f;
+  for (int64_t c = 0; c < nchunk; ++c) s += part[(c * rows + row) * Dv + d];
+  const int64_t t = row % Tq, bh = row / Tq, h = bh % H, b = bh / H;
+  TO* op = static_cast<TO*>(const_cast<void*>(o.p)) + b * o.s0 + h * o.s1 + t * o.s2;
+  op[d] = from_f<TO>(s);
+}
+
+static int64_t n_chunks(int64_t S) { return S > 0 ? (S + kChunk - 1) / kChunk : 1; }
+
+template <typename TQ, typename TK, typename TV>
+static int launch_partial(const DecodeArgs& a, int64_t nchunk, hipStream_t s) {
+  dim3 grid((unsigned)(nchunk), unsigned(a.rows));
+  const size_t shm = size_t(a.Dk + kChunk) * sizeof(float);
+  BDH_LAUNCH("k_decode_partial", (k_decode_partial<TQ, TK, TV>), grid, dim3(kDecNT), shm, s, a);
+  return BDH_OK;
+}
+
+template <typename TQ, typename TK>
+static int pick_v(const DecodeArgs& a, int64_t nchunk, int32_t vdt, hipStream_t s) {
+  return vdt == BDH_BF16 ? launch_partial<TQ, TK, bf16_t>(a, nchunk, s)
+                         : launch_partial<TQ, TK, float>(a, nchunk, s);
+}
+
+template <typename TQ>
+static int pick_k(const DecodeArgs& a, int64_t nchunk, int32_t kdt, int32_t vdt, hipStream_t s) {
+  return kdt == BDH_BF16 ? pick_v<TQ, bf16_t>(a, nchunk, vdt, s) : pick_v<TQ, float>(a, nchunk, vdt, s);
+}
+
+}  // namespace bdh
+
+using namespace bdh;
+
+extern "C" size_t bdh_tril_decode_workspace(int64_t B, int64_t H, int64_t Tq, int64_t S, int64_t Dk,
+                                            int64_t Dv) {
+  (void)Dk;
+  return size_t(n_chunks(S)) * size_t(B * H * Tq) * size_t(Dv) * sizeof(float);
+}
+
+extern "C" int bdh_tril_decode(const bdh_tensor4* q, const bdh_tensor4* k, const bdh_tensor4* v,
+                               const bdh_tensor4* out, void* workspace, size_t workspace_bytes,
+                               bdh_stream stream) {
+  BDH_TRY(check_view(q));
+  BDH_TRY(check_view(k));
+  BDH_TRY(check_view(v));
+  BDH_TRY(check_view(out));
+  const int64_t B = q->size[0], H = q->size[1], Tq = q->size[2], Dk = q->size[3];
+  const int64_t S = k->size[2], Dv = v->size[3];
+  // Contract of kernels/cuda_attn.py:114-131 / csrc/tril_attn_cpu.cpp:214-223.
+  if (k->size[0] != B || k->size[1] != H || k->size[3] != Dk) return BDH_ERR_SHAPE;
+  if (v->size[0] != B || v->size[2] != S) return BDH_ERR_SHAPE;
+  if (v->size[1] != 1 && v->size[1] != H) return BDH_ERR_SHAPE;
+  if (out->size[0] != B || out->size[1] != H || out->size[2] != Tq || out->size[3] != Dv)
+    return BDH_ERR_SHAPE;
+  if (views_overlap(out, q) || views_overlap(out, k) || views_overlap(out, v)) return BDH_ERR_ALIAS;
+  if (B * H * Tq > 65535 || n_chunks(S) > int64_t(1) << 30) return BDH_ERR_SHAPE;
+  if ((Dk + kChunk) * int64_t(sizeof(float)) > 64 * 1024) return BDH_ERR_SHAPE;
+  if (numel4(out) == 0) return BDH_OK;
+  const int64_t nchunk = n_chunks(S);
+  const size_t need = bdh_tril_decode_workspace(B, H, Tq, S, Dk, Dv);
+  if (workspace == nullptr || workspace_bytes < need) return BDH_ERR_WORKSPACE;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+
+  DecodeArgs a;
+  a.q = view_of(q);
+  a.q.s1 = q->stride[1];
+  a.k = view_of(k);
+  a.k.s1 = k->stride[1];
+  a.v = view_of(v);
+  a.H = H;
+  a.Tq = Tq;
+  a.S = S;
+  a.Dk = Dk;
+  a.Dv = Dv;
+  a.Hv = v->size[1];
+  a.vec_k = vec16_ok(k) ? 1 : 0;
+  a.part = static_cast<float*>(workspace);
+  a.rows = B * H * Tq;
+  const int rc = q->dtype == BDH_BF16 ? pick_k<bf16_t>(a, nchunk, k->dtype, v->dtype, st)
+                                      : pick_k<float>(a, nchunk, k->dtype, v->dtype, st);
+  if (rc != BDH_OK) return rc;
+
+  View o = view_of(out);
+  o.s1 = out->stride[1];
+  const int64_t total = a.rows * Dv;
+  dim3 grid((unsigned)((total + kDecNT - 1) / kDecNT));
+  if (out->dtype == BDH_BF16)
+    BDH_LAUNCH("k_decode_reduce", k_decode_reduce<bf16_t>, grid, dim3(kDecNT), 0, st, a.part, nchunk,
+               a.rows, Dv, o, H, Tq);
+  else
+    BDH_LAUNCH("k_decode_reduce", k_decode_reduce<float>, grid, dim3(kDecNT), 0, st, a.part, nchunk,
+               a.rows, Dv, o, H, Tq);
+  return BDH_OK;
+}

@@ -1,0 +1,48 @@
+// Forward-kernel arguments and launch helpers shared by fwd.hip and bwd.hip.
+#pragma once
+
+#include "tile_gemm.h"
+
+namespace bdh {
+
+// Split-K is chosen so that one launch has about this many workgroups.
+constexpr int64_t kTargetWorkgroups = 1024;
+
+struct FwdPlan {
+  int64_t nt = 0;      // 128-row tiles per slab
+  int64_t ntl = 0;     // packed lower tiles per slab
+  int64_t splits = 1;  // split-K factor
+  int64_t kc = 0;      // k extent of one split (multiple of the K stage)
+  size_t ws_bytes = 0; // partial score tiles
+};
+
+struct ScoresArgs {
+  View q, k;
+  int64_t H, T, K;
+  int q_is_k;
+  bool vec_q, vec_k;
+  const float* freqs;
+  int64_t rope_start;
+  float* sp;  // partial tiles [split][slab][tile][128*128]
+  int64_t kc;
+  int ntl;
+  View qr;    // optional RoPE(x) output (diagonal tiles write it)
+  bool qr_bf;
+};
+
+struct ScoreVArgs {
+  const float* sp;
+  int64_t split_stride;
+  int nsplit;
+  int ntl;
+  View v;
+  int64_t H, Hv, T, Dv;
+  bool vec4_v;
+  View o;
+};
+
+FwdPlan plan_fwd(int64_t B, int64_t H, int64_t T, int64_t K, bool bf);
+int run_scores(const ScoresArgs& a, const FwdPlan& p, int64_t BH, bool bf, bool rope, bool trans,
+               hipStream_t s);
+
+}  // namespace bdh

@@ -1,0 +1,117 @@
+// RoPE apply for gfx950: adjacent-pair rotation with caller-provided cos/sin
+// tables (bdh_rope_rotate / bdh_rope_rotate_paired surface).
+//
+// Rounding follows the reference exactly (no FMA contraction):
+//  - fp32 v: y0 = x0*c0 - x1*s0, y1 = x1*c1 + x0*s1 (fp32 products, fp32 add);
+//  - bf16 v: every product is rounded to bf16, then the bf16 terms are added
+//    and rounded again (kernels/rope.py:120-122);
+//  - backward: dx0 = g0*c0 + g1*s1, dx1 = -g0*s0 + g1*c1 with the same
+//    rounding rules (kernels/rope.py:543-556).
+// The result is cast to the output dtype on store.
+#include "common.h"
+
+namespace bdh {
+
+struct RopeArgs {
+  View v, c, s, o;
+  int64_t H, T, N;
+  int64_t pairs;  // rows * N / 2
+  int bwd;
+};
+
+template <typename TV, typename TC, typename TO>
+__global__ __launch_bounds__(256) void k_rope(RopeArgs a) {
+#pragma clang fp contract(off)
+  const int64_t idx = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  if (idx >= a.pairs) return;
+  const int64_t np = a.N / 2;
+  const int64_t row = idx / np, p = idx % np;
+  const int64_t t = row % a.T, bh = row / a.T, h = bh % a.H, b = bh / a.H;
+  const TV* vp = static_cast<const TV*>(a.v.p) + b * a.v.s0 + h * a.v.s1 + t * a.v.s2 + 2 * p;
+  const TC* cp = static_cast<const TC*>(a.c.p) + b * a.c.s0 + h * a.c.s1 + t * a.c.s2 + 2 * p;
+  const TC* sp = static_cast<const TC*>(a.s.p) + b * a.s.s0 + h * a.s.s1 + t * a.s.s2 + 2 * p;
+  TO* op = static_cast<TO*>(const_cast<void*>(a.o.p)) + b * a.o.s0 + h * a.o.s1 + t * a.o.s2 + 2 * p;
+  const float x0 = to_f(vp[0]), x1 = to_f(vp[1]);
+  const float c0 = to_f(cp[0]), c1 = to_f(cp[1]);
+  const float s0 = to_f(sp[0]), s1 = to_f(sp[1]);
+  float y0, y1;
+  if constexpr (std::is_same<TV, bf16_t>::value) {
+    if (a.bwd) {
+      y0 = bf_round(bf_round(x0 * c0) + bf_round(x1 * s1));
+      y1 = bf_round(bf_round((-x0) * s0) + bf_round(x1 * c1));
+    } else {
+      y0 = bf_round(bf_round(x0 * c0) + bf_round((-x1) * s0));
+      y1 = bf_round(bf_round(x1 * c1) + bf_round(x0 * s1));
+    }
+  } else {
+    if (a.bwd) {
+      const float p0 = x0 * c0, p1 = x1 * s1, p2 = x0 * s0, p3 = x1 * c1;
+      y0 = p0 + p1;
+      y1 = -p2 + p3;
+    } else {
+      const float p0 = x0 * c0, p1 = x1 * s0, p2 = x1 * c1, p3 = x0 * s1;
+      y0 = p0 - p1;
+      y1 = p2 + p3;
+    }
+  }
+  op[0] = from_f<TO>(y0);
+  op[1] = from_f<TO>(y1);
+}
+
+template <typename TV, typename TC, typename TO>
+static int launch_rope(const RopeArgs& a, hipStream_t s) {
+  dim3 grid((unsigned)((a.pairs + 255) / 256));
+  BDH_LAUNCH("k_rope", (k_rope<TV, TC, TO>), grid, dim3(256), 0, s, a);
+  return BDH_OK;
+}
+
+template <typename TV, typename TC>
+static int pick_o(const RopeArgs& a, int32_t odt, hipStream_t s) {
+  return odt == BDH_BF16 ? launch_rope<TV, TC, bf16_t>(a, s) : launch_rope<TV, TC, float>(a, s);
+}
+
+template <typename TV>
+static int pick_c(const RopeArgs& a, int32_t cdt, int32_t odt, hipStream_t s) {
+  return cdt == BDH_BF16 ? pick_o<TV, bf16_t>(a, odt, s) : pick_o<TV, float>(a, odt, s);
+}
+
+static View full_view(const bdh_tensor4* t) {
+  View v;
+  v.p = t->data;
+  v.s0 = t->stride[0];
+  v.s1 = t->stride[1];
+  v.s2 = t->stride[2];
+  return v;
+}
+
+}  // namespace bdh
+
+using namespace bdh;
+
+extern "C" int bdh_rope_rotate(const bdh_tensor4* v, const bdh_tensor4* cos, const bdh_tensor4* sin,
+                               const bdh_tensor4* out, int32_t backward, bdh_stream stream) {
+  BDH_TRY(check_view(v));
+  BDH_TRY(check_view(cos));
+  BDH_TRY(check_view(sin));
+  BDH_TRY(check_view(out));
+  if (cos->dtype != sin->dtype) return BDH_ERR_DTYPE;
+  for (int i = 0; i < 4; ++i)
+    if (cos->size[i] != v->size[i] || sin->size[i] != v->size[i] || out->size[i] != v->size[i])
+      return BDH_ERR_SHAPE;
+  if (v->size[3] % 2 != 0) return BDH_ERR_SHAPE;
+  if (views_overlap(out, v) || views_overlap(out, cos) || views_overlap(out, sin)) return BDH_ERR_ALIAS;
+  if (numel4(v) == 0) return BDH_OK;
+  RopeArgs a;
+  a.v = full_view(v);
+  a.c = full_view(cos);
+  a.s = full_view(sin);
+  a.o = full_view(out);
+  a.H = v->size[1];
+  a.T = v->size[2];
+  a.N = v->size[3];
+  a.pairs = v->size[0] * v->size[1] * v->size[2] * (v->size[3] / 2);
+  a.bwd = backward != 0;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  return v->dtype == BDH_BF16 ? pick_c<bf16_t>(a, cos->dtype, out->dtype, s)
+                              : pick_c<float>(a, cos->dtype, out->dtype, s);
+}

@@ -1,0 +1,79 @@
+"""BDH attention + RoPE operators: the reference's ``kernels`` import surface.
+
+Drop-in counterpart of the reference package ``kernels`` (kernels/__init__.py):
+``bdh.py`` imports ``bdh_attn``, ``bdh_attn_decode``, ``resolve_attn_impl``,
+``_env_autograd_enabled``, ``bdh_rope_rotate``, ``bdh_rope_rotate_paired`` and
+``resolve_rope_impl`` from here unchanged.  ``BDH_ATTN_IMPL=hip`` /
+``BDH_ROPE_IMPL=hip`` select the gfx950 HIP kernels; ``eager`` (default) keeps
+the reference's PyTorch semantics.
+"""
+
+from .attention import DEFAULT_BLOCK_COLD, DEFAULT_BLOCK_DECODE, eager_decode_attn, eager_tril_attn
+from .attention_bwd import (
+    StrictTrilAttnFn,
+    StrictTrilSelfAttnFn,
+    TrilRopeSelfAttnFn,
+    analytic_tril_attn_backward,
+    analytic_tril_attn_backward_blocked,
+    strict_tril_attn,
+)
+from .attention_dispatch import (
+    DEFAULT_ATTN_AUTO_THRESHOLD,
+    attn_auto_cold_threshold,
+    attn_auto_enabled,
+    attn_auto_threshold,
+    backend_info,
+    bdh_attn,
+    bdh_attn_decode,
+    bdh_attn_rope,
+    resolve_attn_impl,
+    resolve_cold_impl,
+    resolve_decode_impl,
+)
+from .hip_attn import (
+    ext_status,
+    has_hip_ext,
+    has_hip_kernel,
+    tril_decode,
+    tril_rope_score_v,
+    tril_score_v,
+)
+from .rope import get_freqs, rope_cos_sin
+from .rope_dispatch import backend_info as rope_backend_info
+from .rope_dispatch import bdh_rope_rotate, bdh_rope_rotate_paired, resolve_rope_impl
+
+__all__ = [
+    "bdh_attn",
+    "bdh_attn_rope",
+    "bdh_attn_decode",
+    "resolve_attn_impl",
+    "resolve_cold_impl",
+    "resolve_decode_impl",
+    "attn_auto_threshold",
+    "attn_auto_cold_threshold",
+    "attn_auto_enabled",
+    "DEFAULT_ATTN_AUTO_THRESHOLD",
+    "DEFAULT_BLOCK_COLD",
+    "DEFAULT_BLOCK_DECODE",
+    "backend_info",
+    "strict_tril_attn",
+    "StrictTrilAttnFn",
+    "StrictTrilSelfAttnFn",
+    "TrilRopeSelfAttnFn",
+    "analytic_tril_attn_backward",
+    "analytic_tril_attn_backward_blocked",
+    "eager_tril_attn",
+    "eager_decode_attn",
+    "tril_score_v",
+    "tril_rope_score_v",
+    "tril_decode",
+    "has_hip_ext",
+    "has_hip_kernel",
+    "ext_status",
+    "get_freqs",
+    "rope_cos_sin",
+    "bdh_rope_rotate",
+    "bdh_rope_rotate_paired",
+    "resolve_rope_impl",
+    "rope_backend_info",
+]

@@ -1,0 +1,156 @@
+"""Autograd for strict-tril BDH attention: tril(Q @ K.T, -1) @ V.
+
+Mirrors the reference surface kernels/attention_bwd.py:
+``analytic_tril_attn_backward`` (dense, :45-83), ``StrictTrilAttnFn``
+(:218-256), ``StrictTrilSelfAttnFn`` (:259-291; Q is K -> returns dQ + dK),
+``strict_tril_attn`` (:294-320) and ``_env_autograd_enabled`` (:323-325).
+
+For ``impl="hip"`` the forward is the HIP kernel and the backward is the HIP
+analytic backward (one library call: recomputed scores, G = dS + dS^T, merged
+dQ, head-summed dV).  ``eager`` keeps the reference's dense PyTorch math.
+
+:class:`TrilRopeSelfAttnFn` covers the fused RoPE entry (Q = K = RoPE(x)):
+its backward returns dx directly (RoPE and its transpose fused in-kernel).
+"""
+
+from __future__ import annotations
+
+import os
+from typing import Optional
+
+import torch
+
+from .attention import eager_tril_attn
+from . import hip_attn
+
+_VALID_IMPLS = ("eager", "hip")
+
+
+def analytic_tril_attn_backward(Q, K, V, dO):
+    """Dense analytic gradients of ``tril(Q K^T, -1) V`` (reference attention_bwd.py:45-83)."""
+    B, H, T, _ = Q.shape
+    D = V.shape[-1]
+    bcast = V.size(1) == 1 and H != 1
+    Vh = V.expand(B, H, T, D) if bcast else V
+    M = (Q @ K.transpose(-2, -1)).tril(diagonal=-1)
+    dS = (dO @ Vh.transpose(-2, -1)).tril(diagonal=-1)
+    dQ = dS @ K
+    dK = dS.transpose(-2, -1) @ Q
+    dVh = M.transpose(-2, -1) @ dO
+    dV = dVh.sum(dim=1, keepdim=True) if bcast else dVh
+    return dQ, dK, dV
+
+
+# The reference's tiled variant (attention_bwd.py:86-181) exists to bound the
+# score memory of its PyTorch backends; the same gradients come from the dense
+# form here, and ``hip`` tiles inside the kernel.
+analytic_tril_attn_backward_blocked = analytic_tril_attn_backward
+
+
+def _normalize_impl(impl: Optional[str]) -> str:
+    name = (impl or "eager").strip().lower()
+    if name not in _VALID_IMPLS:
+        raise ValueError(f"unknown attn impl={impl!r} (expected one of {_VALID_IMPLS})")
+    return name
+
+
+def _use_blocked_analytic_bwd(impl: str) -> bool:
+    """True when the backward runs tiled (no T x T tensor): the HIP kernels."""
+    return _normalize_impl(impl) == "hip"
+
+
+def _forward_impl(Q, K, V, impl: str):
+    name = _normalize_impl(impl)
+    if name == "eager":
+        return eager_tril_attn(Q, K, V)
+    return hip_attn.tril_score_v(Q, K, V)
+
+
+class StrictTrilAttnFn(torch.autograd.Function):
+    """Forward via eager / hip; analytic backward for distinct Q, K, V."""
+
+    @staticmethod
+    def forward(ctx, Q, K, V, impl: str):  # type: ignore[override]
+        ctx.impl = impl
+        ctx.save_for_backward(Q, K, V)
+        with torch.no_grad():
+            return _forward_impl(Q, K, V, impl)
+
+    @staticmethod
+    def backward(ctx, dO):  # type: ignore[override]
+        Q, K, V = ctx.saved_tensors
+        if _use_blocked_analytic_bwd(ctx.impl):
+            dQ, dK, dV = hip_attn.tril_score_v_bwd(Q, K, V, dO.to(Q.dtype))
+            dV = dV.to(V.dtype)
+        else:
+            dQ, dK, dV = analytic_tril_attn_backward(Q, K, V, dO)
+        return dQ, dK, dV, None
+
+
+class StrictTrilSelfAttnFn(torch.autograd.Function):
+    """Self-attention form (K is Q): returns dQ + dK for Q (reference :259-291)."""
+
+    @staticmethod
+    def forward(ctx, Q, V, impl: str):  # type: ignore[override]
+        ctx.impl = impl
+        ctx.save_for_backward(Q, V)
+        with torch.no_grad():
+            return _forward_impl(Q, Q, V, impl)
+
+    @staticmethod
+    def backward(ctx, dO):  # type: ignore[override]
+        Q, V = ctx.saved_tensors
+        if _use_blocked_analytic_bwd(ctx.impl):
+            dQm, _, dV = hip_attn.tril_score_v_bwd(Q, None, V, dO.to(Q.dtype))
+            return dQm, dV.to(V.dtype), None
+        dQ, dK, dV = analytic_tril_attn_backward(Q, Q, V, dO)
+        return dQ + dK, dV, None
+
+
+class TrilRopeSelfAttnFn(torch.autograd.Function):
+    """``tril(R(x) R(x)^T, -1) V`` with R = BDH RoPE fused into the HIP kernels.
+
+    The backward returns dx (RoPE^T of the merged dQR) and dV; ``freqs`` is a
+    constant buffer (no gradient), like the reference's detached cos/sin.
+    """
+
+    @staticmethod
+    def forward(ctx, x, V, freqs, rope_start: int, qr_out=None):  # type: ignore[override]
+        ctx.rope_start = int(rope_start)
+        ctx.save_for_backward(x, V, freqs)
+        with torch.no_grad():
+            return hip_attn.tril_rope_score_v(x, V, freqs, rope_start, qr_out=qr_out)
+
+    @staticmethod
+    def backward(ctx, dO):  # type: ignore[override]
+        x, V, freqs = ctx.saved_tensors
+        dx, dV = hip_attn.tril_rope_score_v_bwd(x, V, dO.to(x.dtype), freqs, ctx.rope_start)
+        return dx, dV.to(V.dtype), None, None, None
+
+
+def strict_tril_attn(Q, K, V, *, impl: Optional[str] = None, use_fn: Optional[bool] = None):
+    """Strict-tril score @ V with optional analytic autograd.Function (reference :294-320)."""
+    if use_fn is None:
+        use_fn = _env_autograd_enabled()
+    name = _normalize_impl(impl if impl is not None else os.environ.get("BDH_ATTN_IMPL", "eager"))
+    if use_fn:
+        if Q is K:
+            return StrictTrilSelfAttnFn.apply(Q, V, name)
+        return StrictTrilAttnFn.apply(Q, K, V, name)
+    return _forward_impl(Q, K, V, name)
+
+
+def _env_autograd_enabled() -> bool:
+    raw = os.environ.get("BDH_ATTN_AUTOGRAD", "").strip().lower()
+    return raw in ("1", "true", "yes", "on")
+
+
+__all__ = [
+    "analytic_tril_attn_backward",
+    "analytic_tril_attn_backward_blocked",
+    "StrictTrilAttnFn",
+    "StrictTrilSelfAttnFn",
+    "TrilRopeSelfAttnFn",
+    "strict_tril_attn",
+    "_env_autograd_enabled",
+]

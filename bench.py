@@ -1,0 +1,303 @@
+#!/usr/bin/env python3
+"""Benchmark of the BDH strict-tril attention hot path on one MI355X.
+
+Headline (``value``): the cold tril-attention + RoPE prefill forward at the
+BASELINE shape B=8, nh=4, T=512, N=8192, D=256 in bf16, RoPE fused into the
+HIP kernels (``kernels.bdh_attn_rope(impl="hip")``), inputs resident in HBM.
+One step = one call over the whole batch.  Throughput is the algorithmic
+F = B*nh*(N+D)*T*(T-1) flops per step (strict lower triangle; RoPE's
+elementwise work is not counted) divided by the measured step time.
+
+The JSON line also carries:
+  * ``roofline``: the dominant kernel (``k_scores``, the score tiles QR QR^T)
+    timed with HIP events on its launch stream over a timed region of the same
+    K steps; achieved = its algorithmic flops B*nh*N*T*(T-1) / mean duration,
+    against the 2.5 PFLOP/s bf16 dense MFMA peak.  ``traffic`` is the HBM
+    bytes per launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE runs
+    (profiles/k_scores_c1_bf16_pmc.txt) when present, else null.
+  * ``cpu_baseline``: the CPU oracle (numpy restatement of the reference CPU
+    path, fp32, BLAS threads as reported) on a bounded sample of the same
+    workload, in the same unit.
+  * ``extra``: other hot-path legs (decode step GB/s at C3, training op
+    fwd+bwd TFLOP/s at C4, the unfused path and torch eager on the GPU).
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extra]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import re
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for _p in (str(ROOT), str(ROOT / "bdh-gpu-fast_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "tril-attn TFLOP/s & %MFMA peak; BDH prefill tok/s; decode tok/s + HBM GB/s"
+PEAK_BF16_TFLOPS = 2500.0
+PEAK_HBM_GBS = 8000.0
+C1 = dict(B=8, nh=4, T=512, N=8192, D=256)
+C3 = dict(B=64, nh=4, N=8192, D=256, S=(256, 384, 511))
+C4 = dict(B=16, nh=4, T=1024, N=8192, D=256)
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def attn_flops(B, nh, T, N, D) -> float:
+    return float(B * nh * (N + D) * T * (T - 1))
+
+
+def time_steps(fn, steps: int, warmup: int) -> float:
+    """ms per step over exactly ``steps`` calls, synchronised on both sides."""
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for _ in range(steps):
+        fn()
+    t1.record()
+    torch.cuda.synchronize()
+    return t0.elapsed_time(t1) / steps
+
+
+def kernel_means(fn, steps: int) -> dict:
+    """Mean per-kernel duration (ms) from the library's HIP events on the launch stream."""
+    import torch
+    import bdh_hip_ext as ext
+
+    torch.cuda.synchronize()
+    ext.profile_enable(True)
+    try:
+        for _ in range(steps):
+            fn()
+        torch.cuda.synchronize()
+        recs = ext.profile_collect()
+    finally:
+        ext.profile_enable(False)
+    agg: dict = {}
+    for name, ms in recs:
+        agg.setdefault(name, []).append(ms)
+    return {k: (sum(v) / len(v), len(v) // steps) for k, v in agg.items()}
+
+
+def pmc_traffic(kernel: str, workload_tag: str):
+    """HBM bytes per launch of ``kernel`` from the committed rocprofv3 summary, or None."""
+    path = ROOT / "profiles" / f"{kernel}_{workload_tag}_pmc.txt"
+    if not path.exists():
+        return None
+    m = re.search(r"hbm_bytes_per_launch\s*[:=]\s*([0-9.eE+]+)", path.read_text())
+    return float(m.group(1)) if m else None
+
+
+def cpu_baseline(reps: int = 3) -> dict:
+    """Oracle (numpy, fp32) timing of a bounded sample of C1 on the host cores."""
+    import numpy as np
+
+    import oracle as O
+
+    try:
+        from threadpoolctl import threadpool_info
+
+        threads = max((i.get("num_threads", 1) for i in threadpool_info() if i.get("user_api") == "blas"), default=1)
+    except Exception:  # pragma: no cover - informational only
+        threads = os.cpu_count() or 1
+    Bs = 1
+    nh, T, N, D = C1["nh"], C1["T"], C1["N"], C1["D"]
+    rng = np.random.default_rng(0)
+    x = np.maximum(rng.standard_normal((Bs, nh, T, N), dtype=np.float32) * np.float32(0.32), 0)
+    v = rng.standard_normal((Bs, 1, T, D), dtype=np.float32)
+    f = O.get_freqs(N)
+    O.tril_rope_score_v(x, v, f, 0)  # warmup
+    times = []
+    for _ in range(reps):
+        t = time.perf_counter()
+        O.tril_rope_score_v(x, v, f, 0)
+        times.append(time.perf_counter() - t)
+    med = statistics.median(times)
+    F = attn_flops(Bs, nh, T, N, D)
+    return {
+        "value": F / med / 1e12,
+        "unit": "TFLOP/s",
+        "cores": int(threads),
+        "kind": "port",
+        "sample": f"C1 fp32 with B={Bs} of 8 (nh=4 T=512 N=8192 D=256): numpy RoPE + tiled strict-tril "
+        f"score x V (oracle/tril_attn_oracle.py), median of {reps} after 1 warmup, {med * 1e3:.0f} ms per call",
+        "ms_per_call": med * 1e3,
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
+    ap.add_argument("--no-extra", action="store_true", help="skip the decode / backward / comparison legs")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(
+            "bench.py measures one GPU only: the strict-tril attention hot path is benchmarked on a single "
+            "MI355X (per-GPU work at its real shape); multi-GPU runs are not part of this build.",
+            file=sys.stderr,
+        )
+        return 2
+
+    import torch
+
+    import bdh_hip_ext as ext
+    import kernels
+
+    assert torch.cuda.is_available(), "bench.py needs a ROCm GPU"
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+
+    B, nh, T, N, D = (C1[k] for k in ("B", "nh", "T", "N", "D"))
+    gq = torch.Generator(device=dev).manual_seed(0)
+    gv = torch.Generator(device=dev).manual_seed(1)
+    x = torch.relu(0.32 * torch.randn(B, nh, T, N, generator=gq, device=dev)).to(torch.bfloat16)
+    v = torch.randn(B, 1, T, D, generator=gv, device=dev).to(torch.bfloat16)
+    freqs = kernels.get_freqs(N).to(dev)
+
+    def step():
+        return kernels.bdh_attn_rope(x, v, freqs, 0, impl="hip")
+
+    launches0 = ext.launch_count()
+    ms = time_steps(step, args.steps, args.warmup)
+    assert ext.launch_count() - launches0 == args.steps + args.warmup, "HIP library calls missing"
+    F = attn_flops(B, nh, T, N, D)
+    value = F / (ms * 1e-3) / 1e12
+    log(f"[bench] fused RoPE tril-attn fwd C1 bf16: {ms * 1e3:.1f} us/step, {value:.1f} TFLOP/s")
+
+    means = kernel_means(step, args.steps)
+    k_ms = means["k_scores"][0]
+    F_scores = float(B * nh * N * T * (T - 1))
+    achieved = F_scores / (k_ms * 1e-3) / 1e12
+    traffic = pmc_traffic("k_scores", "c1_bf16")
+    roofline = {
+        "bound": "mfma",
+        "kernel": "k_scores",
+        "achieved": achieved,
+        "peak": PEAK_BF16_TFLOPS,
+        "unit": "TFLOP/s",
+        "frac": achieved / PEAK_BF16_TFLOPS,
+        "traffic": traffic,
+        "kernel_us": k_ms * 1e3,
+        "kernels_us": {k: round(v[0] * 1e3, 2) for k, v in means.items()},
+        "algorithmic_flops_per_launch": F_scores,
+    }
+    log(f"[bench] kernels: {roofline['kernels_us']} -> k_scores {achieved:.1f} TFLOP/s")
+
+    extra: dict = {}
+    if not args.no_extra:
+        extra = run_extra(torch, ext, kernels, dev, max(3, args.steps // 5), max(2, args.warmup // 5), x, v)
+
+    cpu = None
+    if not args.no_cpu:
+        log("[bench] cpu baseline (oracle on host cores)...")
+        cpu = cpu_baseline()
+        log(f"[bench] cpu baseline: {cpu['value']:.4f} TFLOP/s on {cpu['cores']} threads")
+
+    line = {
+        "metric": METRIC,
+        "value": value,
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": "C1 tril-attention + RoPE prefill forward (fused RoPE), bf16 in / fp32 accumulate",
+            "B": B,
+            "nh": nh,
+            "T": T,
+            "N": N,
+            "D": D,
+            "rope_theta": 65536,
+            "frac_of_bf16_peak": value / PEAK_BF16_TFLOPS,
+        },
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+def run_extra(torch, ext, kernels, dev, steps, warmup, x, v) -> dict:
+    out: dict = {}
+    B, nh, T, N, D = (C1[k] for k in ("B", "nh", "T", "N", "D"))
+    F = attn_flops(B, nh, T, N, D)
+    freqs = kernels.get_freqs(N).to(dev)
+    qr = torch.empty_like(x)
+    kernels.bdh_attn_rope(x, v, freqs, 0, out_kr=qr, impl="hip")
+    ms = time_steps(lambda: kernels.bdh_attn(qr, qr, v, impl="hip"), steps, warmup)
+    out["c1_unfused_tril_score_v_on_qr"] = {"us": ms * 1e3, "tflops": F / ms / 1e9}
+    cos, sin = kernels.rope_cos_sin(T, 0, freqs)
+    ms_r = time_steps(lambda: kernels.bdh_rope_rotate(x, cos, sin, out=qr, impl="hip"), steps, warmup)
+    out["c1_rope_apply_hip"] = {"us": ms_r * 1e3, "gbs": 2 * x.numel() * 2 / ms_r / 1e6}
+
+    def eager():
+        s = qr @ qr.mT.contiguous()
+        s.tril_(-1)
+        return s @ v
+
+    ms_e = time_steps(eager, steps, warmup)
+    out["c1_torch_eager_gpu_on_qr"] = {"us": ms_e * 1e3, "tflops": F / ms_e / 1e9}
+    log(f"[bench] unfused {ms * 1e3:.1f} us, rope {ms_r * 1e3:.1f} us, torch eager {ms_e * 1e3:.1f} us")
+
+    # Decode step (C3): B=64 nh=4 N=8192 D=256, bf16 cache read in place.
+    Bd, nhd, Nd, Dd = (C3[k] for k in ("B", "nh", "N", "D"))
+    cap = max(C3["S"]) + 1
+    g = torch.Generator(device=dev).manual_seed(5)
+    kcache = torch.relu(0.32 * torch.randn(Bd, nhd, cap, Nd, generator=g, device=dev)).to(torch.bfloat16)
+    vcache = torch.randn(Bd, 1, cap, Dd, generator=g, device=dev).to(torch.bfloat16)
+    q = torch.relu(0.32 * torch.randn(Bd, nhd, 1, Nd, generator=g, device=dev)).to(torch.bfloat16)
+    dec = {}
+    for S in C3["S"]:
+        kp, vp = kcache.narrow(2, 0, S), vcache.narrow(2, 0, S)
+        ms_d = time_steps(lambda: kernels.bdh_attn_decode(q, kp, vp, impl="hip"), steps * 4, warmup)
+        by = 2 * (Bd * nhd * S * Nd + Bd * S * Dd + Bd * nhd * Nd + Bd * nhd * Dd)
+        dec[str(S)] = {"us": ms_d * 1e3, "gbs": by / ms_d / 1e6, "frac_hbm": by / ms_d / 1e6 / PEAK_HBM_GBS}
+    out["c3_decode_step_per_layer"] = dec
+    log(f"[bench] decode: {json.dumps(dec)}")
+    del kcache, vcache
+
+    # Training op (C4): fwd + merged-gradient bwd, bf16.
+    B4, nh4, T4, N4, D4 = (C4[k] for k in ("B", "nh", "T", "N", "D"))
+    g4 = torch.Generator(device=dev).manual_seed(0)
+    q4 = torch.relu(0.32 * torch.randn(B4, nh4, T4, N4, generator=g4, device=dev)).to(torch.bfloat16)
+    v4 = torch.randn(B4, 1, T4, D4, generator=g4, device=dev).to(torch.bfloat16)
+    d4 = torch.randn(B4, nh4, T4, D4, generator=g4, device=dev).to(torch.bfloat16)
+
+    def train_op():
+        ext.tril_score_v(q4, q4, v4)
+        ext.tril_score_v_bwd(q4, None, v4, d4)
+
+    ms_t = time_steps(train_op, max(2, steps // 2), 1)
+    F4 = 3 * attn_flops(B4, nh4, T4, N4, D4)
+    out["c4_train_op_fwd_bwd"] = {"us": ms_t * 1e3, "tflops": F4 / ms_t / 1e9, "frac_bf16_peak": F4 / ms_t / 1e9 / PEAK_BF16_TFLOPS}
+    log(f"[bench] C4 fwd+bwd: {ms_t * 1e3:.1f} us, {F4 / ms_t / 1e9:.1f} TFLOP/s")
+    return out
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,165 @@
+/*
+ * bdh_hip.h - C ABI of the MI355X (gfx950) BDH strict-tril attention library.
+ *
+ * The op: out[b,h,i,:] = sum_{j<i} <Q[b,h,i,:], K[b,h,j,:]> * V[b,hv,j,:]
+ * (tril(Q K^T, -1) V: no softmax, no 1/sqrt(d), diagonal excluded), with BDH's
+ * RoPE (adjacent-pair rotation, phase = frac(pos * freq)) optionally fused into
+ * the operand loads.
+ *
+ * Conventions
+ *  - Every tensor is a 4-D strided view (bdh_tensor4): element strides, the
+ *    last dimension must have stride 1 (when its size is > 1).  Other strides
+ *    are honoured, so permuted views and capacity-strided cache views are
+ *    passed without copies.  V may broadcast over heads (size[1] == 1).
+ *  - dtype is BDH_F32 or BDH_BF16.  Arithmetic follows the q/k dtype: bf16
+ *    operands use bf16 MFMA with fp32 accumulation, fp32 operands use fp32
+ *    MFMA.  Outputs are cast to their own dtype on store.
+ *  - The library never allocates device memory.  Entry points that need
+ *    scratch take a caller-provided workspace whose size comes from the
+ *    matching *_workspace() query.
+ *  - Work is enqueued on `stream` (a hipStream_t); calls are asynchronous.
+ *  - Return value: BDH_OK (0) or an error code; bdh_error_string() names it.
+ *    Shape/dtype/stride errors are detected before anything is launched.
+ */
+#ifndef BDH_HIP_H_
+#define BDH_HIP_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { BDH_F32 = 0, BDH_BF16 = 1 };
+
+enum {
+  BDH_OK = 0,
+  BDH_ERR_SHAPE = 1,     /* inconsistent sizes between operands            */
+  BDH_ERR_DTYPE = 2,     /* unsupported dtype or dtype combination         */
+  BDH_ERR_STRIDE = 3,    /* last dimension not unit-stride                 */
+  BDH_ERR_WORKSPACE = 4, /* workspace missing or smaller than required     */
+  BDH_ERR_LAUNCH = 5,    /* the HIP runtime rejected a kernel launch       */
+  BDH_ERR_ARG = 6,       /* other invalid argument (NULL pointer, range)   */
+  BDH_ERR_ALIAS = 7      /* an output overlaps an input it must not alias  */
+};
+
+typedef struct bdh_tensor4 {
+  void* data;
+  int64_t size[4];
+  int64_t stride[4]; /* in elements */
+  int32_t dtype;     /* BDH_F32 | BDH_BF16 */
+  int32_t reserved;
+} bdh_tensor4;
+
+typedef void* bdh_stream; /* hipStream_t */
+
+/* Library version string and error names. */
+const char* bdh_version(void);
+const char* bdh_error_string(int code);
+
+/*
+ * Cold strict-tril score x V.
+ * Replaces tril_score_v (reference csrc/tril_attn_bind.cpp:3-12, dispatching to
+ * tril_score_v_cuda, csrc/tril_attn_cuda.cu:251-339; Python wrapper
+ * kernels/cuda_attn.py:391-414).
+ * q, k: (B,H,T,Dk) same dtype; v: (B,1|H,T,Dv); out: (B,H,T,Dv).
+ */
+size_t bdh_tril_score_v_workspace(int64_t B, int64_t H, int64_t T, int64_t Dk,
+                                  int64_t Dv, int32_t qk_dtype);
+int bdh_tril_score_v(const bdh_tensor4* q, const bdh_tensor4* k,
+                     const bdh_tensor4* v, const bdh_tensor4* out,
+                     void* workspace, size_t workspace_bytes, bdh_stream stream);
+
+/*
+ * Cold BDH attention with RoPE fused into the operand loads: Q = K = RoPE(x).
+ * Replaces the pair bdh.py:405 (self.rope(...) -> kernels/rope.py:220-240)
+ * followed by bdh.py:412 (bdh_attn(QR, QR, V), kernels/attention_dispatch.py:
+ * 263-308).  freqs: N fp32 values (bdh.py:41-49 layout, pairs share a value);
+ * positions are rope_start + t.  qr_out (optional, may be NULL): also store
+ * RoPE(x) there, in its own dtype (the KR cache slot, bdh.py:1000-1016).
+ */
+int bdh_tril_rope_score_v(const bdh_tensor4* x, const bdh_tensor4* v,
+                          const bdh_tensor4* out, const float* freqs,
+                          int64_t rope_start, const bdh_tensor4* qr_out,
+                          void* workspace, size_t workspace_bytes,
+                          bdh_stream stream);
+
+/*
+ * Decode against the packed past: out = (q K_past^T) V_past (all past keys
+ * valid; the new token never attends to itself).
+ * Replaces tril_decode (reference csrc/tril_attn_bind.cpp:14-23 ->
+ * csrc/tril_attn_cuda.cu:544-661; kernels/cuda_attn.py:490-502) and the eager
+ * decode of kernels/attention.py:193-219.
+ * q: (B,H,Tq,Dk); k_past: (B,H,S,Dk) (capacity-strided views allowed);
+ * v_past: (B,1|H,S,Dv); out: (B,H,Tq,Dv).  q and the cache may have different
+ * dtypes (e.g. fp32 compute over a bf16 cache).
+ */
+size_t bdh_tril_decode_workspace(int64_t B, int64_t H, int64_t Tq, int64_t S,
+                                 int64_t Dk, int64_t Dv);
+int bdh_tril_decode(const bdh_tensor4* q, const bdh_tensor4* k_past,
+                    const bdh_tensor4* v_past, const bdh_tensor4* out,
+                    void* workspace, size_t workspace_bytes, bdh_stream stream);
+
+/*
+ * RoPE apply: out = rotate(v, cos, sin) over adjacent pairs.
+ * Replaces eager_rope_rotate / rope_rotate_t1 / rope_rotate_paired
+ * (reference kernels/rope.py:174-240) behind bdh_rope_rotate and
+ * bdh_rope_rotate_paired (kernels/rope_dispatch.py:64-99).
+ * cos, sin: views broadcastable to v (stride 0 on broadcast dims), last dim N.
+ * Same rounding as the reference: fp32 v -> fp32 products and add; bf16 v ->
+ * each product rounded to bf16, then a bf16 add.  out may have another dtype.
+ * backward != 0 applies the transpose rotation (kernels/rope.py:543-556).
+ */
+int bdh_rope_rotate(const bdh_tensor4* v, const bdh_tensor4* cos,
+                    const bdh_tensor4* sin, const bdh_tensor4* out,
+                    int32_t backward, bdh_stream stream);
+
+/*
+ * Analytic backward of out = tril(q k^T, -1) v.
+ * Replaces analytic_tril_attn_backward[_blocked] (reference
+ * kernels/attention_bwd.py:45-181) as used by StrictTrilAttnFn and
+ * StrictTrilSelfAttnFn (:218-291).
+ * k == NULL means self attention (k is q): dq receives dq + dk (the merged
+ * gradient of attention_bwd.py:284-291) and dk must be NULL.
+ * dv has v's shape; with broadcast v the head gradients are summed.
+ */
+size_t bdh_tril_score_v_bwd_workspace(int64_t B, int64_t H, int64_t Hv,
+                                      int64_t T, int64_t Dk, int64_t Dv,
+                                      int32_t qk_dtype);
+int bdh_tril_score_v_bwd(const bdh_tensor4* q, const bdh_tensor4* k,
+                         const bdh_tensor4* v, const bdh_tensor4* dout,
+                         const bdh_tensor4* dq, const bdh_tensor4* dk,
+                         const bdh_tensor4* dv, void* workspace,
+                         size_t workspace_bytes, bdh_stream stream);
+
+/*
+ * Backward of bdh_tril_rope_score_v: dx = RoPE^-1((dS + dS^T) RoPE(x)) and
+ * dv = sum_h M_h^T dout_h, M = tril(RoPE(x) RoPE(x)^T, -1).
+ * Replaces the autograd chain of bdh.py:405-412 under BDH_ATTN_AUTOGRAD
+ * (StrictTrilSelfAttnFn, kernels/attention_bwd.py:259-291, then the RoPE
+ * backward of kernels/rope.py:543-556).
+ */
+size_t bdh_tril_rope_score_v_bwd_workspace(int64_t B, int64_t H, int64_t Hv,
+                                           int64_t T, int64_t N, int64_t Dv,
+                                           int32_t x_dtype);
+int bdh_tril_rope_score_v_bwd(const bdh_tensor4* x, const bdh_tensor4* v,
+                              const bdh_tensor4* dout, const float* freqs,
+                              int64_t rope_start, const bdh_tensor4* dx,
+                              const bdh_tensor4* dv, void* workspace,
+                              size_t workspace_bytes, bdh_stream stream);
+
+/*
+ * Per-kernel timing (measurement support; no counterpart in the reference).
+ * While enabled, every kernel the library launches is bracketed by HIP events
+ * on its stream.  bdh_profile_collect() waits for the recorded events and
+ * returns up to `max` (name, milliseconds) records, then clears the log.
+ */
+void bdh_profile_enable(int32_t on);
+int bdh_profile_collect(char* names, int32_t name_len, float* ms, int32_t max);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* BDH_HIP_H_ */
