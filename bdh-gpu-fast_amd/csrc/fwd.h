@@ -41,6 +41,15 @@ struct ScoreVArgs {
   View o;
 };
 
+// bf16 fast path of the cold op (syrk.hip).  sy_cold returns kNotEligible
+// when the operands fall outside its constraints (the caller then uses the
+// generic kernels), otherwise a BDH_* code.
+constexpr int kNotEligible = -1;
+size_t sy_workspace(int64_t B, int64_t H, int64_t T, int64_t N, bool rope);
+int sy_cold(const bdh_tensor4* q, const bdh_tensor4* k, const bdh_tensor4* v, const bdh_tensor4* out,
+            const float* freqs, int64_t rope_start, const bdh_tensor4* qr, void* ws, size_t ws_bytes,
+            hipStream_t s);
+
 FwdPlan plan_fwd(int64_t B, int64_t H, int64_t T, int64_t K, bool bf);
 int run_scores(const ScoresArgs& a, const FwdPlan& p, int64_t BH, bool bf, bool rope, bool trans,
                hipStream_t s);

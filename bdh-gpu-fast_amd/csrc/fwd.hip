@@ -232,6 +232,10 @@ static int run_cold(const bdh_tensor4* q, const bdh_tensor4* k, const bdh_tensor
   const int64_t Dv = v->size[3];
   if (numel4(out) == 0 && (qr == nullptr || numel4(qr) == 0)) return BDH_OK;
   const bool bf = q->dtype == BDH_BF16;
+  if (bf && T > 0) {
+    const int rc = sy_cold(q, k, v, out, freqs, rope_start, qr, ws, ws_bytes, s);
+    if (rc != kNotEligible) return rc;
+  }
   const FwdPlan p = plan_fwd(B, H, T, K, bf);
   if (ws == nullptr || ws_bytes < p.ws_bytes) return BDH_ERR_WORKSPACE;
   if (T == 0) return BDH_OK;
@@ -286,7 +290,10 @@ using namespace bdh;
 extern "C" size_t bdh_tril_score_v_workspace(int64_t B, int64_t H, int64_t T, int64_t Dk,
                                              int64_t Dv, int32_t qk_dtype) {
   (void)Dv;
-  return plan_fwd(B, H, T, Dk, qk_dtype == BDH_BF16).ws_bytes;
+  const size_t generic = plan_fwd(B, H, T, Dk, qk_dtype == BDH_BF16).ws_bytes;
+  // bf16 operands may take the fast path (with a RoPE table when fused).
+  const size_t fast = qk_dtype == BDH_BF16 ? sy_workspace(B, H, T, Dk, true) : 0;
+  return generic > fast ? generic : fast;
 }
 
 extern "C" int bdh_tril_score_v(const bdh_tensor4* q, const bdh_tensor4* k, const bdh_tensor4* v,

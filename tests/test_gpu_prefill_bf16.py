@@ -1,0 +1,122 @@
+"""GPU parity of the bf16 prefill path (256x256 split-K score tiles, LDS-DMA
+stream, RoPE from a per-call table) against the CPU oracle.
+
+These shapes all qualify for that path (bf16, N a multiple of 64, 16-byte
+aligned rows): ragged and exact multiples of the 256-row tile, one to five
+row tiles, slab counts that are and are not multiples of 8 (the XCD grouping),
+split-K from 1 to 8, q != k, permuted views, fused RoPE with a start offset and
+the RoPE(x) copy.  Tolerance: bf16 2e-2 relative Frobenius; row 0 exactly 0.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from helpers import TOL, latent, normal, np_of, rel_fro, to_dev
+
+pytestmark = pytest.mark.gpu
+
+if not torch.cuda.is_available():
+    pytest.skip("needs a ROCm GPU", allow_module_level=True)
+
+import bdh_hip_ext as ext  # noqa: E402
+
+DEV = "cuda"
+BF = torch.bfloat16
+
+
+def _bf(a):
+    return O.bf16_round(a)
+
+
+SHAPES = [
+    # B, H, T, N, D, Hv
+    (1, 1, 1, 64, 16, 1),  # one row, one split
+    (1, 1, 256, 128, 64, 1),  # exactly one tile, split 2 (N=128)
+    (1, 1, 300, 512, 64, 1),  # ragged second tile, high split factor
+    (3, 1, 257, 256, 32, 1),  # slab count 3 (not a multiple of 8)
+    (2, 4, 512, 1024, 256, 1),  # C1-like layout, split 8
+    (1, 2, 1100, 192, 40, 2),  # five row tiles, per-head V
+]
+
+
+@pytest.mark.parametrize("shape", SHAPES)
+def test_bf16_self_attention_matches_oracle(shape):
+    B, H, T, N, D, Hv = shape
+    q = _bf(latent((B, H, T, N), 0))
+    v = _bf(normal((B, Hv, T, D), 1))
+    got = np_of(ext.tril_score_v(to_dev(q, BF), to_dev(q, BF), to_dev(v, BF)))
+    want = O.tril_score_v_cpu(q, q, v)
+    print(f"self {shape}: rel {rel_fro(got, want):.3e}", flush=True)
+    assert rel_fro(got, want) <= TOL[BF]
+    assert not got[:, :, 0].any()
+
+
+@pytest.mark.parametrize("shape", SHAPES[1:4])
+def test_bf16_distinct_q_k_matches_oracle(shape):
+    B, H, T, N, D, Hv = shape
+    q = _bf(latent((B, H, T, N), 0))
+    k = _bf(latent((B, H, T, N), 5))
+    v = _bf(normal((B, Hv, T, D), 1))
+    got = np_of(ext.tril_score_v(to_dev(q, BF), to_dev(k, BF), to_dev(v, BF)))
+    want = O.tril_score_v_cpu(q, k, v)
+    assert rel_fro(got, want) <= TOL[BF]
+    assert not got[:, :, 0].any()
+
+
+def test_bf16_permuted_latent_view_and_fp32_v():
+    """x_sparse as bdh.py makes it: a (B,T,nh,N) buffer viewed as (B,nh,T,N)."""
+    B, T, H, N, D = 2, 333, 3, 128, 48
+    x_bthn = _bf(latent((B, T, H, N), 3))
+    xt = to_dev(x_bthn, BF).permute(0, 2, 1, 3)
+    v = normal((B, 1, T, D), 4)
+    got = np_of(ext.tril_score_v(xt, xt, to_dev(v, torch.float32)))
+    xq = np.ascontiguousarray(x_bthn.transpose(0, 2, 1, 3))
+    want = O.tril_score_v_cpu(xq, xq, _bf(v))
+    assert rel_fro(got, want) <= TOL[BF]
+
+
+@pytest.mark.parametrize("shape,start", [((1, 2, 300, 256, 64), 0), ((2, 1, 520, 512, 32), 17), ((1, 1, 1, 64, 8), 3)])
+def test_bf16_fused_rope_matches_oracle(shape, start):
+    B, H, T, N, D = shape
+    x = _bf(latent((B, H, T, N), 0))
+    v = _bf(normal((B, 1, T, D), 1))
+    freqs = O.get_freqs(N)
+    want, qr_want = O.tril_rope_score_v(x, v, freqs, start, bf16=True)
+    qr = torch.full((B, H, T, N), float("nan"), dtype=BF, device=DEV)
+    got = np_of(ext.tril_rope_score_v(to_dev(x, BF), to_dev(v, BF), torch.from_numpy(freqs).to(DEV), start,
+                                      qr_out=qr))
+    print(f"rope {shape} start {start}: rel {rel_fro(got, want):.3e} qr {rel_fro(np_of(qr), qr_want):.3e}",
+          flush=True)
+    assert rel_fro(got, want) <= TOL[BF]
+    assert not got[:, :, 0].any()
+    assert np.isfinite(np_of(qr)).all()  # every element of RoPE(x) was written
+    assert rel_fro(np_of(qr), qr_want) <= 8e-3
+
+
+def test_bf16_fused_rope_full_c1_properties():
+    """C1 at full size (B=8 nh=4 T=512 N=8192 D=256): size-independent checks.
+
+    Exact homogeneity (both scalings are exact in bf16 and fp32, so the bits
+    must match): out(x, 2v) = 2 out(x, v) and out(2x, v) = 4 out(x, v); row 0
+    exactly zero; and batch element 0 against the oracle.
+    """
+    B, H, T, N, D = 8, 4, 512, 8192, 256
+    g = torch.Generator(device=DEV).manual_seed(0)
+    x = torch.relu(0.32 * torch.randn(B, H, T, N, generator=g, device=DEV)).to(BF)
+    v = torch.randn(B, 1, T, D, generator=g, device=DEV).to(BF)
+    f = torch.from_numpy(O.get_freqs(N)).to(DEV)
+
+    def run(xx, vv):
+        o = torch.empty(B, H, T, D, dtype=torch.float32, device=DEV)
+        return ext.tril_rope_score_v(xx, vv, f, 0, out=o)
+
+    o1 = run(x, v)
+    assert torch.equal(run(x, v * 2), o1 * 2)
+    assert torch.equal(run(x * 2, v), o1 * 4)
+    assert not o1[:, :, 0].any().item()
+    want, _ = O.tril_rope_score_v(np_of(x[:1]), np_of(v[:1]), O.get_freqs(N), 0, bf16=True)
+    assert rel_fro(np_of(o1[:1]), want) <= TOL[BF]
