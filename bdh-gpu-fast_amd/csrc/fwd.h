@@ -45,7 +45,7 @@ struct ScoreVArgs {
 // when the operands fall outside its constraints (the caller then uses the
 // generic kernels), otherwise a BDH_* code.
 constexpr int kNotEligible = -1;
-size_t sy_workspace(int64_t B, int64_t H, int64_t T, int64_t N, bool rope);
+size_t sy_workspace(int64_t B, int64_t H, int64_t T, int64_t N, int64_t Dv, bool rope);
 int sy_cold(const bdh_tensor4* q, const bdh_tensor4* k, const bdh_tensor4* v, const bdh_tensor4* out,
             const float* freqs, int64_t rope_start, const bdh_tensor4* qr, void* ws, size_t ws_bytes,
             hipStream_t s);

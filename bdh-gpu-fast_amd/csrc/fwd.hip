@@ -289,10 +289,9 @@ using namespace bdh;
 
 extern "C" size_t bdh_tril_score_v_workspace(int64_t B, int64_t H, int64_t T, int64_t Dk,
                                              int64_t Dv, int32_t qk_dtype) {
-  (void)Dv;
   const size_t generic = plan_fwd(B, H, T, Dk, qk_dtype == BDH_BF16).ws_bytes;
   // bf16 operands may take the fast path (with a RoPE table when fused).
-  const size_t fast = qk_dtype == BDH_BF16 ? sy_workspace(B, H, T, Dk, true) : 0;
+  const size_t fast = qk_dtype == BDH_BF16 ? sy_workspace(B, H, T, Dk, Dv, true) : 0;
   return generic > fast ? generic : fast;
 }
 

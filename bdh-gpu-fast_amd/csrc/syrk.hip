@@ -14,20 +14,23 @@
 //       so the splits and tiles of a slab walk k in step and the row blocks
 //       re-read by neighbouring tiles are served by the XCD's L2.  Every item
 //       of a slab runs on one XCD (workgroup id % 8 selects the XCD).
-//     * x streams HBM -> LDS through global_load_lds_dwordx4 into a 4-slot
-//       ring of 32-wide k stages (issued three stages ahead).  The 16-byte
-//       chunk c of row r sits at position c ^ ((r >> 2) & 3) of its 64-byte LDS
-//       row, which makes the MFMA fragment reads bank-conflict free.
-//     * RoPE is applied in place: the table entries of stage s+1 are DMA'd
-//       into a fifth slot while stage s runs its MFMAs; then each lane rotates
-//       the chunks it loaded itself (per pair two v_dot2_f32_bf16, products
-//       exact in fp32, one v_cvt_pk_bf16_f32 and one v_alignbit_b32).  No vector-memory load of
-//       the main loop returns to registers, so the only waits on it are the
-//       explicit ones below.
+//     * x streams HBM -> LDS through global_load_lds_dwordx4 into a ring of
+//       32-wide k stages (5 slots, issued four stages ahead; with RoPE 3 slots
+//       plus a 2-slot ring for the table entries of the same stages at the
+//       same offsets, issued two stages ahead).  The 16-byte chunk c of row r sits at position c ^ ((r >> 2) & 3)
+//       of its 64-byte LDS row, which makes the MFMA fragment reads
+//       bank-conflict free.
+//     * RoPE is applied in place at the end of the stage before its MFMAs:
+//       each lane rotates the chunks it loaded itself (per pair two
+//       v_dot2_f32_bf16, products exact in fp32, one v_cvt_pk_bf16_f32 and one
+//       v_alignbit_b32).  No vector-memory load of the main loop returns to
+//       registers, so the only waits on it are the explicit ones below.
 //     * v_mfma_f32_32x32x16_bf16 with fp32 accumulators; the epilogue stores
-//       fp32 partial tiles [slab][item][256][256].
-//  3. k_sy_score_v: out = tril(sum over splits of S, -1) V with the 128x128
-//     MFMA tile engine (scores rounded to bf16 as MFMA operands).
+//       the partial tiles [slab][item][256][256] as bf16.
+//  3. k_sy_vt + k_sy_sv: out = tril(sum over splits of S, -1) V.  V is
+//     transposed once (bf16, contiguous along the contraction); each wave then
+//     loads its MFMA fragments straight from global memory: the split sum of
+//     the partial score rows (formed in fp32, masked, rounded to bf16) and V^T.
 #include <algorithm>
 #include <type_traits>
 
@@ -42,7 +45,7 @@ constexpr int kSyThreads = 512;
 constexpr int kSyTile = 256;
 constexpr int kSyBlk = kSyTile * 64;   // bytes of one row block per stage (256 rows x 32 bf16)
 constexpr int kSySlot = 2 * kSyBlk;    // A and B row blocks
-constexpr int kSySlots = 4;       // x ring; one more slot holds the RoPE table
+constexpr int kSyLdsSlots = 5;    // 160 KB: x ring of 5 (plain) or 3 x + 2 RoPE table (fused)
 constexpr int kSyMaxItems = 256;
 constexpr int kSyMaxTiles = 128;
 constexpr int kSyTileElems = kSyTile * kSyTile;
@@ -55,19 +58,28 @@ struct SyArgs {
   int64_t q0, q1, q2;  // element strides of q over (b, h, t)
   int64_t k0, k1, k2;
   int H, T, N, nslab, ips, nchunk;
-  const uint32_t* cs;  // RoPE table [T][N/2] or null
-  float* part;         // [nslab][ips][256*256]
+  const uint32_t* cs;  // RoPE table [T][tpitch] (first N/2 used) or null
+  int tpitch;          // table row pitch in dwords
+  bf16_t* part;        // [nslab][ips][256*256] partial score tiles (bf16)
   bf16_t* qr;          // optional RoPE(x) copy
   int64_t r0, r1, r2;
   uint32_t items[kSyMaxItems];  // ti | tj << 8 | split << 16 | nsplit << 24
 };
 
-__shared__ __attribute__((aligned(1024))) uint8_t sy_lds[(kSySlots + 1) * kSySlot];  // 160 KB
+__shared__ __attribute__((aligned(1024))) uint8_t sy_lds[kSyLdsSlots * kSySlot];  // 160 KB
 
 // ---------------------------------------------------------------- asm helpers
 // The x stream and the table are moved by LDS DMA issued from inline asm, so
 // the compiler neither counts them in its own vmcnt waits nor orders LDS
 // accesses behind them; the kernel waits for them explicitly (sy_wait).
+// A wave-uniform pointer made explicitly scalar (the asm takes it in SGPRs).
+__device__ __forceinline__ const void* sgpr_ptr(const void* p) {
+  const uint64_t v = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(uint32_t(v));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(uint32_t(v >> 32));
+  return reinterpret_cast<const void*>((uint64_t(hi) << 32) | lo);
+}
+
 __device__ __forceinline__ void dma16(uint32_t lds, const void* gbase, uint32_t voff) {
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
                :
@@ -83,7 +95,10 @@ __device__ __forceinline__ void sy_wait(int n) {
     case 2: asm volatile("s_waitcnt vmcnt(2)" ::: "memory"); break;
     case 4: asm volatile("s_waitcnt vmcnt(4)" ::: "memory"); break;
     case 6: asm volatile("s_waitcnt vmcnt(6)" ::: "memory"); break;
-    default: asm volatile("s_waitcnt vmcnt(8)" ::: "memory"); break;
+    case 8: asm volatile("s_waitcnt vmcnt(8)" ::: "memory"); break;
+    case 10: asm volatile("s_waitcnt vmcnt(10)" ::: "memory"); break;
+    case 12: asm volatile("s_waitcnt vmcnt(12)" ::: "memory"); break;
+    default: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
   }
 }
 
@@ -137,16 +152,15 @@ __device__ __forceinline__ f32x16 mma(bf16x8 a, bf16x8 b, f32x16 c) {
 
 // ------------------------------------------------------------------ kernels
 __global__ __launch_bounds__(256) void k_rope_table(const float* __restrict__ freqs, int64_t rope_start,
-                                                    int T, int N2, uint32_t* __restrict__ cs) {
-  const int64_t idx = int64_t(blockIdx.x) * 256 + threadIdx.x;
-  if (idx >= int64_t(T) * N2) return;
-  const int t = int(idx / N2), m = int(idx % N2);
-  // phase = fp32(pos) * freq; theta = fp32(phase - floor(phase)) * fp32(2 pi)
+                                                    int N2, int pitch, uint32_t* __restrict__ cs) {
+  const int t = blockIdx.y, m = blockIdx.x * 256 + threadIdx.x;
+  if (m >= N2) return;
+  // phase = fp32(pos) * freq, then cos/sin of 2 pi frac(phase); v_cos/v_sin
+  // take the angle in revolutions, so frac(phase) goes in directly.  The
+  // values are rounded to bf16, far above the hardware functions' error.
   const float ph = __fmul_rn(float(rope_start + t), freqs[2 * m]);
-  const float th = __fmul_rn(ph - floorf(ph), 6.28318530717958647692f);
-  float s, c;
-  sincosf(th, &s, &c);
-  cs[idx] = pack_bf2(c, s);
+  const float fr = ph - floorf(ph);
+  cs[int64_t(t) * pitch + m] = pack_bf2(__builtin_amdgcn_cosf(fr), __builtin_amdgcn_sinf(fr));
 }
 
 template <bool ROPE, bool SELF>
@@ -167,8 +181,9 @@ __global__ __launch_bounds__(kSyThreads, 1) void k_sy_scores(const SyArgs a) {
   const int nch = (a.nchunk - split + nsplit - 1) / nsplit;
   const int nst = 2 * nch;
 
-  const bf16_t* baseA = a.q + b * a.q0 + h * a.q1;
-  const bf16_t* baseB = SELF ? baseA : a.k + b * a.k0 + h * a.k1;
+  const void* baseA = sgpr_ptr(a.q + b * a.q0 + h * a.q1);
+  const void* baseB = SELF ? baseA : sgpr_ptr(a.k + b * a.k0 + h * a.k1);
+  const void* tbase = sgpr_ptr(a.cs);
   const uint32_t lds0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_u8*)sy_lds);
 
   // Per DMA instruction u: the 16-byte chunk this lane moves (and rotates).
@@ -186,7 +201,7 @@ __global__ __launch_bounds__(kSyThreads, 1) void k_sy_scores(const SyArgs a) {
     rowg[u] = rg;
     kch[u] = 8 * c;
     xoff[u] = uint32_t((int64_t(rc) * (blk == 0 ? a.q2 : (SELF ? a.q2 : a.k2)) + 8 * c) * 2);
-    toff[u] = uint32_t((int64_t(rc) * a.N + 8 * c) * 2);
+    toff[u] = uint32_t(int64_t(rc) * a.tpitch * 4 + 16 * c);
   }
   // MFMA fragment offsets within a row block for the two k16 steps of a stage.
   uint32_t loff[2];
@@ -197,23 +212,10 @@ __global__ __launch_bounds__(kSyThreads, 1) void k_sy_scores(const SyArgs a) {
   }
 
   auto kofs = [&](int s) { return (split + nsplit * (s >> 1)) * 64 + (s & 1) * 32; };
-  auto slot = [&](int s) { return sy_lds + (s & 3) * kSySlot; };
-  uint8_t* const tslot = sy_lds + kSySlots * kSySlot;
-  auto dma_x = [&](int s) {
-    const uint32_t kb = uint32_t(kofs(s) * 2);
-    const uint32_t sb = lds0 + uint32_t((s & 3) * kSySlot);
-#pragma unroll
-    for (int u = 0; u < 4; ++u)
-      if (u < ndma) dma16(sb + uint32_t((u * 8 + w) * 1024), u < 2 ? baseA : baseB, xoff[u] + kb);
-  };
-  // table entries of the chunks this lane moves, at the same offsets in the table slot
-  auto dma_t = [&](int s) {
-    const uint32_t kb = uint32_t(kofs(s) * 2);
-    const uint32_t sb = lds0 + uint32_t(kSySlots * kSySlot);
-#pragma unroll
-    for (int u = 0; u < 4; ++u)
-      if (u < ndma) dma16(sb + uint32_t((u * 8 + w) * 1024), a.cs, toff[u] + kb);
-  };
+  // x ring depth; issuing runs NX - 1 stages ahead of the MFMAs
+  constexpr int NX = ROPE ? 3 : 5;
+  auto slot = [&](int s) { return sy_lds + (s % NX) * kSySlot; };
+  auto tslot = [&](int s) { return sy_lds + (NX + (s & 1)) * kSySlot; };
   auto rotate = [&](int s) {
     uint8_t* sl = slot(s);
     const int k0 = kofs(s);
@@ -223,7 +225,7 @@ __global__ __launch_bounds__(kSyThreads, 1) void k_sy_scores(const SyArgs a) {
         const int off = (u * 8 + w) * 1024 + lane * 16;
         u32x4* p = reinterpret_cast<u32x4*>(sl + off);
         const u32x4 x = *p;
-        const u32x4 t = *reinterpret_cast<const u32x4*>(tslot + off);
+        const u32x4 t = *reinterpret_cast<const u32x4*>(tslot(s) + off);
         const u32x4 y = rot_chunk(x, t);
         *p = y;
         if (a.qr != nullptr && diag && rowg[u] < a.T)
@@ -256,80 +258,129 @@ __global__ __launch_bounds__(kSyThreads, 1) void k_sy_scores(const SyArgs a) {
   // The wave tile type selects one of four instantiations of the whole
   // pipeline (prologue, loop, epilogue), so each loop holds straight-line MFMA
   // code; all of them run the same stages and barriers.
-  auto run = [&](auto wt_tag) {
+  auto run = [&](auto wt_tag, auto diag_tag) {
     constexpr int WT = decltype(wt_tag)::value;
-    auto mma_stage = [&](int s) {
+    constexpr bool DG = decltype(diag_tag)::value;  // == diag
+    constexpr int NDMA = DG ? 2 : 4;
+    // vector-memory operations per stage per wave, in issue order: the table
+    // chunks (RoPE) then the x chunks
+    constexpr int per_stage = ROPE ? 2 * NDMA : NDMA;
+    auto dma_op = [&](int st, int i) {
+      const uint32_t kb = uint32_t(kofs(st) * 2);
+      if (ROPE && i < NDMA) {
+        dma16(lds0 + uint32_t((NX + (st & 1)) * kSySlot + (i * 8 + w) * 1024), tbase, toff[i] + kb);
+      } else {
+        const int u = ROPE ? i - NDMA : i;
+        dma16(lds0 + uint32_t((st % NX) * kSySlot + (u * 8 + w) * 1024), u < 2 ? baseA : baseB, xoff[u] + kb);
+      }
+    };
+    // The MFMAs of stage s with the loads of stage `ahead` (if any) spread
+    // between them: issuing them all at once stalls the wave on the load
+    // queue while its MFMAs wait.  All fragments of the stage are read first
+    // into distinct registers (sched_group_barrier fixes that order; left
+    // alone the scheduler reuses a few registers and waits on each read right
+    // before its MFMA).
+    auto mma_stage = [&](int s, int ahead) {
       const uint8_t* A = slot(s);
-      const uint8_t* B = diag ? A : A + kSyBlk;
+      const uint8_t* B = DG ? A : A + kSyBlk;
+      const bool issue = ahead < nst;
+      // after MFMA number m of nm, issue the loads [m*P/nm, (m+1)*P/nm)
+      auto loads_after = [&](int m, int nm) {
+        if (!issue) return;
 #pragma unroll
-      for (int k2 = 0; k2 < 2; ++k2) {
-        const uint32_t lo = loff[k2];
-        if constexpr (WT == 0 || WT == 1) {
-          bf16x8 fa[4], fb[2];
+        for (int i = (m * per_stage) / nm; i < ((m + 1) * per_stage) / nm; ++i) dma_op(ahead, i);
+      };
+      if constexpr (WT == 0 || WT == 1) {
+        bf16x8 fa[2][4], fb[2][2];
 #pragma unroll
-          for (int i = 0; i < 4; ++i) fa[i] = frag(A, 4 * wm + i, lo);
+        for (int k2 = 0; k2 < 2; ++k2) {
 #pragma unroll
-          for (int j = 0; j < 2; ++j) fb[j] = frag(B, 2 * wn + j, lo);
+          for (int i = 0; i < 4; ++i) fa[k2][i] = frag(A, 4 * wm + i, loff[k2]);
+#pragma unroll
+          for (int j = 0; j < 2; ++j) fb[k2][j] = frag(B, 2 * wn + j, loff[k2]);
+        }
+        constexpr int NM = WT == 0 ? 16 : 14;
+        int m = 0;
+#pragma unroll
+        for (int k2 = 0; k2 < 2; ++k2)
 #pragma unroll
           for (int i = 0; i < 4; ++i)
 #pragma unroll
             for (int j = 0; j < 2; ++j)
-              if (WT == 0 || i >= j) acc[2 * i + j] = mma(fa[i], fb[j], acc[2 * i + j]);
-        } else if constexpr (WT == 2) {
-          bf16x8 fa[2], fb[2];
+              if (WT == 0 || i >= j) {
+                acc[2 * i + j] = mma(fa[k2][i], fb[k2][j], acc[2 * i + j]);
+                if (m == 0) {
+                  __builtin_amdgcn_sched_group_barrier(0x100, 12, 0);
+                  __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                }
+                loads_after(m, NM);
+                ++m;
+              }
+      } else if constexpr (WT == 2) {
+        bf16x8 fa[2][2], fb[2][2];
 #pragma unroll
-          for (int i = 0; i < 2; ++i) fa[i] = frag(A, 4 * wm + 2 + i, lo);
+        for (int k2 = 0; k2 < 2; ++k2) {
 #pragma unroll
-          for (int j = 0; j < 2; ++j) fb[j] = frag(B, 2 * wn + j, lo);
-          acc[4] = mma(fa[0], fb[0], acc[4]);
-          acc[6] = mma(fa[1], fb[0], acc[6]);
-          acc[7] = mma(fa[1], fb[1], acc[7]);
+          for (int i = 0; i < 2; ++i) fa[k2][i] = frag(A, 4 * wm + 2 + i, loff[k2]);
+#pragma unroll
+          for (int j = 0; j < 2; ++j) fb[k2][j] = frag(B, 2 * wn + j, loff[k2]);
         }
+#pragma unroll
+        for (int k2 = 0; k2 < 2; ++k2) {
+          acc[4] = mma(fa[k2][0], fb[k2][0], acc[4]);
+          if (k2 == 0) {
+            __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          }
+          loads_after(3 * k2, 6);
+          acc[6] = mma(fa[k2][1], fb[k2][0], acc[6]);
+          loads_after(3 * k2 + 1, 6);
+          acc[7] = mma(fa[k2][1], fb[k2][1], acc[7]);
+          loads_after(3 * k2 + 2, 6);
+        }
+      } else {
+        loads_after(0, 1);
       }
     };
     constexpr auto live = [](int i, int j) { return WT == 0 || (WT == 1 && i >= j) || (WT == 2 && i >= j + 2); };
     // ------------------------------------------------------------ prologue
     // Issue order is what the waits count on: operations complete in order.
-    if (ROPE) dma_t(0);
-    dma_x(0);
-    if (nst > 1) dma_x(1);
-    if (nst > 2) dma_x(2);
-    if (ROPE) {
-      sy_wait((nst > 1 ? ndma : 0) + (nst > 2 ? ndma : 0));  // table and x of stage 0
-      rotate(0);
-    } else {
-      sy_wait((nst > 1 ? ndma : 0) + (nst > 2 ? ndma : 0));  // x of stage 0
-    }
+    const int lead = NX - 1;
+    for (int st = 0; st < lead && st < nst; ++st)
+      for (int i = 0; i < per_stage; ++i) dma_op(st, i);
+    sy_wait((min(nst, lead) - 1) * per_stage);  // stage 0 landed
+    if (ROPE) rotate(0);
     sy_barrier();
 
     // ------------------------------------------------------------ main loop
     for (int s = 0; s < nst; ++s) {
-      // slot (s+3)&3 held stage s-1, whose MFMAs ended before the last barrier;
-      // the table slot held stage s, rotated before it.
-      if (ROPE && s + 1 < nst) dma_t(s + 1);
-      if (s + 3 < nst) dma_x(s + 3);
-      mma_stage(s);
+      // the loads of stage s + lead go to x slot (s-1) % NX and (fused) table
+      // slot s % 2, consumed before the last barrier
+      mma_stage(s, s + lead);
       if (s + 1 < nst) {
-        // ROPE: the table of stage s+1 (and everything issued before it, so the
-        // x of stages <= s+2); plain: the x of stage s+1 of every wave.
-        if (ROPE) {
-          sy_wait(s + 3 < nst ? ndma : 0);
-          rotate(s + 1);
-        } else {
-          sy_wait((s + 2 < nst ? ndma : 0) + (s + 3 < nst ? ndma : 0));
-        }
+        // stage s+1 landed (this wave's part): the stages issued after it may
+        // still be in flight
+        sy_wait((min(nst - 1, s + lead) - (s + 1)) * per_stage);
+        if (ROPE) rotate(s + 1);
       }
       sy_barrier();
     }
 
     // ------------------------------------------------------------ epilogue
-    float* dst = a.part + (int64_t(slab) * a.ips + itx) * kSyTileElems;
+    bf16_t* dst = a.part + (int64_t(slab) * a.ips + itx) * kSyTileElems;
+    // Partial tiles are stored as bf16 (halving their traffic; the scores are
+    // bf16 MFMA operands of the score x V product anyway).  Lane pairs swap one
+    // value so each lane writes two adjacent columns of one row.
+    const bool even = (lane & 1) == 0;
     auto store_block = [&](const f32x16& c, int rb, int cb) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int row = rb * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-        const int col = cb * 32 + (lane & 31);
-        dst[row * kSyTile + col] = c[r];
+      for (int r = 0; r < 16; r += 2) {
+        const float send = even ? c[r + 1] : c[r];
+        const float recv = __shfl_xor(send, 1, 64);
+        const int row = rb * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3) + (even ? 0 : 1);
+        const int col = cb * 32 + ((lane & 31) & ~1);
+        const uint32_t w2 = even ? pack_bf2(c[r], recv) : pack_bf2(recv, c[r + 1]);
+        *reinterpret_cast<uint32_t*>(dst + row * kSyTile + col) = w2;
       }
     };
 #pragma unroll
@@ -338,131 +389,169 @@ __global__ __launch_bounds__(kSyThreads, 1) void k_sy_scores(const SyArgs a) {
       for (int j = 0; j < 2; ++j)
         if (live(i, j)) store_block(acc[2 * i + j], 4 * wm + i, 2 * wn + j);
   };
-  switch (wtype) {
-    case 0: run(std::integral_constant<int, 0>()); break;
-    case 1: run(std::integral_constant<int, 1>()); break;
-    case 2: run(std::integral_constant<int, 2>()); break;
-    default: run(std::integral_constant<int, 3>()); break;
+  using T0 = std::integral_constant<int, 0>;
+  using F = std::integral_constant<bool, false>;
+  using D = std::integral_constant<bool, SELF>;  // diagonal tiles exist only with Q = K
+  if (!diag) {
+    run(T0(), F());
+  } else {
+    switch (wtype) {
+      case 0: run(T0(), D()); break;
+      case 1: run(std::integral_constant<int, 1>(), D()); break;
+      case 2: run(std::integral_constant<int, 2>(), D()); break;
+      default: run(std::integral_constant<int, 3>(), D()); break;
+    }
   }
 }
 
-// ---------------------------------------------------------------- score x V
-struct SyVArgs {
-  const float* part;
-  int ips;
-  View v;
-  int64_t H, Hv, T, Dv;
-  bool vec4_v;
+// ------------------------------------------------------ score x V (direct)
+// V^T, bf16: vt[bv][d][t] = v[b][hv][t][d] (bv = b * Hv + hv), t padded to tp
+// with zeros.  The score x V product contracts over t, and MFMA operands are
+// contiguous along the contraction, so V is transposed once per call.
+template <typename TV>
+__global__ __launch_bounds__(256) void k_sy_vt(View v, int Hv, int T, int D, int tp, bf16_t* __restrict__ vt) {
+  __shared__ float tile[32][33];
+  const int bv = blockIdx.z, b = bv / Hv, hv = bv - b * Hv;
+  const int t0 = blockIdx.x * 32, d0 = blockIdx.y * 32;
+  const TV* src = static_cast<const TV*>(v.p) + b * v.s0 + hv * v.s1;
+  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;  // 32 x 8
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int t = t0 + ty + 8 * r, d = d0 + tx;
+    tile[ty + 8 * r][tx] = (t < T && d < D) ? to_f(src[int64_t(t) * v.s2 + d]) : 0.f;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int d = d0 + ty + 8 * r, t = t0 + tx;
+    if (d < D && t < tp) vt[(int64_t(bv) * D + d) * tp + t] = f2bf(tile[tx][ty + 8 * r]);
+  }
+}
+
+struct SvArgs {
+  const bf16_t* part;  // partial score tiles [slab][ips][256*256]
+  const bf16_t* vt;    // [B*Hv][D][tp]
+  int ips, sf, sd, H, Hv, T, D, tp;
   View o;
-  int sf, sd;  // splits of off-diagonal / diagonal tiles (items ordered tile by tile)
 };
 
-// A operand of out = tril(S, -1) V: rows i of the 128-row block R, k = j; the
-// sum of a tile's split partials, masked to j < i, as bf16.
-struct PartRows {
-  static constexpr int BK = Mode<true>::BK, E = Mode<true>::E;
-  static constexpr int CPR = BK / E;
-  static constexpr int CPT = kTile * CPR / kNT;
-
-  const float* slab = nullptr;
-  int T = 0, sf = 1, sd = 1;
-  int R = 0;
-  float v[CPT][E];
-
-  __device__ __forceinline__ void load(int k0) {
+// out rows [32 rb, +32) of one (b,h) slab, all D: each wave owns 64 columns
+// (two 32x32 MFMA blocks) and loads its fragments straight from global
+// memory: A = the masked split sum of the partial score rows, B = V^T.  The
+// loads of U k16 steps (every split, predicated) are issued before any of
+// them is used, so a wave keeps U * (NS + 2) loads in flight.
+template <typename TO, int NS, int U>
+__global__ __launch_bounds__(256) void k_sy_sv(const SvArgs a) {
+  const int rb = blockIdx.x, slab = blockIdx.y;
+  const int b = slab / a.H, h = slab - b * a.H, hv = a.Hv == 1 ? 0 : h;
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int row = rb * 32 + (lane & 31);
+  const int kq = (lane >> 5) * 8;
+  const bf16_t* pslab = a.part + int64_t(slab) * a.ips * kSyTileElems;
+  const bf16_t* vtb = a.vt + (int64_t(b) * a.Hv + hv) * a.D * a.tp;
+  f32x16 acc[2];
 #pragma unroll
-    for (int c = 0; c < CPT; ++c) {
-      const int ch = threadIdx.x + c * kNT;
-      const int row = ch / CPR, kc = (ch % CPR) * E;
-      const int gi = R * kTile + row, gj = k0 + kc;
+  for (int c = 0; c < 2; ++c)
 #pragma unroll
-      for (int e = 0; e < E; ++e) v[c][e] = 0.f;
-      if (gi < T && gj < gi) {
-        const int ti = gi >> 8, tj = gj >> 8;
-        // items of the lower tiles in row-major order: row r holds r tiles of
-        // sf splits and one diagonal tile of sd splits
-        const int first = sf * (ti * (ti - 1) / 2 + tj) + sd * ti;
-        const float* p = slab + int64_t(first) * kSyTileElems + (gi & 255) * kSyTile + (gj & 255);
-        const int ns = ti == tj ? sd : sf;
-        for (int sp = 0; sp < ns; ++sp) {
-          const float4 x0 = *reinterpret_cast<const float4*>(p + int64_t(sp) * kSyTileElems);
-          const float4 x1 = *reinterpret_cast<const float4*>(p + int64_t(sp) * kSyTileElems + 4);
-          v[c][0] += x0.x; v[c][1] += x0.y; v[c][2] += x0.z; v[c][3] += x0.w;
-          v[c][4] += x1.x; v[c][5] += x1.y; v[c][6] += x1.z; v[c][7] += x1.w;
+    for (int r = 0; r < 16; ++r) acc[c][r] = 0.f;
+  const int ti = min(row, a.T - 1) >> 8;
+  const int kend = min(a.T, (rb + 1) * 32);  // keys j < rows of this block
+  const bool lastrow_ok = row < a.T;
+  int dcol[2];
+  bool dok[2];
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+    dcol[c] = 64 * w + 32 * c + (lane & 31);
+    dok[c] = dcol[c] < a.D;
+  }
+  for (int k0 = 0; k0 < kend; k0 += 16 * U) {
+    uint4 ra[U][NS];
+    bf16x8 rb2[U][2];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int j = k0 + 16 * u + kq;
+      const bool in = k0 + 16 * u < kend;
+      const bool av = in && lastrow_ok && j < row;
+      const int tj = j >> 8;
+      const int first = a.sf * (ti * (ti - 1) / 2 + tj) + a.sd * ti;
+      const int ns = ti == tj ? a.sd : a.sf;
+      const bf16_t* p = pslab + int64_t(first) * kSyTileElems + (row & 255) * kSyTile + (j & 255);
+#pragma unroll
+      for (int sp = 0; sp < NS; ++sp)
+        ra[u][sp] = (av && sp < ns) ? *reinterpret_cast<const uint4*>(p + int64_t(sp) * kSyTileElems)
+                                    : uint4{0u, 0u, 0u, 0u};
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+        rb2[u][c] = (in && dok[c]) ? *reinterpret_cast<const bf16x8*>(vtb + int64_t(dcol[c]) * a.tp + j)
+                                   : __builtin_bit_cast(bf16x8, u32x4{0u, 0u, 0u, 0u});
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (k0 + 16 * u >= kend) break;
+      const int j = k0 + 16 * u + kq;
+      float sacc[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) sacc[e] = 0.f;
+#pragma unroll
+      for (int sp = 0; sp < NS; ++sp) {
+        const uint32_t xw[4] = {ra[u][sp].x, ra[u][sp].y, ra[u][sp].z, ra[u][sp].w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          sacc[2 * e] += __uint_as_float(xw[e] << 16);
+          sacc[2 * e + 1] += __uint_as_float(xw[e] & 0xffff0000u);
         }
       }
+      uint32_t pk[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float lo = (j + 2 * e < row) ? sacc[2 * e] : 0.f;
+        const float hi = (j + 2 * e + 1 < row) ? sacc[2 * e + 1] : 0.f;
+        pk[e] = pack_bf2(lo, hi);
+      }
+      const bf16x8 fa = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(pk));
+#pragma unroll
+      for (int c = 0; c < 2; ++c) acc[c] = mma(fa, rb2[u][c], acc[c]);
     }
   }
-
-  __device__ __forceinline__ void store(LdsTile<true> dst, int k0) {
-#pragma unroll
-    for (int c = 0; c < CPT; ++c) {
-      const int ch = threadIdx.x + c * kNT;
-      const int row = ch / CPR, kc = (ch % CPR) * E;
-      const int gi = R * kTile + row, gj = k0 + kc;
-      float f[E];
-#pragma unroll
-      for (int e = 0; e < E; ++e) f[e] = (gj + e < gi) ? v[c][e] : 0.f;
-      lds_put<true>(dst, row, kc, f);
-    }
-  }
-};
-
-template <typename TV, typename TO>
-__global__ __launch_bounds__(kNT) void k_sy_score_v(const SyVArgs a) {
-  __shared__ Smem<true> sm;
-  const int R = blockIdx.x, Dt = blockIdx.y, slab = blockIdx.z;
-  const int b = slab / int(a.H), h = slab % int(a.H);
-  const int hv = a.Hv == 1 ? 0 : h;
-  PartRows la;
-  la.slab = a.part + int64_t(slab) * a.ips * kSyTileElems;
-  la.T = int(a.T);
-  la.sf = a.sf;
-  la.sd = a.sd;
-  la.R = R;
-  NRows<TV, true, false> lb;
-  lb.base = static_cast<const TV*>(a.v.p) + b * a.v.s0 + hv * a.v.s1;
-  lb.rs = a.v.s2;
-  lb.n0 = Dt * kTile;
-  lb.ncols = int(a.Dv);
-  lb.krows = int(a.T);
-  lb.vec4 = a.vec4_v;
-  f32x16 acc[2][2];
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
-  const int ke = int(min(a.T, int64_t(R + 1) * kTile));
-  mainloop<true, false>(sm, la, lb, false, 0, ke, acc, true);
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int wm = wave >> 1, wn = wave & 1;
   TO* o = static_cast<TO*>(const_cast<void*>(a.o.p)) + b * a.o.s0 + h * a.o.s1;
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int c = 0; c < 2; ++c)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        int row, col;
-        acc_coord<false>(wm, wn, lane, i, j, r, row, col);
-        const int gi = R * kTile + row, gd = Dt * kTile + col;
-        if (gi < a.T && gd < a.Dv) o[int64_t(gi) * a.o.s2 + gd] = from_f<TO>(acc[i][j][r]);
-      }
+    for (int r = 0; r < 16; ++r) {
+      const int i = rb * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+      if (i < a.T && dok[c]) o[int64_t(i) * a.o.s2 + dcol[c]] = from_f<TO>(acc[c][r]);
+    }
+}
+
+template <typename TO>
+int launch_sy_sv(const SvArgs& sa, dim3 grid, hipStream_t s) {
+  const int ns = std::max(sa.sf, sa.sd);
+  if (ns <= 2)
+    BDH_LAUNCH("k_sy_sv", (k_sy_sv<TO, 2, 4>), grid, dim3(256), 0, s, sa);
+  else if (ns <= 4)
+    BDH_LAUNCH("k_sy_sv", (k_sy_sv<TO, 4, 4>), grid, dim3(256), 0, s, sa);
+  else
+    BDH_LAUNCH("k_sy_sv", (k_sy_sv<TO, 8, 2>), grid, dim3(256), 0, s, sa);
+  return BDH_OK;
 }
 
 // ---------------------------------------------------------------- host plan
+// Table rows are padded by 256 bytes so the rows one DMA instruction reads
+// (same pair offset, consecutive positions) fall on different L2 channels.
+inline int sy_table_pitch(int64_t N) { return int(N / 2) + 64; }
+// V^T rows hold the positions padded to a multiple of 32 (zeros beyond T).
+inline int sy_vt_pitch(int64_t T) { return int((T + 31) / 32 * 32); }
+
 struct SyPlan {
   int nt = 0, ntl = 0, ips = 0, nchunk = 0, sf = 1, sd = 1;
-  size_t table_bytes = 0, part_bytes = 0, ws_bytes = 0;
+  size_t table_bytes = 0, part_bytes = 0, vt_bytes = 0, ws_bytes = 0;
   uint32_t items[kSyMaxItems];
   bool ok = false;
 };
 
 // Split factors: the smallest full-tile split that gives every CU a work item,
 // diagonal tiles (36/64 of a full tile's MFMAs when Q = K) split in proportion.
-SyPlan sy_plan(int64_t nslab, int64_t T, int64_t N, bool self, bool rope) {
+SyPlan sy_plan(int64_t nslab, int64_t T, int64_t N, bool self, bool rope, int64_t Dv = 0) {
   SyPlan p;
   if (T <= 0 || N <= 0 || N % 64 != 0 || nslab <= 0) return p;
   p.nt = int((T + kSyTile - 1) / kSyTile);
@@ -491,9 +580,11 @@ SyPlan sy_plan(int64_t nslab, int64_t T, int64_t N, bool self, bool rope) {
         p.items[n++] = uint32_t(ti) | (uint32_t(tj) << 8) | (uint32_t(s) << 16) | (uint32_t(ns) << 24);
     }
   p.ips = n;
-  p.table_bytes = rope ? align_up(size_t(T) * size_t(N / 2) * 4, 256) : 0;
-  p.part_bytes = size_t(nslab) * size_t(p.ips) * kSyTileElems * sizeof(float);
-  p.ws_bytes = p.table_bytes + p.part_bytes;
+  p.table_bytes = rope ? align_up(size_t(T) * size_t(sy_table_pitch(N)) * 4, 256) : 0;
+  p.part_bytes = size_t(nslab) * size_t(p.ips) * kSyTileElems * sizeof(bf16_t);
+  // V^T for the score x V product: at most one copy per (b, h) slab
+  p.vt_bytes = align_up(size_t(nslab) * size_t(Dv) * size_t(sy_vt_pitch(T)) * sizeof(bf16_t), 256);
+  p.ws_bytes = p.table_bytes + p.part_bytes + p.vt_bytes;
   p.ok = true;
   return p;
 }
@@ -513,18 +604,11 @@ bool vec4_rows_sy(const bdh_tensor4* t) {
   return t->size[3] % 4 == 0;
 }
 
-template <typename TV, typename TO>
-int launch_sy_sv(const SyVArgs& va, int64_t nslab, hipStream_t s) {
-  dim3 grid(unsigned((va.T + kTile - 1) / kTile), unsigned((va.Dv + kTile - 1) / kTile), unsigned(nslab));
-  BDH_LAUNCH("k_sy_score_v", (k_sy_score_v<TV, TO>), grid, dim3(kNT), 0, s, va);
-  return BDH_OK;
-}
-
 }  // namespace
 
-size_t sy_workspace(int64_t B, int64_t H, int64_t T, int64_t N, bool rope) {
-  const SyPlan p = sy_plan(B * H, T, N, true, rope);
-  const SyPlan p2 = sy_plan(B * H, T, N, false, rope);
+size_t sy_workspace(int64_t B, int64_t H, int64_t T, int64_t N, int64_t Dv, bool rope) {
+  const SyPlan p = sy_plan(B * H, T, N, true, rope, Dv);
+  const SyPlan p2 = sy_plan(B * H, T, N, false, rope, Dv);
   return p.ok ? std::max(p.ws_bytes, p2.ok ? p2.ws_bytes : size_t(0)) : 0;
 }
 
@@ -538,22 +622,27 @@ int sy_cold(const bdh_tensor4* q, const bdh_tensor4* k, const bdh_tensor4* v, co
   const bool rope = freqs != nullptr;
   if (rope && !self) return kNotEligible;
   if (T < 1 || N < 64 || N % 64 != 0 || !rows16(q) || !rows16(k)) return kNotEligible;
+  if (v->size[3] > 256) return kNotEligible;  // score x V: four waves x 64 columns
   if (((T - 1) * std::max(q->stride[2], k->stride[2]) + N) * 2 >= (int64_t(1) << 31)) return kNotEligible;
-  if (rope && int64_t(T) * N * 2 >= (int64_t(1) << 31)) return kNotEligible;
+  if (rope && int64_t(T) * sy_table_pitch(N) * 4 >= (int64_t(1) << 31)) return kNotEligible;
+  if (T > 65535) return kNotEligible;
   if (qr != nullptr && (qr->dtype != BDH_BF16 || !rows16(qr))) return kNotEligible;
   const int64_t nslab = B * H;
   if (nslab > (int64_t(1) << 24)) return kNotEligible;
-  SyPlan p = sy_plan(nslab, T, N, self, rope);
+  const int64_t Dv = v->size[3];
+  SyPlan p = sy_plan(nslab, T, N, self, rope, Dv);
   if (!p.ok) return kNotEligible;
+  const int64_t grid_scores = 8 * ((nslab + 7) / 8) * p.ips;
+  if (grid_scores >= (int64_t(1) << 31)) return kNotEligible;
   if (ws == nullptr || ws_bytes < p.ws_bytes) return BDH_ERR_WORKSPACE;
 
   uint8_t* wsb = static_cast<uint8_t*>(ws);
   uint32_t* table = rope ? reinterpret_cast<uint32_t*>(wsb) : nullptr;
-  float* part = reinterpret_cast<float*>(wsb + p.table_bytes);
+  bf16_t* part = reinterpret_cast<bf16_t*>(wsb + p.table_bytes);
+  const int tpitch = sy_table_pitch(N);
   if (rope) {
-    const int64_t n = T * (N / 2);
-    BDH_LAUNCH("k_rope_table", k_rope_table, dim3(unsigned((n + 255) / 256)), dim3(256), 0, s, freqs, rope_start,
-               int(T), int(N / 2), table);
+    BDH_LAUNCH("k_rope_table", k_rope_table, dim3(unsigned((N / 2 + 255) / 256), unsigned(T)), dim3(256), 0, s,
+               freqs, rope_start, int(N / 2), tpitch, table);
   }
   SyArgs a;
   a.q = static_cast<const bf16_t*>(q->data);
@@ -571,6 +660,7 @@ int sy_cold(const bdh_tensor4* q, const bdh_tensor4* k, const bdh_tensor4* v, co
   a.ips = p.ips;
   a.nchunk = p.nchunk;
   a.cs = table;
+  a.tpitch = tpitch;
   a.part = part;
   a.qr = nullptr;
   a.r0 = a.r1 = a.r2 = 0;
@@ -581,32 +671,44 @@ int sy_cold(const bdh_tensor4* q, const bdh_tensor4* k, const bdh_tensor4* v, co
     a.r2 = qr->stride[2];
   }
   for (int i = 0; i < p.ips; ++i) a.items[i] = p.items[i];
-  const int64_t grid = 8 * ((nslab + 7) / 8) * p.ips;
-  if (grid >= (int64_t(1) << 31)) return kNotEligible;
+  const dim3 gs{unsigned(grid_scores)};
   if (rope)
-    BDH_LAUNCH("k_sy_scores", (k_sy_scores<true, true>), dim3(unsigned(grid)), dim3(kSyThreads), 0, s, a);
+    BDH_LAUNCH("k_sy_scores", (k_sy_scores<true, true>), gs, dim3(kSyThreads), 0, s, a);
   else if (self)
-    BDH_LAUNCH("k_sy_scores", (k_sy_scores<false, true>), dim3(unsigned(grid)), dim3(kSyThreads), 0, s, a);
+    BDH_LAUNCH("k_sy_scores", (k_sy_scores<false, true>), gs, dim3(kSyThreads), 0, s, a);
   else
-    BDH_LAUNCH("k_sy_scores", (k_sy_scores<false, false>), dim3(unsigned(grid)), dim3(kSyThreads), 0, s, a);
+    BDH_LAUNCH("k_sy_scores", (k_sy_scores<false, false>), gs, dim3(kSyThreads), 0, s, a);
   if (numel4(out) == 0) return BDH_OK;
 
-  SyVArgs va;
-  va.part = part;
-  va.ips = p.ips;
-  va.v = view_of(v);
-  va.H = H;
-  va.Hv = v->size[1];
-  va.T = T;
-  va.Dv = v->size[3];
-  va.vec4_v = vec4_rows_sy(v);
-  va.o = view_of(out);
-  va.o.s1 = out->stride[1];
-  va.sf = p.sf;
-  va.sd = p.sd;
-  const bool vb = v->dtype == BDH_BF16, ob = out->dtype == BDH_BF16;
-  if (vb) return ob ? launch_sy_sv<bf16_t, bf16_t>(va, nslab, s) : launch_sy_sv<bf16_t, float>(va, nslab, s);
-  return ob ? launch_sy_sv<float, bf16_t>(va, nslab, s) : launch_sy_sv<float, float>(va, nslab, s);
+  // score x V: V^T once, then the direct-load MFMA kernel
+  const int tp = sy_vt_pitch(T);
+  bf16_t* vt = reinterpret_cast<bf16_t*>(wsb + p.table_bytes + p.part_bytes);
+  const int Hv = int(v->size[1]);
+  const int D = int(Dv);
+  {
+    View vv = view_of(v);
+    vv.s1 = v->stride[1];
+    const dim3 gv(unsigned((tp + 31) / 32), unsigned((D + 31) / 32), unsigned(B * Hv));
+    if (v->dtype == BDH_BF16)
+      BDH_LAUNCH("k_sy_vt", k_sy_vt<bf16_t>, gv, dim3(256), 0, s, vv, Hv, int(T), D, tp, vt);
+    else
+      BDH_LAUNCH("k_sy_vt", k_sy_vt<float>, gv, dim3(256), 0, s, vv, Hv, int(T), D, tp, vt);
+  }
+  SvArgs sa;
+  sa.part = part;
+  sa.vt = vt;
+  sa.ips = p.ips;
+  sa.sf = p.sf;
+  sa.sd = p.sd;
+  sa.H = int(H);
+  sa.Hv = Hv;
+  sa.T = int(T);
+  sa.D = D;
+  sa.tp = tp;
+  sa.o = view_of(out);
+  sa.o.s1 = out->stride[1];
+  const dim3 gsv(unsigned((T + 31) / 32), unsigned(nslab));
+  return out->dtype == BDH_BF16 ? launch_sy_sv<bf16_t>(sa, gsv, s) : launch_sy_sv<float>(sa, gsv, s);
 }
 
 }  // namespace bdh
