@@ -26,6 +26,7 @@ import torch
 
 __all__ = [
     "has_hip",
+    "has_cuda",
     "lib_path",
     "version",
     "tril_score_v",
@@ -119,6 +120,9 @@ def _load():
 
 _lib, _path = _load()
 has_hip = True
+# The reference's pybind module reports has_cuda (tril_attn_bind.cpp:34-39); this
+# library has no CUDA path, so a caller probing that attribute sees False.
+has_cuda = False
 lib_path = str(_path)
 _launches = 0
 

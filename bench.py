@@ -46,6 +46,7 @@ PEAK_HBM_GBS = 8000.0
 C1 = dict(B=8, nh=4, T=512, N=8192, D=256)
 C3 = dict(B=64, nh=4, N=8192, D=256, S=(256, 384, 511))
 C4 = dict(B=16, nh=4, T=1024, N=8192, D=256)
+CALIB_BYTES = 1 << 29  # plain copy used to scale the HBM byte counters
 
 
 def log(msg: str) -> None:
@@ -146,6 +147,12 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--no-extra", action="store_true", help="skip the decode / backward / comparison legs")
+    ap.add_argument(
+        "--calibrate",
+        action="store_true",
+        help="also run one plain device copy of CALIB_BYTES (the reference point that scales the "
+        "rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes)",
+    )
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -174,6 +181,14 @@ def main() -> int:
 
     def step():
         return kernels.bdh_attn_rope(x, v, freqs, 0, impl="hip")
+
+    if args.calibrate:
+        src = torch.ones(CALIB_BYTES // 4, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"[bench] calibration copy: {CALIB_BYTES} bytes read, {CALIB_BYTES} bytes written")
+        del src, dst
 
     launches0 = ext.launch_count()
     ms = time_steps(step, args.steps, args.warmup)
