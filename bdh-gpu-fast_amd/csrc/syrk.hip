@@ -33,6 +33,7 @@
 //     the partial score rows (formed in fp32, masked, rounded to bf16) and V^T.
 #include <algorithm>
 #include <type_traits>
+#include <utility>
 
 #include "fwd.h"
 
@@ -52,18 +53,22 @@ constexpr int kSyTileElems = kSyTile * kSyTile;
 
 typedef __attribute__((address_space(3))) uint8_t lds_u8;
 
+// Work item word: ta | tb << 8 | split << 16 | kind << 24.  kSyFull: tile
+// (ta, tb), ta > tb, or any tile when Q != K; kSyDiag2: diagonal tiles ta and
+// tb; kSyDiag1: diagonal tile ta alone (tb = ta: loaded twice, stored once).
+enum : int { kSyFull = 0, kSyDiag2 = 1, kSyDiag1 = 2 };
+
 struct SyArgs {
   const bf16_t* q;
   const bf16_t* k;
   int64_t q0, q1, q2;  // element strides of q over (b, h, t)
   int64_t k0, k1, k2;
-  int H, T, N, nslab, ips, nchunk;
-  const uint32_t* cs;  // RoPE table [T][tpitch] (first N/2 used) or null
-  int tpitch;          // table row pitch in dwords
-  bf16_t* part;        // [nslab][ips][256*256] partial score tiles (bf16)
+  int H, T, N, nslab, ips, nchunk, nsplit, ntl;
+  const uint32_t* cs;  // RoPE table, stage-major [N/32][T][16] (cos, sin) dwords, or null
+  bf16_t* part;        // [nslab][ntl][nsplit][256*256] partial score tiles (bf16)
   bf16_t* qr;          // optional RoPE(x) copy
   int64_t r0, r1, r2;
-  uint32_t items[kSyMaxItems];  // ti | tj << 8 | split << 16 | nsplit << 24
+  uint32_t items[kSyMaxItems];
 };
 
 __shared__ __attribute__((aligned(1024))) uint8_t sy_lds[kSyLdsSlots * kSySlot];  // 160 KB
@@ -80,26 +85,22 @@ __device__ __forceinline__ const void* sgpr_ptr(const void* p) {
   return reinterpret_cast<const void*>((uint64_t(hi) << 32) | lo);
 }
 
-__device__ __forceinline__ void dma16(uint32_t lds, const void* gbase, uint32_t voff) {
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
+// 16 bytes per lane from gbase + voff to LDS address m0base + IMM + 16 * lane.
+// The immediate keeps one scalar base per stage instead of one per instruction.
+template <int IMM>
+__device__ __forceinline__ void dma16(uint32_t m0base, const void* gbase, uint32_t voff) {
+  asm volatile("s_add_u32 m0, %0, %3\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
                :
-               : "s"(lds), "v"(voff), "s"(gbase)
-               : "memory", "m0");
+               : "s"(m0base), "v"(voff), "s"(gbase), "i"(IMM)
+               : "memory", "m0", "scc");
 }
 
-// Wait until at most n vector-memory operations of this wave are outstanding
+// Wait until at most N vector-memory operations of this wave are outstanding
 // (they complete in issue order).
-__device__ __forceinline__ void sy_wait(int n) {
-  switch (n) {
-    case 0: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
-    case 2: asm volatile("s_waitcnt vmcnt(2)" ::: "memory"); break;
-    case 4: asm volatile("s_waitcnt vmcnt(4)" ::: "memory"); break;
-    case 6: asm volatile("s_waitcnt vmcnt(6)" ::: "memory"); break;
-    case 8: asm volatile("s_waitcnt vmcnt(8)" ::: "memory"); break;
-    case 10: asm volatile("s_waitcnt vmcnt(10)" ::: "memory"); break;
-    case 12: asm volatile("s_waitcnt vmcnt(12)" ::: "memory"); break;
-    default: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
-  }
+template <int N>
+__device__ __forceinline__ void sy_wait() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
 __device__ __forceinline__ void sy_barrier() {
@@ -111,9 +112,9 @@ __device__ __forceinline__ void sy_barrier() {
 // x.lo = x[2m], x.hi = x[2m+1] with cs = (cos, sin) as bf16 halves, giving
 // (x0 c - x1 s, x1 c + x0 s) rounded to bf16 once (products exact in fp32).
 // One asm block so the hazard spacing is explicit: a v_dot2 result is read
-// no sooner than three wait states after it is written (s_nop 2).
+// no sooner than three wait states after it is written (s_nop 2).  The
+// results overwrite the swapped copies, which are dead by then.
 __device__ __forceinline__ u32x4 rot_chunk(u32x4 x, u32x4 cs) {
-  u32x4 y;
   uint32_t s0, s1, s2, s3;
   float a0, a1, a2, a3, b0, b1, b2, b3;
   asm("v_alignbit_b32 %[s0], %[x0], %[x0], 16\n\t"
@@ -129,21 +130,16 @@ __device__ __forceinline__ u32x4 rot_chunk(u32x4 x, u32x4 cs) {
       "v_dot2_f32_bf16 %[b2], %[s2], %[c2], 0\n\t"
       "v_dot2_f32_bf16 %[b3], %[s3], %[c3], 0\n\t"
       "s_nop 2\n\t"
-      "v_cvt_pk_bf16_f32 %[y0], %[a0], %[b0]\n\t"
-      "v_cvt_pk_bf16_f32 %[y1], %[a1], %[b1]\n\t"
-      "v_cvt_pk_bf16_f32 %[y2], %[a2], %[b2]\n\t"
-      "v_cvt_pk_bf16_f32 %[y3], %[a3], %[b3]"
-      : [y0] "=&v"(y.x), [y1] "=&v"(y.y), [y2] "=&v"(y.z), [y3] "=&v"(y.w),
-        [s0] "=&v"(s0), [s1] "=&v"(s1), [s2] "=&v"(s2), [s3] "=&v"(s3),
+      "v_cvt_pk_bf16_f32 %[s0], %[a0], %[b0]\n\t"
+      "v_cvt_pk_bf16_f32 %[s1], %[a1], %[b1]\n\t"
+      "v_cvt_pk_bf16_f32 %[s2], %[a2], %[b2]\n\t"
+      "v_cvt_pk_bf16_f32 %[s3], %[a3], %[b3]"
+      : [s0] "=&v"(s0), [s1] "=&v"(s1), [s2] "=&v"(s2), [s3] "=&v"(s3),
         [a0] "=&v"(a0), [a1] "=&v"(a1), [a2] "=&v"(a2), [a3] "=&v"(a3),
         [b0] "=&v"(b0), [b1] "=&v"(b1), [b2] "=&v"(b2), [b3] "=&v"(b3)
       : [x0] "v"(x.x), [x1] "v"(x.y), [x2] "v"(x.z), [x3] "v"(x.w),
         [c0] "v"(cs.x), [c1] "v"(cs.y), [c2] "v"(cs.z), [c3] "v"(cs.w));
-  return y;
-}
-
-__device__ __forceinline__ bf16x8 frag(const uint8_t* blk, int rb, uint32_t loff) {
-  return *reinterpret_cast<const bf16x8*>(blk + rb * 2048 + loff);
+  return u32x4{s0, s1, s2, s3};
 }
 
 __device__ __forceinline__ f32x16 mma(bf16x8 a, bf16x8 b, f32x16 c) {
@@ -151,8 +147,11 @@ __device__ __forceinline__ f32x16 mma(bf16x8 a, bf16x8 b, f32x16 c) {
 }
 
 // ------------------------------------------------------------------ kernels
+// RoPE table, stage-major: the (cos, sin) of pair m at position t sits in
+// dword ((m / 16) * T + t) * 16 + m % 16, so the table entries one k32 stage
+// of the score kernel needs for a 256-row block are one contiguous 16 KB run.
 __global__ __launch_bounds__(256) void k_rope_table(const float* __restrict__ freqs, int64_t rope_start,
-                                                    int N2, int pitch, uint32_t* __restrict__ cs) {
+                                                    int N2, int T, uint32_t* __restrict__ cs) {
   const int t = blockIdx.y, m = blockIdx.x * 256 + threadIdx.x;
   if (m >= N2) return;
   // phase = fp32(pos) * freq, then cos/sin of 2 pi frac(phase); v_cos/v_sin
@@ -160,8 +159,53 @@ __global__ __launch_bounds__(256) void k_rope_table(const float* __restrict__ fr
   // values are rounded to bf16, far above the hardware functions' error.
   const float ph = __fmul_rn(float(rope_start + t), freqs[2 * m]);
   const float fr = ph - floorf(ph);
-  cs[int64_t(t) * pitch + m] = pack_bf2(__builtin_amdgcn_cosf(fr), __builtin_amdgcn_sinf(fr));
+  cs[(int64_t(m >> 4) * T + t) * 16 + (m & 15)] = pack_bf2(__builtin_amdgcn_cosf(fr), __builtin_amdgcn_sinf(fr));
 }
+
+// Diagonal tiles (Q = K) in pairs: the 36 lower 32x32 blocks of one diagonal
+// tile are split into four wave programs of 9 blocks; waves 0-3 run them on
+// the first tile of the pair and waves 4-7 on the second, so each SIMD issues
+// 18 MFMAs per k16 step (a full tile: 16).  Because A and B are the same row
+// block, the fragment of row block r serves as either operand.
+struct SyDiagWave {
+  int nf;        // fragments per k16 step
+  int rows[6];   // their row blocks
+  int bi[9], bj[9];  // output blocks (row block, column block)
+};
+constexpr SyDiagWave kSyDiag[4] = {
+    {6, {0, 1, 4, 5, 6, 7}, {4, 4, 5, 5, 6, 6, 7, 7, 0}, {0, 1, 0, 1, 0, 1, 0, 1, 0}},
+    {6, {2, 3, 4, 5, 6, 7}, {4, 4, 5, 5, 6, 6, 7, 7, 4}, {2, 3, 2, 3, 2, 3, 2, 3, 4}},
+    {4, {0, 1, 2, 3, 0, 0}, {1, 1, 2, 2, 2, 3, 3, 3, 3}, {0, 1, 0, 1, 2, 0, 1, 2, 3}},
+    {4, {4, 5, 6, 7, 0, 0}, {5, 5, 6, 6, 6, 7, 7, 7, 7}, {4, 5, 4, 5, 6, 4, 5, 6, 7}},
+};
+constexpr int sy_fidx(const SyDiagWave& d, int r) {
+  for (int k = 0; k < d.nf; ++k)
+    if (d.rows[k] == r) return k;
+  return -1;
+}
+// Wave program WT: 0 = a 128x64 corner of a full tile (8 blocks), 1..4 = the
+// diagonal programs above.  Fragment indices of the A and B operands of MFMA m.
+// Compile-time loop: f(integral_constant<int, i>) for i = 0 .. N-1, so array
+// indices derived from i are constants (registers, not scratch).
+template <typename F, int... I>
+__device__ __forceinline__ void sy_static_for_impl(F&& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>()), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void sy_static_for(F&& f) {
+  sy_static_for_impl(f, std::make_integer_sequence<int, N>());
+}
+
+template <int WT>
+struct SyProg {
+  static constexpr int nf = WT == 0 ? 6 : kSyDiag[WT - 1].nf;
+  static constexpr int nm = WT == 0 ? 8 : 9;
+  static constexpr int fa(int m) { return WT == 0 ? m >> 1 : sy_fidx(kSyDiag[WT - 1], kSyDiag[WT - 1].bi[m]); }
+  static constexpr int fb(int m) { return WT == 0 ? 4 + (m & 1) : sy_fidx(kSyDiag[WT - 1], kSyDiag[WT - 1].bj[m]); }
+  static constexpr int row(int k) { return WT == 0 ? 0 : kSyDiag[WT - 1].rows[k]; }
+  static constexpr int bi(int m) { return WT == 0 ? 0 : kSyDiag[WT - 1].bi[m]; }
+  static constexpr int bj(int m) { return WT == 0 ? 0 : kSyDiag[WT - 1].bj[m]; }
+};
 
 template <bool ROPE, bool SELF>
 __global__ __launch_bounds__(kSyThreads, 1) void k_sy_scores(const SyArgs a) {
@@ -172,13 +216,14 @@ __global__ __launch_bounds__(kSyThreads, 1) void k_sy_scores(const SyArgs a) {
   if (slab >= a.nslab) return;
   const int itx = kk - grp * a.ips;
   const uint32_t item = a.items[itx];
-  const int ti = item & 255, tj = (item >> 8) & 255, split = (item >> 16) & 255, nsplit = int(item >> 24);
-  const bool diag = SELF && ti == tj;
+  const int ta = item & 255, tb = (item >> 8) & 255, split = (item >> 16) & 255;
+  const int kind = int(item >> 24);
+  const bool diag = SELF && kind != kSyFull;
   const int b = slab / a.H, h = slab - b * a.H;
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int ndma = diag ? 2 : 4;  // 1 KB DMA instructions per wave per stage
-  const int nch = (a.nchunk - split + nsplit - 1) / nsplit;
+  const int S = a.nsplit;
+  const int nch = (a.nchunk - split + S - 1) / S;
   const int nst = 2 * nch;
 
   const void* baseA = sgpr_ptr(a.q + b * a.q0 + h * a.q1);
@@ -187,8 +232,8 @@ __global__ __launch_bounds__(kSyThreads, 1) void k_sy_scores(const SyArgs a) {
   const uint32_t lds0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_u8*)sy_lds);
 
   // Per DMA instruction u: the 16-byte chunk this lane moves (and rotates).
+  // Instructions 0-1 fill the row block of tile row ta, 2-3 that of tb.
   uint32_t xoff[4], toff[4];
-  int rowg[4], kch[4];
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
     const int q = (u * 8 + w) * 1024 + lane * 16;
@@ -196,210 +241,279 @@ __global__ __launch_bounds__(kSyThreads, 1) void k_sy_scores(const SyArgs a) {
     const int ob = q & (kSyBlk - 1);
     const int row = ob >> 6;
     const int c = ((ob >> 4) & 3) ^ ((row >> 2) & 3);
-    const int rg = (blk == 0 ? ti : tj) * kSyTile + row;
+    const int rg = (blk == 0 ? ta : tb) * kSyTile + row;
     const int rc = rg < a.T ? rg : a.T - 1;
-    rowg[u] = rg;
-    kch[u] = 8 * c;
     xoff[u] = uint32_t((int64_t(rc) * (blk == 0 ? a.q2 : (SELF ? a.q2 : a.k2)) + 8 * c) * 2);
-    toff[u] = uint32_t(int64_t(rc) * a.tpitch * 4 + 16 * c);
+    toff[u] = uint32_t(rc * 64 + 16 * c);
   }
-  // MFMA fragment offsets within a row block for the two k16 steps of a stage.
+  // MFMA fragment offsets within a row block for the two k16 halves of a stage.
   uint32_t loff[2];
 #pragma unroll
   for (int kk2 = 0; kk2 < 2; ++kk2) {
     const int c = (2 * kk2 + (lane >> 5)) ^ ((lane >> 2) & 3);
     loff[kk2] = uint32_t((lane & 31) * 64 + c * 16);
   }
+  // RoPE(x) copy: each row of a slab belongs to exactly one diagonal tile and
+  // each k chunk to one split, so the diagonal items write it (the first row
+  // block only for a single diagonal tile, which loads it twice).
+  const bool write_qr = ROPE && a.qr != nullptr && diag;
 
-  auto kofs = [&](int s) { return (split + nsplit * (s >> 1)) * 64 + (s & 1) * 32; };
-  // x ring depth; issuing runs NX - 1 stages ahead of the MFMAs
-  constexpr int NX = ROPE ? 3 : 5;
-  auto slot = [&](int s) { return sy_lds + (s % NX) * kSySlot; };
-  auto tslot = [&](int s) { return sy_lds + (NX + (s & 1)) * kSySlot; };
-  auto rotate = [&](int s) {
-    uint8_t* sl = slot(s);
-    const int k0 = kofs(s);
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      if (u < ndma) {
-        const int off = (u * 8 + w) * 1024 + lane * 16;
-        u32x4* p = reinterpret_cast<u32x4*>(sl + off);
-        const u32x4 x = *p;
-        const u32x4 t = *reinterpret_cast<const u32x4*>(tslot(s) + off);
-        const u32x4 y = rot_chunk(x, t);
-        *p = y;
-        if (a.qr != nullptr && diag && rowg[u] < a.T)
-          *reinterpret_cast<u32x4*>(a.qr + b * a.r0 + h * a.r1 + int64_t(rowg[u]) * a.r2 + k0 + kch[u]) = y;
-      }
+  auto kofs = [&](int s) { return (split + S * (s >> 1)) * 64 + (s & 1) * 32; };
+  // x ring depth; issuing runs NX - 1 stages ahead of the MFMAs.  With RoPE
+  // the two remaining slots hold the table entries of the next two stages.
+  // LDS: an x ring of NX slots, issued lead = NX - 1 stages ahead; with RoPE
+  // four x slots and one slot for the table entries of the next stage.
+  constexpr int NX = ROPE ? 4 : 5;
+  constexpr int lead = NX - 1;
+  auto xslot_ofs = [&](int s) { return (s % NX) * kSySlot; };
+  auto slot = [&](int s) { return sy_lds + xslot_ofs(s); };
+  auto tslot = [&](int) { return sy_lds + NX * kSySlot; };
+  // The DMA instructions of one stage: per-stage scalar bases, per-instruction
+  // immediates (instruction u of wave w fills LDS bytes [(8u + w) KB, +1 KB)
+  // of its slot).
+  const uint32_t wl = lds0 + uint32_t(w) * 1024u;
+  struct StageDma {
+    uint32_t xm0, tm0, kx, kt;
+  };
+  // Stage st goes to the slots of st; stages past the end re-load the last
+  // stage into slots that are no longer read, so every stage issues the same
+  // instructions and every wait counts the same number of them.
+  auto stage_dma = [&](int st) {
+    StageDma d;
+    const int ko = kofs(min(st, nst - 1));
+    d.xm0 = wl + uint32_t(xslot_ofs(st));
+    d.tm0 = wl + uint32_t(NX * kSySlot);
+    d.kx = uint32_t(ko * 2);
+    d.kt = uint32_t(ko >> 5) * uint32_t(a.T) * 64u;
+    return d;
+  };
+  auto dma_x = [&](const StageDma& d, auto uc) {
+    constexpr int u = decltype(uc)::value;
+    dma16<u * 8192>(d.xm0, u < 2 ? baseA : baseB, xoff[u] + d.kx);
+  };
+  auto dma_t = [&](const StageDma& d, auto ic) {
+    constexpr int i = decltype(ic)::value;
+    dma16<i * 8192>(d.tm0, tbase, toff[i] + d.kt);
+  };
+  // RoPE in place of chunk u of stage s (this lane's own DMA chunk)
+  // (the row and chunk of instruction u follow from the lane: row
+  // (u & 1) * 128 + 16 w + lane / 4 of the block of tile row ta (u < 2) or tb,
+  // chunk (lane & 3) ^ ((lane >> 4) & 3) of the 64-byte row)
+  const int vrot = w * 1024 + lane * 16;
+  auto rot_store = [&](int s, int u, u32x4 x, u32x4 t) {
+    const u32x4 y = rot_chunk(x, t);
+    *reinterpret_cast<u32x4*>(slot(s) + vrot + u * 8192) = y;
+    if (write_qr && (kind == kSyDiag2 || u < 2)) {
+      const int rg = (u < 2 ? ta : tb) * kSyTile + (u & 1) * 128 + 16 * w + (lane >> 2);
+      const int c = (lane & 3) ^ ((lane >> 4) & 3);
+      if (rg < a.T)
+        *reinterpret_cast<u32x4*>(a.qr + b * a.r0 + h * a.r1 + int64_t(rg) * a.r2 + kofs(s) + 8 * c) = y;
     }
   };
+  auto rot_load = [&](int s, int u, u32x4& x, u32x4& t) {
+    x = *reinterpret_cast<const u32x4*>(slot(s) + vrot + u * 8192);
+    t = *reinterpret_cast<const u32x4*>(tslot(s) + vrot + u * 8192);
+  };
 
-  f32x16 acc[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) acc[i][r] = 0.f;
-
-  // Wave tile: rows [128 wm, +128) x cols [64 wn, +64) = 4 x 2 blocks of 32x32.
-  // On a diagonal tile only blocks with row block >= column block are needed;
-  // the wave tiles then cost 7,3,0,0 (wm = 0) and 8,8,7,3 (wm = 1) MFMAs per
-  // k16 step, and waves w and w+4 (one SIMD) are given tiles summing to at
-  // most 10 (a full tile: 16).
-  int wm = w >> 2, wn = w & 3;
-  if (diag) {
-    constexpr int kDiagWave[8] = {4, 5, 0, 6, 2, 3, 7, 1};  // wm * 4 + wn per wave
-    const int t = kDiagWave[w];
-    wm = t >> 2;
-    wn = t & 3;
-  }
-  // Blocks (i, j) of the wave tile that lie on or below the diagonal:
-  // 0 all 8, 1 i >= j (7), 2 i >= j + 2 (3), 3 none.
-  const int wtype = !diag ? 0 : (4 * wm >= 2 * wn + 1) ? 0 : (4 * wm == 2 * wn) ? 1 : (4 * wm == 2 * wn - 2) ? 2 : 3;
-  // The wave tile type selects one of four instantiations of the whole
-  // pipeline (prologue, loop, epilogue), so each loop holds straight-line MFMA
-  // code; all of them run the same stages and barriers.
-  auto run = [&](auto wt_tag, auto diag_tag) {
+  // The wave program selects one of five instantiations of the whole pipeline
+  // (prologue, loop, epilogue), so each loop holds straight-line MFMA code; all
+  // of them run the same stages and barriers.
+  auto run = [&](auto wt_tag) {
     constexpr int WT = decltype(wt_tag)::value;
-    constexpr bool DG = decltype(diag_tag)::value;  // == diag
-    constexpr int NDMA = DG ? 2 : 4;
-    // vector-memory operations per stage per wave, in issue order: the table
-    // chunks (RoPE) then the x chunks
-    constexpr int per_stage = ROPE ? 2 * NDMA : NDMA;
-    auto dma_op = [&](int st, int i) {
-      const uint32_t kb = uint32_t(kofs(st) * 2);
-      if (ROPE && i < NDMA) {
-        dma16(lds0 + uint32_t((NX + (st & 1)) * kSySlot + (i * 8 + w) * 1024), tbase, toff[i] + kb);
-      } else {
-        const int u = ROPE ? i - NDMA : i;
-        dma16(lds0 + uint32_t((st % NX) * kSySlot + (u * 8 + w) * 1024), u < 2 ? baseA : baseB, xoff[u] + kb);
+    using P = SyProg<WT>;
+    constexpr int NF = P::nf, NM = P::nm;
+    // Fragment addresses: a per-wave base (with the lane's offset) in a
+    // register, the fragment's row block as an immediate.  Full tile: A rows
+    // 4 wm + k at fbase[0], B rows 2 wn + j at fbase[1]; diagonal: row
+    // block P::row(k) of the wave's tile at fbase[0].
+    int fbase[2][2];  // [half][A, B]
+    int tile_out;     // partial tile this wave writes (-1: none)
+    if constexpr (WT == 0) {
+      const int wm = w >> 2, wn = w & 3;
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf) {
+        fbase[hf][0] = 4 * wm * 2048 + int(loff[hf]);
+        fbase[hf][1] = kSyBlk + 2 * wn * 2048 + int(loff[hf]);
       }
+      tile_out = ta * (ta + 1) / 2 + tb;
+    } else {
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf) fbase[hf][0] = fbase[hf][1] = (w >> 2) * kSyBlk + int(loff[hf]);
+      const int t = w < 4 ? ta : tb;
+      tile_out = (w < 4 || kind == kSyDiag2) ? t * (t + 1) / 2 + t : -1;
+    }
+    f32x16 acc[NM];
+#pragma unroll
+    for (int i = 0; i < NM; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][r] = 0.f;
+    bf16x8 f0[NF], f1[NF];
+    auto read_frags = [&](bf16x8(&f)[NF], int s, int half) {
+      const uint8_t* pa = slot(s) + fbase[half][0];
+      const uint8_t* pb = slot(s) + fbase[half][1];
+      sy_static_for<NF>([&](auto kc) {
+        constexpr int k = decltype(kc)::value;
+        if constexpr (WT == 0)
+          f[k] = *reinterpret_cast<const bf16x8*>(k < 4 ? pa + k * 2048 : pb + (k - 4) * 2048);
+        else
+          f[k] = *reinterpret_cast<const bf16x8*>(pa + P::row(k) * 2048);
+      });
     };
-    // The MFMAs of stage s with the loads of stage `ahead` (if any) spread
-    // between them: issuing them all at once stalls the wave on the load
-    // queue while its MFMAs wait.  All fragments of the stage are read first
-    // into distinct registers (sched_group_barrier fixes that order; left
-    // alone the scheduler reuses a few registers and waits on each read right
-    // before its MFMA).
-    auto mma_stage = [&](int s, int ahead) {
-      const uint8_t* A = slot(s);
-      const uint8_t* B = DG ? A : A + kSyBlk;
-      const bool issue = ahead < nst;
-      // after MFMA number m of nm, issue the loads [m*P/nm, (m+1)*P/nm)
-      auto loads_after = [&](int m, int nm) {
-        if (!issue) return;
-#pragma unroll
-        for (int i = (m * per_stage) / nm; i < ((m + 1) * per_stage) / nm; ++i) dma_op(ahead, i);
-      };
-      if constexpr (WT == 0 || WT == 1) {
-        bf16x8 fa[2][4], fb[2][2];
-#pragma unroll
-        for (int k2 = 0; k2 < 2; ++k2) {
-#pragma unroll
-          for (int i = 0; i < 4; ++i) fa[k2][i] = frag(A, 4 * wm + i, loff[k2]);
-#pragma unroll
-          for (int j = 0; j < 2; ++j) fb[k2][j] = frag(B, 2 * wn + j, loff[k2]);
-        }
-        constexpr int NM = WT == 0 ? 16 : 14;
-        int m = 0;
-#pragma unroll
-        for (int k2 = 0; k2 < 2; ++k2)
-#pragma unroll
-          for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int j = 0; j < 2; ++j)
-              if (WT == 0 || i >= j) {
-                acc[2 * i + j] = mma(fa[k2][i], fb[k2][j], acc[2 * i + j]);
-                if (m == 0) {
-                  __builtin_amdgcn_sched_group_barrier(0x100, 12, 0);
-                  __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                }
-                loads_after(m, NM);
-                ++m;
-              }
-      } else if constexpr (WT == 2) {
-        bf16x8 fa[2][2], fb[2][2];
-#pragma unroll
-        for (int k2 = 0; k2 < 2; ++k2) {
-#pragma unroll
-          for (int i = 0; i < 2; ++i) fa[k2][i] = frag(A, 4 * wm + 2 + i, loff[k2]);
-#pragma unroll
-          for (int j = 0; j < 2; ++j) fb[k2][j] = frag(B, 2 * wn + j, loff[k2]);
-        }
-#pragma unroll
-        for (int k2 = 0; k2 < 2; ++k2) {
-          acc[4] = mma(fa[k2][0], fb[k2][0], acc[4]);
-          if (k2 == 0) {
-            __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-          }
-          loads_after(3 * k2, 6);
-          acc[6] = mma(fa[k2][1], fb[k2][0], acc[6]);
-          loads_after(3 * k2 + 1, 6);
-          acc[7] = mma(fa[k2][1], fb[k2][1], acc[7]);
-          loads_after(3 * k2 + 2, 6);
-        }
-      } else {
-        loads_after(0, 1);
-      }
-    };
-    constexpr auto live = [](int i, int j) { return WT == 0 || (WT == 1 && i >= j) || (WT == 2 && i >= j + 2); };
+
     // ------------------------------------------------------------ prologue
     // Issue order is what the waits count on: operations complete in order.
-    const int lead = NX - 1;
-    for (int st = 0; st < lead && st < nst; ++st)
-      for (int i = 0; i < per_stage; ++i) dma_op(st, i);
-    sy_wait((min(nst, lead) - 1) * per_stage);  // stage 0 landed
-    if (ROPE) rotate(0);
-    sy_barrier();
+    // Per stage each wave issues four x chunks of stage s + lead, two with
+    // each half, and (RoPE) the four table chunks of stage s+2 first thing
+    // after the mid-stage barrier.
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    using I2 = std::integral_constant<int, 2>;
+    using I3 = std::integral_constant<int, 3>;
+    for (int st = 0; st < lead - 1; ++st) {
+      const StageDma d = stage_dma(st);
+      sy_static_for<4>([&](auto uc) { dma_x(d, uc); });
+    }
+    {
+      const StageDma d = stage_dma(lead - 1);
+      dma_x(d, I0());
+      dma_x(d, I1());
+      if constexpr (ROPE) {
+        sy_static_for<4>([&](auto ic) { dma_t(stage_dma(0), ic); });
+        sy_wait<0>();  // stage 0 and its table landed
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          u32x4 x, t;
+          rot_load(0, u, x, t);
+          rot_store(0, u, x, t);
+        }
+        sy_barrier();
+        sy_static_for<4>([&](auto ic) { dma_t(stage_dma(1), ic); });
+        dma_x(d, I2());
+        dma_x(d, I3());
+      } else {
+        dma_x(d, I2());
+        dma_x(d, I3());
+        sy_wait<(lead - 1) * 4>();  // stage 0 landed
+        sy_barrier();
+      }
+    }
+    read_frags(f0, 0, 0);
 
     // ------------------------------------------------------------ main loop
-    for (int s = 0; s < nst; ++s) {
-      // the loads of stage s + lead go to x slot (s-1) % NX and (fused) table
-      // slot s % 2, consumed before the last barrier
-      mma_stage(s, s + lead);
-      if (s + 1 < nst) {
-        // stage s+1 landed (this wave's part): the stages issued after it may
-        // still be in flight
-        sy_wait((min(nst - 1, s + lead) - (s + 1)) * per_stage);
-        if (ROPE) rotate(s + 1);
+    // Stage s, per wave:
+    //  A. read the second-half fragments of s; first-half MFMAs of s with x
+    //     chunks 0-1 of stage s + lead issued between them; once this lane's
+    //     part of stage s+1 (and its table) landed, the rotation of stage s+1
+    //  B. barrier: stage s+1 is complete (loaded and rotated) in LDS
+    //  C. read the first-half fragments of s+1; (RoPE) issue the table of
+    //     stage s+2; second-half MFMAs of s with x chunks 2-3 of stage s + lead.
+    // The barrier sits between the halves, so after it the MFMA pipe runs the
+    // second half while the next fragments load.  Stage s + lead goes to x
+    // slot (s-1) % NX, last read before the previous barrier; the table slot
+    // is rewritten after the barrier that follows its rotation.
+    constexpr int KW = NM / 2 - 1;  // wait for stage s+1 after first-half MFMA KW
+    // operations issued after the awaited ones at that wait: RoPE, after the
+    // table of s+1: x chunks 2-3 of s + lead - 1 and 0-1 of s + lead; else,
+    // after x of s+1: x of s+2 .. s+lead-1 and chunks 0-1 of s + lead
+    constexpr int NWAIT = ROPE ? 4 : (lead - 2) * 4 + 2;
+    for (int s = 0; s + 1 < nst; ++s) {
+      read_frags(f1, s, 1);
+      __builtin_amdgcn_sched_barrier(0);
+      const StageDma d = stage_dma(s + lead);
+      u32x4 x[2], t[2];
+      sy_static_for<NM>([&](auto mc) {
+        constexpr int m = decltype(mc)::value;
+        acc[m] = mma(f0[P::fa(m)], f0[P::fb(m)], acc[m]);
+        if constexpr (m == 0) dma_x(d, I0());
+        if constexpr (m == 2) dma_x(d, I1());
+        if constexpr (m == KW) {
+          sy_wait<NWAIT>();
+          if constexpr (ROPE) {
+            rot_load(s + 1, 0, x[0], t[0]);
+            rot_load(s + 1, 1, x[1], t[1]);
+          }
+        }
+        // rotation: chunk u after MFMA KW + 1 + u, two chunks in flight
+        constexpr int u = m - KW - 1;
+        if constexpr (ROPE && u >= 0 && u < 4) {
+          rot_store(s + 1, u, x[u & 1], t[u & 1]);
+          if constexpr (u + 2 < 4) rot_load(s + 1, u + 2, x[u & 1], t[u & 1]);
+        }
+      });
+      if constexpr (ROPE && NM - KW - 1 < 4) {
+        // fewer MFMAs after the wait than chunks: rotate the rest here
+        sy_static_for<4>([&](auto uc) {
+          constexpr int u = decltype(uc)::value;
+          if constexpr (u >= NM - KW - 1) {
+            rot_store(s + 1, u, x[u & 1], t[u & 1]);
+            if constexpr (u + 2 < 4) rot_load(s + 1, u + 2, x[u & 1], t[u & 1]);
+          }
+        });
       }
+      __builtin_amdgcn_sched_barrier(0);
       sy_barrier();
+      read_frags(f0, s + 1, 0);
+      if constexpr (ROPE) {
+        const StageDma dt = stage_dma(s + 2);
+        sy_static_for<4>([&](auto ic) { dma_t(dt, ic); });
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      sy_static_for<NM>([&](auto mc) {
+        constexpr int m = decltype(mc)::value;
+        acc[m] = mma(f1[P::fa(m)], f1[P::fb(m)], acc[m]);
+        if constexpr (m == 1) dma_x(d, I2());
+        if constexpr (m == 3) dma_x(d, I3());
+      });
     }
+    // last stage: nothing left to load or rotate
+    read_frags(f1, nst - 1, 1);
+    sy_static_for<NM>([&](auto mc) {
+      constexpr int m = decltype(mc)::value;
+      acc[m] = mma(f0[P::fa(m)], f0[P::fb(m)], acc[m]);
+    });
+    sy_static_for<NM>([&](auto mc) {
+      constexpr int m = decltype(mc)::value;
+      acc[m] = mma(f1[P::fa(m)], f1[P::fb(m)], acc[m]);
+    });
+    // the re-loads past the end must land before the workgroup's LDS is freed
+    sy_wait<0>();
 
     // ------------------------------------------------------------ epilogue
-    bf16_t* dst = a.part + (int64_t(slab) * a.ips + itx) * kSyTileElems;
+    if (tile_out < 0) return;
+    bf16_t* dst = a.part + ((int64_t(slab) * a.ntl + tile_out) * S + split) * kSyTileElems;
     // Partial tiles are stored as bf16 (halving their traffic; the scores are
     // bf16 MFMA operands of the score x V product anyway).  Lane pairs swap one
     // value so each lane writes two adjacent columns of one row.
     const bool even = (lane & 1) == 0;
-    auto store_block = [&](const f32x16& c, int rb, int cb) {
+    sy_static_for<NM>([&](auto mc) {
+      constexpr int m = decltype(mc)::value;
+      int rb, cb;
+      if constexpr (WT == 0) {
+        rb = 4 * (w >> 2) + (m >> 1);
+        cb = 2 * (w & 3) + (m & 1);
+      } else {
+        rb = P::bi(m);
+        cb = P::bj(m);
+      }
 #pragma unroll
       for (int r = 0; r < 16; r += 2) {
-        const float send = even ? c[r + 1] : c[r];
+        const float send = even ? acc[m][r + 1] : acc[m][r];
         const float recv = __shfl_xor(send, 1, 64);
         const int row = rb * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3) + (even ? 0 : 1);
         const int col = cb * 32 + ((lane & 31) & ~1);
-        const uint32_t w2 = even ? pack_bf2(c[r], recv) : pack_bf2(recv, c[r + 1]);
+        const uint32_t w2 = even ? pack_bf2(acc[m][r], recv) : pack_bf2(recv, acc[m][r + 1]);
         *reinterpret_cast<uint32_t*>(dst + row * kSyTile + col) = w2;
       }
-    };
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-        if (live(i, j)) store_block(acc[2 * i + j], 4 * wm + i, 2 * wn + j);
+    });
   };
-  using T0 = std::integral_constant<int, 0>;
-  using F = std::integral_constant<bool, false>;
-  using D = std::integral_constant<bool, SELF>;  // diagonal tiles exist only with Q = K
   if (!diag) {
-    run(T0(), F());
+    run(std::integral_constant<int, 0>());
   } else {
-    switch (wtype) {
-      case 0: run(T0(), D()); break;
-      case 1: run(std::integral_constant<int, 1>(), D()); break;
-      case 2: run(std::integral_constant<int, 2>(), D()); break;
-      default: run(std::integral_constant<int, 3>(), D()); break;
+    switch (w & 3) {
+      case 0: run(std::integral_constant<int, 1>()); break;
+      case 1: run(std::integral_constant<int, 2>()); break;
+      case 2: run(std::integral_constant<int, 3>()); break;
+      default: run(std::integral_constant<int, 4>()); break;
     }
   }
 }
@@ -429,34 +543,40 @@ __global__ __launch_bounds__(256) void k_sy_vt(View v, int Hv, int T, int D, int
 }
 
 struct SvArgs {
-  const bf16_t* part;  // partial score tiles [slab][ips][256*256]
+  const bf16_t* part;  // partial score tiles [slab][ntl][nsplit][256*256]
   const bf16_t* vt;    // [B*Hv][D][tp]
-  int ips, sf, sd, H, Hv, T, D, tp;
+  int ntl, nsplit, H, Hv, T, D, tp;
   View o;
 };
 
-// out rows [32 rb, +32) of one (b,h) slab, all D: each wave owns 64 columns
-// (two 32x32 MFMA blocks) and loads its fragments straight from global
-// memory: A = the masked split sum of the partial score rows, B = V^T.  The
-// loads of U k16 steps (every split, predicated) are issued before any of
-// them is used, so a wave keeps U * (NS + 2) loads in flight.
-template <typename TO, int NS, int U>
+// out rows [64 rb, +64) of one (b,h) slab, all D (<= 256) columns.  Keys go
+// in chunks of 64.  The 256 threads first form the chunk's score block in LDS
+// (64 rows x 64 keys: the split sum of the partial rows in fp32, the
+// strict-lower mask, one rounding to bf16), each thread 16 keys of one row,
+// read as two 16-byte loads per split; wave w then multiplies it with V^T
+// columns [64 w, +64): 2 x 2 blocks of 32 x 32, four k16 steps, B fragments
+// straight from V^T.  The partial rows and V^T fragments of the next chunk are
+// loaded before this chunk's MFMAs.  LDS rows are 128 bytes; the 16-byte
+// chunk kc of row r sits at kc ^ ((r >> 1) & 7), so the fragment reads (16
+// rows per pass) and the block writes are bank-conflict free.
+template <typename TO, int NS>
 __global__ __launch_bounds__(256) void k_sy_sv(const SvArgs a) {
+  __shared__ __attribute__((aligned(16))) uint8_t blk[2][64 * 128];
   const int rb = blockIdx.x, slab = blockIdx.y;
   const int b = slab / a.H, h = slab - b * a.H, hv = a.Hv == 1 ? 0 : h;
-  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int row = rb * 32 + (lane & 31);
-  const int kq = (lane >> 5) * 8;
-  const bf16_t* pslab = a.part + int64_t(slab) * a.ips * kSyTileElems;
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  const int r0 = rb * 64;
+  const int kend = min(a.T, r0 + 64);  // keys j < rows of this block
+  const int nch = (kend + 63) / 64;
+  const bf16_t* pslab = a.part + int64_t(slab) * a.ntl * a.nsplit * kSyTileElems;
   const bf16_t* vtb = a.vt + (int64_t(b) * a.Hv + hv) * a.D * a.tp;
-  f32x16 acc[2];
-#pragma unroll
-  for (int c = 0; c < 2; ++c)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) acc[c][r] = 0.f;
-  const int ti = min(row, a.T - 1) >> 8;
-  const int kend = min(a.T, (rb + 1) * 32);  // keys j < rows of this block
-  const bool lastrow_ok = row < a.T;
+
+  // block builder: row lr, keys [lk, +16) of the chunk
+  const int lr = tid >> 2, lk = (tid & 3) * 16;
+  const int gi = r0 + lr;
+  const int ti = min(gi, a.T - 1) >> 8;
+  const bool row_ok = gi < a.T;
+  // MFMA roles: output columns d = 64 w + 32 c + lane % 32
   int dcol[2];
   bool dok[2];
 #pragma unroll
@@ -464,93 +584,136 @@ __global__ __launch_bounds__(256) void k_sy_sv(const SvArgs a) {
     dcol[c] = 64 * w + 32 * c + (lane & 31);
     dok[c] = dcol[c] < a.D;
   }
-  for (int k0 = 0; k0 < kend; k0 += 16 * U) {
-    uint4 ra[U][NS];
-    bf16x8 rb2[U][2];
+
+  uint4 pr[NS][2];       // partial rows of the next chunk
+  bf16x8 vb[2][4];       // V^T fragments of the next chunk [c][k16 step]
+  auto load_chunk = [&](int ck) {
+    const int j0 = ck * 64;
+    const int tile = ti * (ti + 1) / 2 + (j0 >> 8);
+    const bf16_t* p = pslab + int64_t(tile) * a.nsplit * kSyTileElems + (gi & 255) * kSyTile + ((j0 + lk) & 255);
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int j = k0 + 16 * u + kq;
-      const bool in = k0 + 16 * u < kend;
-      const bool av = in && lastrow_ok && j < row;
-      const int tj = j >> 8;
-      const int first = a.sf * (ti * (ti - 1) / 2 + tj) + a.sd * ti;
-      const int ns = ti == tj ? a.sd : a.sf;
-      const bf16_t* p = pslab + int64_t(first) * kSyTileElems + (row & 255) * kSyTile + (j & 255);
+    for (int sp = 0; sp < NS; ++sp)
 #pragma unroll
-      for (int sp = 0; sp < NS; ++sp)
-        ra[u][sp] = (av && sp < ns) ? *reinterpret_cast<const uint4*>(p + int64_t(sp) * kSyTileElems)
-                                    : uint4{0u, 0u, 0u, 0u};
+      for (int e = 0; e < 2; ++e)
+        pr[sp][e] = sp < a.nsplit ? *reinterpret_cast<const uint4*>(p + int64_t(sp) * kSyTileElems + 8 * e)
+                                  : uint4{0u, 0u, 0u, 0u};
 #pragma unroll
-      for (int c = 0; c < 2; ++c)
-        rb2[u][c] = (in && dok[c]) ? *reinterpret_cast<const bf16x8*>(vtb + int64_t(dcol[c]) * a.tp + j)
-                                   : __builtin_bit_cast(bf16x8, u32x4{0u, 0u, 0u, 0u});
-    }
+    for (int c = 0; c < 2; ++c)
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      if (k0 + 16 * u >= kend) break;
-      const int j = k0 + 16 * u + kq;
+      for (int ks = 0; ks < 4; ++ks) {
+        const int j = j0 + 16 * ks + 8 * (lane >> 5);
+        vb[c][ks] = (dok[c] && j < kend) ? *reinterpret_cast<const bf16x8*>(vtb + int64_t(dcol[c]) * a.tp + j)
+                                         : __builtin_bit_cast(bf16x8, u32x4{0u, 0u, 0u, 0u});
+      }
+  };
+  // split sum, mask (j < i, j < T), one rounding; two 16-byte LDS writes
+  auto build = [&](int ck, uint8_t* dst) {
+    const int j0 = ck * 64 + lk;
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
       float sacc[8];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) sacc[e] = 0.f;
+      for (int q = 0; q < 8; ++q) sacc[q] = 0.f;
 #pragma unroll
       for (int sp = 0; sp < NS; ++sp) {
-        const uint32_t xw[4] = {ra[u][sp].x, ra[u][sp].y, ra[u][sp].z, ra[u][sp].w};
+        const uint32_t xw[4] = {pr[sp][e].x, pr[sp][e].y, pr[sp][e].z, pr[sp][e].w};
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          sacc[2 * e] += __uint_as_float(xw[e] << 16);
-          sacc[2 * e + 1] += __uint_as_float(xw[e] & 0xffff0000u);
+        for (int q = 0; q < 4; ++q) {
+          sacc[2 * q] += __uint_as_float(xw[q] << 16);
+          sacc[2 * q + 1] += __uint_as_float(xw[q] & 0xffff0000u);
         }
       }
       uint32_t pk[4];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float lo = (j + 2 * e < row) ? sacc[2 * e] : 0.f;
-        const float hi = (j + 2 * e + 1 < row) ? sacc[2 * e + 1] : 0.f;
-        pk[e] = pack_bf2(lo, hi);
+      for (int q = 0; q < 4; ++q) {
+        const int j = j0 + 8 * e + 2 * q;
+        const float lo = (row_ok && j < gi) ? sacc[2 * q] : 0.f;
+        const float hi = (row_ok && j + 1 < gi) ? sacc[2 * q + 1] : 0.f;
+        pk[q] = pack_bf2(lo, hi);
       }
-      const bf16x8 fa = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(pk));
+      const int kc = (lk >> 3) + e;
+      *reinterpret_cast<u32x4*>(dst + lr * 128 + ((kc ^ ((lr >> 1) & 7)) * 16)) = u32x4{pk[0], pk[1], pk[2], pk[3]};
+    }
+  };
+
+  f32x16 acc[2][2];
 #pragma unroll
-      for (int c = 0; c < 2; ++c) acc[c] = mma(fa, rb2[u][c], acc[c]);
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][c][r] = 0.f;
+
+  load_chunk(0);
+  for (int ck = 0; ck < nch; ++ck) {
+    uint8_t* buf = blk[ck & 1];
+    build(ck, buf);
+    bf16x8 vcur[2][4];
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) vcur[c][ks] = vb[c][ks];
+    if (ck + 1 < nch) load_chunk(ck + 1);
+    // chunk ck's block is complete; buffer (ck+1) & 1 was last read before it
+    __syncthreads();
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      bf16x8 fa[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int row = 32 * i + (lane & 31);
+        const int kc = 2 * ks + (lane >> 5);
+        fa[i] = *reinterpret_cast<const bf16x8*>(buf + row * 128 + ((kc ^ ((row >> 1) & 7)) * 16));
+      }
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int c = 0; c < 2; ++c) acc[i][c] = mma(fa[i], vcur[c][ks], acc[i][c]);
     }
   }
   TO* o = static_cast<TO*>(const_cast<void*>(a.o.p)) + b * a.o.s0 + h * a.o.s1;
 #pragma unroll
-  for (int c = 0; c < 2; ++c)
+  for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int i = rb * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-      if (i < a.T && dok[c]) o[int64_t(i) * a.o.s2 + dcol[c]] = from_f<TO>(acc[c][r]);
-    }
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = r0 + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        if (row < a.T && dok[c]) o[int64_t(row) * a.o.s2 + dcol[c]] = from_f<TO>(acc[i][c][r]);
+      }
 }
 
 template <typename TO>
 int launch_sy_sv(const SvArgs& sa, dim3 grid, hipStream_t s) {
-  const int ns = std::max(sa.sf, sa.sd);
+  const int ns = sa.nsplit;
   if (ns <= 2)
-    BDH_LAUNCH("k_sy_sv", (k_sy_sv<TO, 2, 4>), grid, dim3(256), 0, s, sa);
+    BDH_LAUNCH("k_sy_sv", (k_sy_sv<TO, 2>), grid, dim3(256), 0, s, sa);
   else if (ns <= 4)
-    BDH_LAUNCH("k_sy_sv", (k_sy_sv<TO, 4, 4>), grid, dim3(256), 0, s, sa);
+    BDH_LAUNCH("k_sy_sv", (k_sy_sv<TO, 4>), grid, dim3(256), 0, s, sa);
   else
-    BDH_LAUNCH("k_sy_sv", (k_sy_sv<TO, 8, 2>), grid, dim3(256), 0, s, sa);
+    BDH_LAUNCH("k_sy_sv", (k_sy_sv<TO, 8>), grid, dim3(256), 0, s, sa);
   return BDH_OK;
 }
 
 // ---------------------------------------------------------------- host plan
-// Table rows are padded by 256 bytes so the rows one DMA instruction reads
-// (same pair offset, consecutive positions) fall on different L2 channels.
-inline int sy_table_pitch(int64_t N) { return int(N / 2) + 64; }
 // V^T rows hold the positions padded to a multiple of 32 (zeros beyond T).
 inline int sy_vt_pitch(int64_t T) { return int((T + 31) / 32 * 32); }
 
 struct SyPlan {
-  int nt = 0, ntl = 0, ips = 0, nchunk = 0, sf = 1, sd = 1;
+  int nt = 0, ntl = 0, ips = 0, nchunk = 0, nsplit = 1;
   size_t table_bytes = 0, part_bytes = 0, vt_bytes = 0, ws_bytes = 0;
   uint32_t items[kSyMaxItems];
   bool ok = false;
 };
 
-// Split factors: the smallest full-tile split that gives every CU a work item,
-// diagonal tiles (36/64 of a full tile's MFMAs when Q = K) split in proportion.
+// Work items of one (b, h) slab: with Q = K the full tiles below the diagonal
+// plus the diagonal tiles in pairs (each pair costs about one full tile and
+// loads two row blocks, like a full tile), else every lower tile in full.
+// Every item of a slab runs the same split count, so all items have the same
+// number of stages and walk k in step: a full tile and the diagonal pair of
+// the same two row blocks then load the same bytes at the same time and the
+// second load is served by the XCD's L2.  The split count is the smallest
+// that gives every CU a work item.
 SyPlan sy_plan(int64_t nslab, int64_t T, int64_t N, bool self, bool rope, int64_t Dv = 0) {
   SyPlan p;
   if (T <= 0 || N <= 0 || N % 64 != 0 || nslab <= 0) return p;
@@ -558,30 +721,29 @@ SyPlan sy_plan(int64_t nslab, int64_t T, int64_t N, bool self, bool rope, int64_
   p.ntl = p.nt * (p.nt + 1) / 2;
   p.nchunk = int(N / 64);
   if (p.ntl > kSyMaxTiles) return p;
-  const int nfull = p.ntl - p.nt, ndiag = p.nt;
-  int sf = 1, sd = 1;
-  for (sf = 1; sf <= 8; ++sf) {
-    sd = self ? std::max(1, (sf * 36 + 32) / 64) : sf;
-    if (nslab * (nfull * sf + ndiag * sd) >= 256) break;
-  }
-  if (sf > 8) sf = 8;
-  sf = std::min(sf, p.nchunk);
-  sd = std::min(sd, p.nchunk);
-  p.sf = sf;
-  p.sd = sd;
+  const int per_split = self ? (p.ntl - p.nt) + (p.nt + 1) / 2 : p.ntl;
+  // one item per CU if that takes at most 8 splits, else the fewest that fill
+  // every CU once
+  const int64_t per_pass = nslab * per_split;
+  int S = int(std::max<int64_t>(1, std::min<int64_t>(8, 256 / per_pass)));
+  S = std::min(S, p.nchunk);
+  if (per_split * S > kSyMaxItems) return p;
+  p.nsplit = S;
   int n = 0;
-  for (int ti = 0; ti < p.nt; ++ti)
-    for (int tj = 0; tj <= ti; ++tj) {
-      const int t = ti * (ti + 1) / 2 + tj;
-      const int ns = (ti == tj) ? sd : sf;
-      if (n + ns > kSyMaxItems) return p;
-      (void)t;
-      for (int s = 0; s < ns; ++s)
-        p.items[n++] = uint32_t(ti) | (uint32_t(tj) << 8) | (uint32_t(s) << 16) | (uint32_t(ns) << 24);
+  auto add = [&](int ta, int tb, int sp, int kind) {
+    p.items[n++] = uint32_t(ta) | (uint32_t(tb) << 8) | (uint32_t(sp) << 16) | (uint32_t(kind) << 24);
+  };
+  for (int sp = 0; sp < S; ++sp) {
+    for (int ti = 0; ti < p.nt; ++ti)
+      for (int tj = 0; tj < ti + (self ? 0 : 1); ++tj) add(ti, tj, sp, kSyFull);
+    if (self) {
+      for (int t = 0; t + 1 < p.nt; t += 2) add(t, t + 1, sp, kSyDiag2);
+      if (p.nt % 2) add(p.nt - 1, p.nt - 1, sp, kSyDiag1);
     }
+  }
   p.ips = n;
-  p.table_bytes = rope ? align_up(size_t(T) * size_t(sy_table_pitch(N)) * 4, 256) : 0;
-  p.part_bytes = size_t(nslab) * size_t(p.ips) * kSyTileElems * sizeof(bf16_t);
+  p.table_bytes = rope ? align_up(size_t(T) * size_t(N / 2) * 4, 256) : 0;
+  p.part_bytes = size_t(nslab) * size_t(p.ntl) * size_t(S) * kSyTileElems * sizeof(bf16_t);
   // V^T for the score x V product: at most one copy per (b, h) slab
   p.vt_bytes = align_up(size_t(nslab) * size_t(Dv) * size_t(sy_vt_pitch(T)) * sizeof(bf16_t), 256);
   p.ws_bytes = p.table_bytes + p.part_bytes + p.vt_bytes;
@@ -624,7 +786,7 @@ int sy_cold(const bdh_tensor4* q, const bdh_tensor4* k, const bdh_tensor4* v, co
   if (T < 1 || N < 64 || N % 64 != 0 || !rows16(q) || !rows16(k)) return kNotEligible;
   if (v->size[3] > 256) return kNotEligible;  // score x V: four waves x 64 columns
   if (((T - 1) * std::max(q->stride[2], k->stride[2]) + N) * 2 >= (int64_t(1) << 31)) return kNotEligible;
-  if (rope && int64_t(T) * sy_table_pitch(N) * 4 >= (int64_t(1) << 31)) return kNotEligible;
+  if (rope && int64_t(T) * N * 2 >= (int64_t(1) << 31)) return kNotEligible;
   if (T > 65535) return kNotEligible;
   if (qr != nullptr && (qr->dtype != BDH_BF16 || !rows16(qr))) return kNotEligible;
   const int64_t nslab = B * H;
@@ -639,10 +801,9 @@ int sy_cold(const bdh_tensor4* q, const bdh_tensor4* k, const bdh_tensor4* v, co
   uint8_t* wsb = static_cast<uint8_t*>(ws);
   uint32_t* table = rope ? reinterpret_cast<uint32_t*>(wsb) : nullptr;
   bf16_t* part = reinterpret_cast<bf16_t*>(wsb + p.table_bytes);
-  const int tpitch = sy_table_pitch(N);
   if (rope) {
     BDH_LAUNCH("k_rope_table", k_rope_table, dim3(unsigned((N / 2 + 255) / 256), unsigned(T)), dim3(256), 0, s,
-               freqs, rope_start, int(N / 2), tpitch, table);
+               freqs, rope_start, int(N / 2), int(T), table);
   }
   SyArgs a;
   a.q = static_cast<const bf16_t*>(q->data);
@@ -659,8 +820,9 @@ int sy_cold(const bdh_tensor4* q, const bdh_tensor4* k, const bdh_tensor4* v, co
   a.nslab = int(nslab);
   a.ips = p.ips;
   a.nchunk = p.nchunk;
+  a.nsplit = p.nsplit;
+  a.ntl = p.ntl;
   a.cs = table;
-  a.tpitch = tpitch;
   a.part = part;
   a.qr = nullptr;
   a.r0 = a.r1 = a.r2 = 0;
@@ -697,9 +859,8 @@ int sy_cold(const bdh_tensor4* q, const bdh_tensor4* k, const bdh_tensor4* v, co
   SvArgs sa;
   sa.part = part;
   sa.vt = vt;
-  sa.ips = p.ips;
-  sa.sf = p.sf;
-  sa.sd = p.sd;
+  sa.ntl = p.ntl;
+  sa.nsplit = p.nsplit;
   sa.H = int(H);
   sa.Hv = Hv;
   sa.T = int(T);
@@ -707,7 +868,7 @@ int sy_cold(const bdh_tensor4* q, const bdh_tensor4* k, const bdh_tensor4* v, co
   sa.tp = tp;
   sa.o = view_of(out);
   sa.o.s1 = out->stride[1];
-  const dim3 gsv(unsigned((T + 31) / 32), unsigned(nslab));
+  const dim3 gsv(unsigned((T + 63) / 64), unsigned(nslab));
   return out->dtype == BDH_BF16 ? launch_sy_sv<bf16_t>(sa, gsv, s) : launch_sy_sv<float>(sa, gsv, s);
 }
 
