@@ -91,6 +91,84 @@ __global__ __launch_bounds__(kDecNT) void k_decode_partial(DecodeArgs a) {
   }
 }
 
+// bf16 q and K_past (the cache path): q is staged once as bf16 (16 KB at
+// N = 8192); each wave scores two key rows at a time with eight 16-byte loads
+// in flight per lane, accumulating v_dot2_f32_bf16 (exact bf16 products, fp32
+// sums) against the staged q; then the 256 threads form the chunk's partial
+// out[d] = sum_s score_s V[s,d].  Needs Dk a multiple of 2048.
+constexpr int kDecChunkB = 64;  // keys per workgroup
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+// (The dwords are copied to scalars before the bit cast: this clang lowers
+// __builtin_bit_cast of a vector element such as k.y as element 0.)
+__device__ __forceinline__ float dot2w(uint32_t k, uint32_t q, float acc) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, k), __builtin_bit_cast(bf16x2, q), acc, false);
+}
+__device__ __forceinline__ float dot8(u32x4 k, u32x4 q, float acc) {
+  const uint32_t k0 = k.x, k1 = k.y, k2 = k.z, k3 = k.w;
+  const uint32_t q0 = q.x, q1 = q.y, q2 = q.z, q3 = q.w;
+  acc = dot2w(k0, q0, acc);
+  acc = dot2w(k1, q1, acc);
+  acc = dot2w(k2, q2, acc);
+  return dot2w(k3, q3, acc);
+}
+
+template <typename TV>
+__global__ __launch_bounds__(kDecNT) void k_decode_bf16(DecodeArgs a) {
+  extern __shared__ float smem[];
+  float* sc = smem;                                         // kDecChunkB scores
+  u32x4* qs = reinterpret_cast<u32x4*>(smem + kDecChunkB);  // q as Dk / 8 chunks of 8 bf16
+  const int64_t row = blockIdx.y;
+  const int64_t t = row % a.Tq, bh = row / a.Tq;
+  const int64_t h = bh % a.H, b = bh / a.H;
+  const int64_t hv = a.Hv == 1 ? 0 : h;
+  const bf16_t* qp = static_cast<const bf16_t*>(a.q.p) + b * a.q.s0 + h * a.q.s1 + t * a.q.s2;
+  for (int64_t i = threadIdx.x; i < a.Dk / 8; i += kDecNT) qs[i] = *reinterpret_cast<const u32x4*>(qp + 8 * i);
+  __syncthreads();
+
+  const int64_t s0 = int64_t(blockIdx.x) * kDecChunkB;
+  const int64_t s1 = min(a.S, s0 + kDecChunkB);
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const bf16_t* kb = static_cast<const bf16_t*>(a.k.p) + b * a.k.s0 + h * a.k.s1;
+  const int nc = int(a.Dk / 512);  // 16-byte chunks per lane per key row
+  // keys s0 + wave + 4 j of this wave, in pairs (s, s + 4)
+  for (int64_t s = s0 + wave; s < s1; s += 8) {
+    const bool two = s + 4 < s1;
+    const bf16_t* k0 = kb + s * a.k.s2 + lane * 8;
+    const bf16_t* k1 = kb + (two ? s + 4 : s) * a.k.s2 + lane * 8;
+    float acc0 = 0.f, acc1 = 0.f;
+    for (int c = 0; c < nc; c += 4) {
+      u32x4 x0[4], x1[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        x0[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(k0 + (c + u) * 512));
+        x1[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(k1 + (c + u) * 512));
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const u32x4 q = qs[(c + u) * 64 + lane];
+        acc0 = dot8(x0[u], q, acc0);
+        acc1 = dot8(x1[u], q, acc1);
+      }
+    }
+    acc0 = wave_sum(acc0);
+    acc1 = wave_sum(acc1);
+    if (lane == 0) {
+      sc[s - s0] = acc0;
+      if (two) sc[s + 4 - s0] = acc1;
+    }
+  }
+  __syncthreads();
+
+  const TV* vb = static_cast<const TV*>(a.v.p) + b * a.v.s0 + hv * a.v.s1;
+  float* out = a.part + (int64_t(blockIdx.x) * a.rows + row) * a.Dv;
+  for (int64_t d = threadIdx.x; d < a.Dv; d += kDecNT) {
+    float o = 0.f;
+    for (int64_t s = s0; s < s1; ++s) o += sc[s - s0] * to_f(vb[s * a.v.s2 + d]);
+    out[d] = o;
+  }
+}
+
 template <typename TO>
 __global__ __launch_bounds__(kDecNT) void k_decode_reduce(const float* part, int64_t nchunk, int64_t rows,
                                                           int64_t Dv, View o, int64_t H, int64_t Tq) {
@@ -174,19 +252,34 @@ extern "C" int bdh_tril_decode(const bdh_tensor4* q, const bdh_tensor4* k, const
   a.vec_k = vec16_ok(k) ? 1 : 0;
   a.part = static_cast<float*>(workspace);
   a.rows = B * H * Tq;
-  const int rc = q->dtype == BDH_BF16 ? pick_k<bf16_t>(a, nchunk, k->dtype, v->dtype, st)
-                                      : pick_k<float>(a, nchunk, k->dtype, v->dtype, st);
-  if (rc != BDH_OK) return rc;
+  // bf16 cache path: fewer, larger key chunks (the workspace for kChunk-key
+  // chunks covers them)
+  const bool fast = q->dtype == BDH_BF16 && k->dtype == BDH_BF16 && vec16_ok(q) && vec16_ok(k) &&
+                    Dk % 2048 == 0 && Dk * 2 + kDecChunkB * 4 <= 64 * 1024 && S > 0;
+  int64_t nred = nchunk;
+  if (fast) {
+    nred = (S + kDecChunkB - 1) / kDecChunkB;
+    const dim3 grid((unsigned)nred, unsigned(a.rows));
+    const size_t shm = size_t(kDecChunkB) * sizeof(float) + size_t(Dk) * 2;
+    if (v->dtype == BDH_BF16)
+      BDH_LAUNCH("k_decode_bf16", k_decode_bf16<bf16_t>, grid, dim3(kDecNT), shm, st, a);
+    else
+      BDH_LAUNCH("k_decode_bf16", k_decode_bf16<float>, grid, dim3(kDecNT), shm, st, a);
+  } else {
+    const int rc = q->dtype == BDH_BF16 ? pick_k<bf16_t>(a, nchunk, k->dtype, v->dtype, st)
+                                        : pick_k<float>(a, nchunk, k->dtype, v->dtype, st);
+    if (rc != BDH_OK) return rc;
+  }
 
   View o = view_of(out);
   o.s1 = out->stride[1];
   const int64_t total = a.rows * Dv;
   dim3 grid((unsigned)((total + kDecNT - 1) / kDecNT));
   if (out->dtype == BDH_BF16)
-    BDH_LAUNCH("k_decode_reduce", k_decode_reduce<bf16_t>, grid, dim3(kDecNT), 0, st, a.part, nchunk,
+    BDH_LAUNCH("k_decode_reduce", k_decode_reduce<bf16_t>, grid, dim3(kDecNT), 0, st, a.part, nred,
                a.rows, Dv, o, H, Tq);
   else
-    BDH_LAUNCH("k_decode_reduce", k_decode_reduce<float>, grid, dim3(kDecNT), 0, st, a.part, nchunk,
+    BDH_LAUNCH("k_decode_reduce", k_decode_reduce<float>, grid, dim3(kDecNT), 0, st, a.part, nred,
                a.rows, Dv, o, H, Tq);
   return BDH_OK;
 }

@@ -17,6 +17,8 @@ struct RopeArgs {
   int64_t H, T, N;
   int64_t pairs;  // rows * N / 2
   int bwd;
+  int vec8;       // every view 16-byte aligned per 8 elements (k_rope8)
+  int64_t BH;     // B * H
 };
 
 template <typename TV, typename TC, typename TO>
@@ -58,8 +60,90 @@ __global__ __launch_bounds__(256) void k_rope(RopeArgs a) {
   op[1] = from_f<TO>(y1);
 }
 
+// The same rotation, eight elements (four pairs) per thread with 16-byte
+// accesses: grid (N / 2048, T, B * H), so no per-thread index division.
+template <typename T>
+struct Vec8 {
+  T e[8];
+};
+template <typename T>
+__device__ __forceinline__ Vec8<T> load8(const T* p) {
+  Vec8<T> r;
+  if constexpr (sizeof(T) == 2) {
+    *reinterpret_cast<u32x4*>(r.e) = *reinterpret_cast<const u32x4*>(p);
+  } else {
+    reinterpret_cast<u32x4*>(r.e)[0] = reinterpret_cast<const u32x4*>(p)[0];
+    reinterpret_cast<u32x4*>(r.e)[1] = reinterpret_cast<const u32x4*>(p)[1];
+  }
+  return r;
+}
+template <typename T>
+__device__ __forceinline__ void store8(T* p, const Vec8<T>& r) {
+  if constexpr (sizeof(T) == 2) {
+    *reinterpret_cast<u32x4*>(p) = *reinterpret_cast<const u32x4*>(r.e);
+  } else {
+    reinterpret_cast<u32x4*>(p)[0] = reinterpret_cast<const u32x4*>(r.e)[0];
+    reinterpret_cast<u32x4*>(p)[1] = reinterpret_cast<const u32x4*>(r.e)[1];
+  }
+}
+
+template <typename TV, typename TC, typename TO>
+__global__ __launch_bounds__(256) void k_rope8(RopeArgs a) {
+#pragma clang fp contract(off)
+  const int64_t e0 = (int64_t(blockIdx.x) * 256 + threadIdx.x) * 8;
+  if (e0 >= a.N) return;
+  const int64_t t = blockIdx.y, bh = blockIdx.z;
+  const int64_t h = bh % a.H, b = bh / a.H;
+  const Vec8<TV> x = load8(static_cast<const TV*>(a.v.p) + b * a.v.s0 + h * a.v.s1 + t * a.v.s2 + e0);
+  const Vec8<TC> c = load8(static_cast<const TC*>(a.c.p) + b * a.c.s0 + h * a.c.s1 + t * a.c.s2 + e0);
+  const Vec8<TC> sn = load8(static_cast<const TC*>(a.s.p) + b * a.s.s0 + h * a.s.s1 + t * a.s.s2 + e0);
+  Vec8<TO> y;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const float x0 = to_f(x.e[2 * q]), x1 = to_f(x.e[2 * q + 1]);
+    const float c0 = to_f(c.e[2 * q]), c1 = to_f(c.e[2 * q + 1]);
+    const float s0 = to_f(sn.e[2 * q]), s1 = to_f(sn.e[2 * q + 1]);
+    float y0, y1;
+    if constexpr (std::is_same<TV, bf16_t>::value) {
+      if (a.bwd) {
+        y0 = bf_round(bf_round(x0 * c0) + bf_round(x1 * s1));
+        y1 = bf_round(bf_round((-x0) * s0) + bf_round(x1 * c1));
+      } else {
+        y0 = bf_round(bf_round(x0 * c0) + bf_round((-x1) * s0));
+        y1 = bf_round(bf_round(x1 * c1) + bf_round(x0 * s1));
+      }
+    } else {
+      if (a.bwd) {
+        const float p0 = x0 * c0, p1 = x1 * s1, p2 = x0 * s0, p3 = x1 * c1;
+        y0 = p0 + p1;
+        y1 = -p2 + p3;
+      } else {
+        const float p0 = x0 * c0, p1 = x1 * s0, p2 = x1 * c1, p3 = x0 * s1;
+        y0 = p0 - p1;
+        y1 = p2 + p3;
+      }
+    }
+    y.e[2 * q] = from_f<TO>(y0);
+    y.e[2 * q + 1] = from_f<TO>(y1);
+  }
+  store8(static_cast<TO*>(const_cast<void*>(a.o.p)) + b * a.o.s0 + h * a.o.s1 + t * a.o.s2 + e0, y);
+}
+
+// 16-byte alignment of every 8-element group of a view
+static bool vec8_ok(const bdh_tensor4* t) {
+  if ((reinterpret_cast<uintptr_t>(t->data) & 15) != 0) return false;
+  for (int i = 0; i < 3; ++i)
+    if (t->size[i] > 1 && (t->stride[i] % 8) != 0) return false;
+  return t->size[3] % 8 == 0;
+}
+
 template <typename TV, typename TC, typename TO>
 static int launch_rope(const RopeArgs& a, hipStream_t s) {
+  if (a.vec8) {
+    dim3 grid((unsigned)((a.N + 2047) / 2048), (unsigned)a.T, (unsigned)a.BH);
+    BDH_LAUNCH("k_rope", (k_rope8<TV, TC, TO>), grid, dim3(256), 0, s, a);
+    return BDH_OK;
+  }
   dim3 grid((unsigned)((a.pairs + 255) / 256));
   BDH_LAUNCH("k_rope", (k_rope<TV, TC, TO>), grid, dim3(256), 0, s, a);
   return BDH_OK;
@@ -111,6 +195,8 @@ extern "C" int bdh_rope_rotate(const bdh_tensor4* v, const bdh_tensor4* cos, con
   a.N = v->size[3];
   a.pairs = v->size[0] * v->size[1] * v->size[2] * (v->size[3] / 2);
   a.bwd = backward != 0;
+  a.BH = v->size[0] * v->size[1];
+  a.vec8 = vec8_ok(v) && vec8_ok(cos) && vec8_ok(sin) && vec8_ok(out) && a.T <= 65535 && a.BH <= 65535;
   hipStream_t s = static_cast<hipStream_t>(stream);
   return v->dtype == BDH_BF16 ? pick_c<bf16_t>(a, cos->dtype, out->dtype, s)
                               : pick_c<float>(a, cos->dtype, out->dtype, s);
