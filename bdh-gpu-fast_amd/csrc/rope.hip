@@ -19,6 +19,7 @@ struct RopeArgs {
   int bwd;
   int vec8;       // every view 16-byte aligned per 8 elements (k_rope8)
   int64_t BH;     // B * H
+  int bcast;      // cos/sin do not vary over batch and heads (k_rope8_bc)
 };
 
 template <typename TV, typename TC, typename TO>
@@ -129,6 +130,76 @@ __global__ __launch_bounds__(256) void k_rope8(RopeArgs a) {
   store8(static_cast<TO*>(const_cast<void*>(a.o.p)) + b * a.o.s0 + h * a.o.s1 + t * a.o.s2 + e0, y);
 }
 
+// Tables broadcast over batch and heads (the model's case): grid (N / 2048,
+// T); each thread loads its cos/sin once and walks the B * H rows, four in
+// flight, so the tables are read once instead of once per (b, h).
+template <typename TV, typename TC, typename TO>
+__global__ __launch_bounds__(256) void k_rope8_bc(RopeArgs a) {
+#pragma clang fp contract(off)
+  const int64_t e0 = (int64_t(blockIdx.x) * 256 + threadIdx.x) * 8;
+  if (e0 >= a.N) return;
+  const int64_t t = blockIdx.y;
+  const Vec8<TC> c = load8(static_cast<const TC*>(a.c.p) + t * a.c.s2 + e0);
+  const Vec8<TC> sn = load8(static_cast<const TC*>(a.s.p) + t * a.s.s2 + e0);
+  float cf[8], sf[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    cf[e] = to_f(c.e[e]);
+    sf[e] = to_f(sn.e[e]);
+  }
+  auto rot = [&](const Vec8<TV>& x) {
+    Vec8<TO> y;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const float x0 = to_f(x.e[2 * q]), x1 = to_f(x.e[2 * q + 1]);
+      const float c0 = cf[2 * q], c1 = cf[2 * q + 1], s0 = sf[2 * q], s1 = sf[2 * q + 1];
+      float y0, y1;
+      if constexpr (std::is_same<TV, bf16_t>::value) {
+        if (a.bwd) {
+          y0 = bf_round(bf_round(x0 * c0) + bf_round(x1 * s1));
+          y1 = bf_round(bf_round((-x0) * s0) + bf_round(x1 * c1));
+        } else {
+          y0 = bf_round(bf_round(x0 * c0) + bf_round((-x1) * s0));
+          y1 = bf_round(bf_round(x1 * c1) + bf_round(x0 * s1));
+        }
+      } else {
+        if (a.bwd) {
+          const float p0 = x0 * c0, p1 = x1 * s1, p2 = x0 * s0, p3 = x1 * c1;
+          y0 = p0 + p1;
+          y1 = -p2 + p3;
+        } else {
+          const float p0 = x0 * c0, p1 = x1 * s0, p2 = x1 * c1, p3 = x0 * s1;
+          y0 = p0 - p1;
+          y1 = p2 + p3;
+        }
+      }
+      y.e[2 * q] = from_f<TO>(y0);
+      y.e[2 * q + 1] = from_f<TO>(y1);
+    }
+    return y;
+  };
+  const TV* vp = static_cast<const TV*>(a.v.p) + t * a.v.s2 + e0;
+  TO* op = static_cast<TO*>(const_cast<void*>(a.o.p)) + t * a.o.s2 + e0;
+  int64_t bh = 0;
+  for (; bh + 4 <= a.BH; bh += 4) {
+    Vec8<TV> x[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int64_t r = bh + u, h = r % a.H, b = r / a.H;
+      x[u] = load8(vp + b * a.v.s0 + h * a.v.s1);
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int64_t r = bh + u, h = r % a.H, b = r / a.H;
+      store8(op + b * a.o.s0 + h * a.o.s1, rot(x[u]));
+    }
+  }
+  for (; bh < a.BH; ++bh) {
+    const int64_t h = bh % a.H, b = bh / a.H;
+    store8(op + b * a.o.s0 + h * a.o.s1, rot(load8(vp + b * a.v.s0 + h * a.v.s1)));
+  }
+}
+
 // 16-byte alignment of every 8-element group of a view
 static bool vec8_ok(const bdh_tensor4* t) {
   if ((reinterpret_cast<uintptr_t>(t->data) & 15) != 0) return false;
@@ -139,6 +210,11 @@ static bool vec8_ok(const bdh_tensor4* t) {
 
 template <typename TV, typename TC, typename TO>
 static int launch_rope(const RopeArgs& a, hipStream_t s) {
+  if (a.vec8 && a.bcast) {
+    dim3 grid((unsigned)((a.N + 2047) / 2048), (unsigned)a.T);
+    BDH_LAUNCH("k_rope", (k_rope8_bc<TV, TC, TO>), grid, dim3(256), 0, s, a);
+    return BDH_OK;
+  }
   if (a.vec8) {
     dim3 grid((unsigned)((a.N + 2047) / 2048), (unsigned)a.T, (unsigned)a.BH);
     BDH_LAUNCH("k_rope", (k_rope8<TV, TC, TO>), grid, dim3(256), 0, s, a);
@@ -197,6 +273,10 @@ extern "C" int bdh_rope_rotate(const bdh_tensor4* v, const bdh_tensor4* cos, con
   a.bwd = backward != 0;
   a.BH = v->size[0] * v->size[1];
   a.vec8 = vec8_ok(v) && vec8_ok(cos) && vec8_ok(sin) && vec8_ok(out) && a.T <= 65535 && a.BH <= 65535;
+  auto flat = [](const bdh_tensor4* t) {
+    return (t->size[0] <= 1 || t->stride[0] == 0) && (t->size[1] <= 1 || t->stride[1] == 0);
+  };
+  a.bcast = flat(cos) && flat(sin);
   hipStream_t s = static_cast<hipStream_t>(stream);
   return v->dtype == BDH_BF16 ? pick_c<bf16_t>(a, cos->dtype, out->dtype, s)
                               : pick_c<float>(a, cos->dtype, out->dtype, s);

@@ -171,6 +171,34 @@ def test_rope_apply_is_bit_exact(vdt, odt, backward):
     assert np.array_equal(np_of(got), want)
 
 
+@pytest.mark.parametrize("layout", ["per_head_tables", "narrow_rows", "permuted_view"])
+@pytest.mark.parametrize("vdt", [torch.float32, torch.bfloat16])
+def test_rope_apply_paths_are_bit_exact(layout, vdt):
+    """Each kernel variant against the oracle's rounding: tables that vary per
+    (b, h) (8-wide path without the broadcast), N not a multiple of 8 (scalar
+    path) and the permuted x_sparse view with broadcast tables."""
+    B, H, T = 2, 3, 17
+    N = 12 if layout == "narrow_rows" else 64
+    c, s = O.rope_cos_sin(T, 5, O.get_freqs(N))
+    if layout == "per_head_tables":
+        scale = (1.0 + 0.01 * np.arange(B * H, dtype=np.float32)).reshape(B, H, 1, 1)
+        c4, s4 = (c.reshape(1, 1, T, N) * scale).astype(np.float32), (s.reshape(1, 1, T, N) * scale).astype(np.float32)
+    else:
+        c4, s4 = np.broadcast_to(c.reshape(1, 1, T, N), (B, H, T, N)), np.broadcast_to(s.reshape(1, 1, T, N), (B, H, T, N))
+    x = as_dtype_values(normal((B, T, H, N) if layout == "permuted_view" else (B, H, T, N), 8), vdt)
+    xv = np.ascontiguousarray(x.transpose(0, 2, 1, 3)) if layout == "permuted_view" else x
+    want = O.rope_rotate(xv, c4, s4, bf16=(vdt == torch.bfloat16))
+    xd = to_dev(x, vdt)
+    xd = xd.permute(0, 2, 1, 3) if layout == "permuted_view" else xd
+    if layout == "per_head_tables":
+        cd, sd = torch.from_numpy(c4).to(DEV), torch.from_numpy(s4).to(DEV)
+    else:
+        cd = torch.from_numpy(c).to(DEV).view(1, 1, T, N).expand(B, H, T, N)
+        sd = torch.from_numpy(s).to(DEV).view(1, 1, T, N).expand(B, H, T, N)
+    got = ext.rope_rotate(xd, cd, sd)
+    assert np.array_equal(np_of(got), as_dtype_values(want, vdt))
+
+
 # ---------------------------------------------------------------- backward
 BWD_SHAPES = [(1, 1, 5, 4, 3, 1), (2, 3, 70, 24, 16, 1), (1, 2, 200, 136, 72, 2), (1, 2, 300, 512, 256, 1)]
 
