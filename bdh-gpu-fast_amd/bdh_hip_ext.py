@@ -278,18 +278,31 @@ tril_decode_hip = tril_decode
 
 # ------------------------------------------------------------------ backward
 def tril_score_v_bwd(
-    q: torch.Tensor, k: Optional[torch.Tensor], v: torch.Tensor, dout: torch.Tensor
+    q: torch.Tensor,
+    k: Optional[torch.Tensor],
+    v: torch.Tensor,
+    dout: torch.Tensor,
+    *,
+    dq: Optional[torch.Tensor] = None,
+    dk: Optional[torch.Tensor] = None,
+    dv: Optional[torch.Tensor] = None,
 ) -> Tuple[torch.Tensor, Optional[torch.Tensor], torch.Tensor]:
     """Analytic gradients of ``tril(q k^T, -1) v``.
 
     ``k is None`` means self attention (k is q): returns ``(dq + dk, None, dv)``.
-    Otherwise ``(dq, dk, dv)``.  Gradients take their input's dtype.
+    Otherwise ``(dq, dk, dv)``.  Gradients take their input's dtype unless
+    output tensors (any float dtype, same shapes) are passed.
     """
-    dev = _require_device(q, k, v, dout)
+    dev = _require_device(q, k, v, dout, dq, dk, dv)
     B, H, T, N = q.shape
-    dq = torch.empty_like(q, memory_format=torch.contiguous_format)
-    dk = None if k is None else torch.empty_like(k, memory_format=torch.contiguous_format)
-    dv = torch.empty_like(v, memory_format=torch.contiguous_format)
+    if dq is None:
+        dq = torch.empty_like(q, memory_format=torch.contiguous_format)
+    if dk is None and k is not None:
+        dk = torch.empty_like(k, memory_format=torch.contiguous_format)
+    if k is None:
+        dk = None
+    if dv is None:
+        dv = torch.empty_like(v, memory_format=torch.contiguous_format)
     with torch.cuda.device(dev):
         need = _lib.bdh_tril_score_v_bwd_workspace(B, H, v.size(1), T, N, v.size(-1), _dtype_code(q))
         ws, nb = _workspace(need, dev)

@@ -237,7 +237,9 @@ BwdPlan plan_bwd(int64_t B, int64_t H, int64_t T, int64_t K, bool bf) {
   BwdPlan p;
   p.f = plan_fwd(B, H, T, K, bf);
   p.tpad = p.f.nt * kTile;
-  p.g_off = align_up(p.f.ws_bytes, 256);
+  // the first region holds the generic M^T partials or the bf16 score tiles
+  // of the MFMA path, whichever is larger
+  p.g_off = align_up(std::max(p.f.ws_bytes, bf ? sy_bwd_workspace(B, H, T, K) : size_t(0)), 256);
   p.ws_bytes = p.g_off + size_t(B * H) * size_t(p.tpad) * size_t(p.tpad) * (bf ? 2 : 4);
   return p;
 }
@@ -343,6 +345,12 @@ int run_bwd(const bdh_tensor4* q, const bdh_tensor4* k, const bdh_tensor4* v, co
   if (ws == nullptr || ws_bytes < p.ws_bytes) return BDH_ERR_WORKSPACE;
   const int64_t BH = B * H;
 
+  // bf16 self attention without RoPE: score tiles by the forward score kernel
+  // and dV from them (syrk.hip), in place of steps 1 and 4 below
+  int fast_dv = kNotEligible;
+  if (self && bf && !rope) fast_dv = sy_bwd_dv(q, v, dout, dv, ws, p.g_off, s);
+  if (fast_dv != kNotEligible && fast_dv != BDH_OK) return fast_dv;
+
   // 1. M^T partial tiles.
   ScoresArgs sa;
   sa.q = view_of(q);
@@ -362,7 +370,7 @@ int run_bwd(const bdh_tensor4* q, const bdh_tensor4* k, const bdh_tensor4* v, co
   sa.ntl = int(p.f.ntl);
   sa.qr.p = nullptr;
   sa.qr_bf = false;
-  BDH_TRY(run_scores(sa, p.f, BH, bf, rope, true, s));
+  if (fast_dv == kNotEligible) BDH_TRY(run_scores(sa, p.f, BH, bf, rope, true, s));
 
   // 2. G = dS + dS^T.
   GArgs ga;
@@ -390,7 +398,13 @@ int run_bwd(const bdh_tensor4* q, const bdh_tensor4* k, const bdh_tensor4* v, co
   da.freqs = freqs;
   da.rope_start = rope_start;
   if (numel4(dq) > 0) {
-    if (self) {
+    // bf16 self attention without RoPE: the MFMA kernel with transposing LDS
+    // reads (syrk.hip); otherwise the generic tile kernel below
+    int fast = kNotEligible;
+    if (self && bf && !rope) fast = sy_dq(ga.g, p.tpad, q, dq, s);
+    if (fast != kNotEligible) {
+      BDH_TRY(fast);
+    } else if (self) {
       da.x = view_of(q);
       da.x.s1 = q->stride[1];
       da.vec4_x = vec4_rows(q);
@@ -421,7 +435,7 @@ int run_bwd(const bdh_tensor4* q, const bdh_tensor4* k, const bdh_tensor4* v, co
   }
 
   // 4. dV.
-  if (numel4(dv) > 0) {
+  if (numel4(dv) > 0 && fast_dv == kNotEligible) {
     DvArgs va;
     va.spT = sa.sp;
     va.split_stride = BH * p.f.ntl * int64_t(kTileElems);

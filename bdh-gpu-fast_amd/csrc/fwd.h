@@ -50,6 +50,14 @@ int sy_cold(const bdh_tensor4* q, const bdh_tensor4* k, const bdh_tensor4* v, co
             const float* freqs, int64_t rope_start, const bdh_tensor4* qr, void* ws, size_t ws_bytes,
             hipStream_t s);
 
+// Backward dV on the MFMA path (syrk.hip): score tiles recomputed by the
+// forward score kernel into ws (sy_bwd_workspace bytes), then dV from them.
+size_t sy_bwd_workspace(int64_t B, int64_t H, int64_t T, int64_t N);
+int sy_bwd_dv(const bdh_tensor4* q, const bdh_tensor4* v, const bdh_tensor4* dout, const bdh_tensor4* dv, void* ws,
+              size_t ws_bytes, hipStream_t s);
+// Backward dQ = G X on the MFMA path (syrk.hip): bf16 X, self attention, no RoPE.
+int sy_dq(const void* g, int64_t tpad, const bdh_tensor4* x, const bdh_tensor4* out, hipStream_t s);
+
 FwdPlan plan_fwd(int64_t B, int64_t H, int64_t T, int64_t K, bool bf);
 int run_scores(const ScoresArgs& a, const FwdPlan& p, int64_t BH, bool bf, bool rope, bool trans,
                hipStream_t s);

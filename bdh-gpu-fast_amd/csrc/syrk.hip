@@ -518,6 +518,337 @@ __global__ __launch_bounds__(kSyThreads, 1) void k_sy_scores(const SyArgs a) {
   }
 }
 
+// ------------------------------------------------ backward: dQ = G X
+// dQ[slab] = G[slab] X[slab] for self attention (G = dS + dS^T, bf16, T x T
+// padded to tpad with zeros), X (T x N) bf16 row-major.  The contraction runs
+// over time, which is X's row index, so the B operand tiles are taken from X
+// as stored: 32 rows x 256 columns per k32 stage, DMA'd row-major into LDS
+// and read as MFMA B fragments with ds_read_b64_tr_b16.  Within each 16-lane
+// group that instruction hands lane i element i % 4 of the 8-byte chunks
+// addressed by group lanes i / 4 + 4 k (k = 0..3); so group lane q = 4 k + c
+// addresses row k0 + k, columns nb + 4 c .. + 3 and lane i receives
+// X[k0 .. k0 + 3][nb + i], half of a B fragment.
+//  * 256 x 256 output tiles, full K per workgroup (no partials), every tile of
+//    a slab on one XCD; the ring, barriers and waits are those of k_sy_scores
+//    (full tile, no RoPE).
+//  * A (G rows) uses the 64-byte-row swizzle of k_sy_scores; B rows are 512
+//    bytes with 16-byte chunk c stored at c ^ 4 (row & 3), so the four rows of
+//    one transposing read fall in different banks.
+typedef __attribute__((__vector_size__(4 * sizeof(__bf16)))) __bf16 bf16x4;
+typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
+
+struct DqsArgs {
+  const bf16_t* g;  // [slab][tpad][tpad]
+  const bf16_t* x;
+  int64_t x0, x1, x2;  // element strides of X over (b, h, t)
+  void* o;
+  int64_t o0, o1, o2;
+  int H, T, N, tpad, nslab, nti, ntn;
+};
+
+__device__ __forceinline__ bf16x4 lds_tr4(const uint8_t* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(p));
+}
+
+template <typename TO>
+__global__ __launch_bounds__(kSyThreads, 1) void k_dq_sy(const DqsArgs a) {
+  const int bid = blockIdx.x;
+  const int xcd = bid & 7, kk = bid >> 3;
+  const int tiles = a.nti * a.ntn;
+  const int grp = kk / tiles;
+  const int slab = grp * 8 + xcd;
+  if (slab >= a.nslab) return;
+  const int tt = kk - grp * tiles;
+  const int tn = tt / a.nti, ti = tt - tn * a.nti;
+  const int b = slab / a.H, h = slab - b * a.H;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int nst = a.tpad / 32;
+  const int i0 = ti * kSyTile, n0 = tn * kSyTile;
+  const void* gbase = sgpr_ptr(a.g + int64_t(slab) * a.tpad * a.tpad);
+  const void* xbase = sgpr_ptr(a.x + b * a.x0 + h * a.x1);
+  const uint32_t lds0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_u8*)sy_lds);
+
+  // DMA chunks of this lane: A (G rows) instructions 0-1, B (X rows) 2-3
+  uint32_t aoff[2], bcol[2];
+  int brow[2];
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int q = (u * 8 + w) * 1024 + lane * 16;
+    const int row = q >> 6;
+    const int c = ((q >> 4) & 3) ^ ((row >> 2) & 3);
+    const int gi = min(i0 + row, a.tpad - 1);  // rows past tpad: garbage, not stored
+    aoff[u] = uint32_t((gi * a.tpad + 8 * c) * 2);
+    const int rb = q >> 9, pb = (q >> 4) & 31;
+    brow[u] = rb;
+    bcol[u] = uint32_t((n0 + 8 * (pb ^ (4 * (rb & 3)))) * 2);
+  }
+  constexpr int NX = 5, lead = NX - 1;
+  auto slot = [&](int st) { return sy_lds + (st % NX) * kSySlot; };
+  struct StageDma {
+    uint32_t m0, ka, krow;
+  };
+  const uint32_t wl = lds0 + uint32_t(w) * 1024u;
+  auto stage_dma = [&](int st) {
+    StageDma d;
+    d.m0 = wl + uint32_t((st % NX) * kSySlot);
+    const int sc = min(st, nst - 1);
+    d.ka = uint32_t(sc * 64);
+    d.krow = uint32_t(sc * 32);
+    return d;
+  };
+  auto dma_a = [&](const StageDma& d, auto uc) {
+    constexpr int u = decltype(uc)::value;
+    dma16<u * 8192>(d.m0, gbase, aoff[u] + d.ka);
+  };
+  auto dma_b = [&](const StageDma& d, auto uc) {
+    constexpr int u = decltype(uc)::value;
+    const int row = min(int(d.krow) + brow[u], a.T - 1);  // rows past T meet zero G columns
+    dma16<kSyBlk + u * 8192>(d.m0, xbase, uint32_t(int64_t(row) * a.x2 * 2) + bcol[u]);
+  };
+
+  // fragments: A rows 4 wm + i; B columns 64 wn + 32 jb, two transposing reads each
+  const int wm = w >> 2, wn = w & 3;
+  uint32_t loff[2];
+#pragma unroll
+  for (int k2 = 0; k2 < 2; ++k2) {
+    const int c = (2 * k2 + (lane >> 5)) ^ ((lane >> 2) & 3);
+    loff[k2] = uint32_t((lane & 31) * 64 + c * 16);
+  }
+  const int g4 = lane >> 4, q = lane & 15;
+  int boff[2];
+#pragma unroll
+  for (int jb = 0; jb < 2; ++jb) {
+    const int col = 64 * wn + 32 * jb + 16 * (g4 & 1) + 4 * (q & 3);
+    const int row = 8 * (g4 >> 1) + (q >> 2);
+    boff[jb] = kSyBlk + row * 512 + (((col >> 3) ^ (4 * (row & 3))) * 16) + ((col >> 2) & 1) * 8;
+  }
+  f32x16 acc[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[i][r] = 0.f;
+  bf16x8 f0[6], f1[6];
+  auto read_frags = [&](bf16x8(&f)[6], int st, int hf) {
+    const uint8_t* sl = slot(st);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) f[i] = *reinterpret_cast<const bf16x8*>(sl + (4 * wm + i) * 2048 + loff[hf]);
+#pragma unroll
+    for (int jb = 0; jb < 2; ++jb) {
+      const uint8_t* pb = sl + boff[jb] + hf * 16 * 512;
+      const bf16x4 lo = lds_tr4(pb), hi = lds_tr4(pb + 4 * 512);
+      f[4 + jb] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+    }
+  };
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+
+  // prologue: stages 0 .. lead-1, then stage 0 landed
+  for (int st = 0; st < lead; ++st) {
+    const StageDma d = stage_dma(st);
+    dma_a(d, I0());
+    dma_a(d, I1());
+    dma_b(d, I0());
+    dma_b(d, I1());
+  }
+  sy_wait<(lead - 1) * 4>();
+  sy_barrier();
+  read_frags(f0, 0, 0);
+  // stage s: second-half fragment reads; first-half MFMAs with the A chunks of
+  // stage s + lead; wait for stage s+1; barrier; first-half fragments of s+1;
+  // second-half MFMAs with the B chunks of stage s + lead
+  for (int s = 0; s + 1 < nst; ++s) {
+    read_frags(f1, s, 1);
+    __builtin_amdgcn_sched_barrier(0);
+    const StageDma d = stage_dma(s + lead);
+    sy_static_for<8>([&](auto mc) {
+      constexpr int m = decltype(mc)::value;
+      acc[m] = mma(f0[m >> 1], f0[4 + (m & 1)], acc[m]);
+      if constexpr (m == 0) dma_a(d, I0());
+      if constexpr (m == 2) dma_a(d, I1());
+      if constexpr (m == 3) sy_wait<(lead - 2) * 4 + 2>();  // stage s+1 landed
+    });
+    __builtin_amdgcn_sched_barrier(0);
+    sy_barrier();
+    read_frags(f0, s + 1, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    sy_static_for<8>([&](auto mc) {
+      constexpr int m = decltype(mc)::value;
+      acc[m] = mma(f1[m >> 1], f1[4 + (m & 1)], acc[m]);
+      if constexpr (m == 1) dma_b(d, I0());
+      if constexpr (m == 3) dma_b(d, I1());
+    });
+  }
+  read_frags(f1, nst - 1, 1);
+  sy_static_for<8>([&](auto mc) {
+    constexpr int m = decltype(mc)::value;
+    acc[m] = mma(f0[m >> 1], f0[4 + (m & 1)], acc[m]);
+  });
+  sy_static_for<8>([&](auto mc) {
+    constexpr int m = decltype(mc)::value;
+    acc[m] = mma(f1[m >> 1], f1[4 + (m & 1)], acc[m]);
+  });
+  sy_wait<0>();  // the re-loads past the end land before the LDS is freed
+
+  TO* o = static_cast<TO*>(a.o) + b * a.o0 + h * a.o1;
+#pragma unroll
+  for (int m = 0; m < 8; ++m)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int row = i0 + 128 * wm + 32 * (m >> 1) + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+      const int col = n0 + 64 * wn + 32 * (m & 1) + (lane & 31);
+      if (row < a.T) o[int64_t(row) * a.o2 + col] = from_f<TO>(acc[m][r]);
+    }
+}
+
+// ---------------------------------------- backward: dV from score tiles
+// dV[b, hv, j, :] = sum over heads h and rows i > j of M_h[i, j] dO_h[i, :],
+// M from the partial score tiles of k_sy_scores (split sum in fp32, one
+// rounding to bf16).  Rows j in blocks of 64 per workgroup, all D (<= 256)
+// columns: wave w owns columns [64 w, +64).  Per 64-row chunk of i the M block
+// (64 i x 64 j) and the dO block (64 i x 256 d) are staged row-major in LDS
+// and both MFMA operands (M^T as A, dO as B, both contracting over i, their
+// row index) are read with ds_read_b64_tr_b16.  The next chunk's loads are
+// issued before the current chunk's MFMAs.
+struct DvsArgs {
+  const bf16_t* part;  // [slab][ntl][nsplit][256*256]
+  int ntl, nsplit;
+  const bf16_t* dO;
+  int64_t d0, d1, d2;
+  void* o;
+  int64_t o0, o1, o2;
+  int H, Hv, T, D;
+};
+
+template <typename TO, int NS>
+__global__ __launch_bounds__(256) void k_dv_sy(const DvsArgs a) {
+  __shared__ __attribute__((aligned(16))) uint8_t mblk[64 * 128];  // M [i][j], 16-byte chunk c at c ^ 2 (i & 3)
+  __shared__ __attribute__((aligned(16))) uint8_t dblk[64 * 512];  // dO [i][d], chunk c at c ^ 4 (i & 3)
+  const int rb = blockIdx.x, bv = blockIdx.y;
+  const int b = bv / a.Hv, hv = bv - b * a.Hv;
+  const int j0 = rb * 64;
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  const int h_lo = a.Hv == 1 ? 0 : hv, h_hi = a.Hv == 1 ? a.H : hv + 1;
+  const int ic0 = j0 / 64, nic = (a.T + 63) / 64;  // chunks of i: i >= j0 (i > j)
+  const int tj = j0 >> 8;
+
+  // builder roles: M rows li = tid / 4, 16 columns from lj; dO chunks e = tid + 256 u
+  const int li = tid >> 2, lj = (tid & 3) * 16;
+  uint4 mp[NS][2];
+  uint4 dp[8];
+  auto load_chunk = [&](int h, int ic) {
+    const int i0 = ic * 64;
+    const int ti = i0 >> 8;
+    const int slab = b * a.H + h;
+    const int gi = i0 + li;
+    const bf16_t* p = a.part + ((int64_t(slab) * a.ntl + ti * (ti + 1) / 2 + tj) * a.nsplit) * kSyTileElems +
+                      (gi & 255) * kSyTile + ((j0 + lj) & 255);
+#pragma unroll
+    for (int sp = 0; sp < NS; ++sp)
+#pragma unroll
+      for (int e = 0; e < 2; ++e)
+        mp[sp][e] = sp < a.nsplit ? *reinterpret_cast<const uint4*>(p + int64_t(sp) * kSyTileElems + 8 * e)
+                                  : uint4{0u, 0u, 0u, 0u};
+    const bf16_t* dob = a.dO + b * a.d0 + h * a.d1;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int e = tid + 256 * u, r = e >> 5, c = e & 31;
+      const int ig = i0 + r;
+      dp[u] = (ig < a.T && 8 * c < a.D) ? *reinterpret_cast<const uint4*>(dob + int64_t(ig) * a.d2 + 8 * c)
+                                        : uint4{0u, 0u, 0u, 0u};
+    }
+  };
+  auto store_chunk = [&](int ic) {
+    const int gi = ic * 64 + li;
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      float sacc[8];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) sacc[q] = 0.f;
+#pragma unroll
+      for (int sp = 0; sp < NS; ++sp) {
+        const uint32_t xw[4] = {mp[sp][e].x, mp[sp][e].y, mp[sp][e].z, mp[sp][e].w};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          sacc[2 * q] += __uint_as_float(xw[q] << 16);
+          sacc[2 * q + 1] += __uint_as_float(xw[q] & 0xffff0000u);
+        }
+      }
+      uint32_t pk[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int gj = j0 + lj + 8 * e + 2 * q;
+        const float lo = (gi < a.T && gi > gj) ? sacc[2 * q] : 0.f;
+        const float hi = (gi < a.T && gi > gj + 1) ? sacc[2 * q + 1] : 0.f;
+        pk[q] = pack_bf2(lo, hi);
+      }
+      const int c = (lj >> 3) + e;
+      *reinterpret_cast<u32x4*>(mblk + li * 128 + ((c ^ (2 * (li & 3))) * 16)) = u32x4{pk[0], pk[1], pk[2], pk[3]};
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int e = tid + 256 * u, r = e >> 5, c = e & 31;
+      *reinterpret_cast<uint4*>(dblk + r * 512 + ((c ^ (4 * (r & 3))) * 16)) = dp[u];
+    }
+  };
+  // transposing fragment reads: group lane q addresses row kbase + 4 t + q / 4,
+  // columns nb + 4 (q % 4)
+  const int g4 = lane >> 4, q = lane & 15;
+  int aoff[2], boff[2];
+#pragma unroll
+  for (int x = 0; x < 2; ++x) {
+    const int row = 8 * (g4 >> 1) + (q >> 2);
+    const int cm = 32 * x + 16 * (g4 & 1) + 4 * (q & 3);            // j column of M
+    aoff[x] = row * 128 + (((cm >> 3) ^ (2 * (row & 3))) * 16) + ((cm >> 2) & 1) * 8;
+    const int cd = 64 * w + 32 * x + 16 * (g4 & 1) + 4 * (q & 3);   // d column of dO
+    boff[x] = row * 512 + (((cd >> 3) ^ (4 * (row & 3))) * 16) + ((cd >> 2) & 1) * 8;
+  }
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][c][r] = 0.f;
+
+  const int per_h = nic - ic0;
+  const int total = per_h * (h_hi - h_lo);
+  if (total > 0) load_chunk(h_lo, ic0);
+  for (int it = 0; it < total; ++it) {
+    const int ic = ic0 + it % per_h;
+    __syncthreads();  // the previous chunk's fragment reads are done
+    store_chunk(ic);
+    if (it + 1 < total) load_chunk(h_lo + (it + 1) / per_h, ic0 + (it + 1) % per_h);
+    __syncthreads();
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      bf16x8 fa[2], fb[2];
+#pragma unroll
+      for (int x = 0; x < 2; ++x) {
+        const uint8_t* pa = mblk + aoff[x] + ks * 16 * 128;
+        fa[x] = __builtin_shufflevector(lds_tr4(pa), lds_tr4(pa + 4 * 128), 0, 1, 2, 3, 4, 5, 6, 7);
+        const uint8_t* pb = dblk + boff[x] + ks * 16 * 512;
+        fb[x] = __builtin_shufflevector(lds_tr4(pb), lds_tr4(pb + 4 * 512), 0, 1, 2, 3, 4, 5, 6, 7);
+      }
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int c = 0; c < 2; ++c) acc[i][c] = mma(fa[i], fb[c], acc[i][c]);
+    }
+  }
+  TO* o = static_cast<TO*>(a.o) + b * a.o0 + hv * a.o1;
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int j = j0 + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        const int d = 64 * w + 32 * c + (lane & 31);
+        if (j < a.T && d < a.D) o[int64_t(j) * a.o2 + d] = from_f<TO>(acc[i][c][r]);
+      }
+}
+
 // ------------------------------------------------------ score x V (direct)
 // V^T, bf16: vt[bv][d][t] = v[b][hv][t][d] (bv = b * Hv + hv), t padded to tp
 // with zeros.  The score x V product contracts over t, and MFMA operands are
@@ -870,6 +1201,119 @@ int sy_cold(const bdh_tensor4* q, const bdh_tensor4* k, const bdh_tensor4* v, co
   sa.o.s1 = out->stride[1];
   const dim3 gsv(unsigned((T + 63) / 64), unsigned(nslab));
   return out->dtype == BDH_BF16 ? launch_sy_sv<bf16_t>(sa, gsv, s) : launch_sy_sv<float>(sa, gsv, s);
+}
+
+
+// dQ = G X (self attention, bf16 X, no RoPE) on the MFMA path; kNotEligible
+// when the shapes fall outside it.
+int sy_dq(const void* g, int64_t tpad, const bdh_tensor4* x, const bdh_tensor4* out, hipStream_t s) {
+  const int64_t B = x->size[0], H = x->size[1], T = x->size[2], N = x->size[3];
+  if (x->dtype != BDH_BF16 || N % kSyTile != 0 || T < 1 || !rows16(x)) return kNotEligible;
+  if (out->size[0] != B || out->size[1] != H || out->size[2] != T || out->size[3] != N) return kNotEligible;
+  if (tpad % 32 != 0 || tpad * tpad * 2 >= (int64_t(1) << 31)) return kNotEligible;
+  if (((T - 1) * x->stride[2] + N) * 2 >= (int64_t(1) << 31)) return kNotEligible;
+  const int64_t nslab = B * H;
+  const int64_t nti = (T + kSyTile - 1) / kSyTile, ntn = N / kSyTile;
+  const int64_t grid = 8 * ((nslab + 7) / 8) * nti * ntn;
+  if (grid >= (int64_t(1) << 31) || nslab > (int64_t(1) << 24)) return kNotEligible;
+  DqsArgs a;
+  a.g = static_cast<const bf16_t*>(g);
+  a.x = static_cast<const bf16_t*>(x->data);
+  a.x0 = x->stride[0];
+  a.x1 = x->stride[1];
+  a.x2 = x->stride[2];
+  a.o = out->data;
+  a.o0 = out->stride[0];
+  a.o1 = out->stride[1];
+  a.o2 = out->stride[2];
+  a.H = int(H);
+  a.T = int(T);
+  a.N = int(N);
+  a.tpad = int(tpad);
+  a.nslab = int(nslab);
+  a.nti = int(nti);
+  a.ntn = int(ntn);
+  const dim3 gs{unsigned(grid)};
+  if (out->dtype == BDH_BF16)
+    BDH_LAUNCH("k_dq_sy", k_dq_sy<bf16_t>, gs, dim3(kSyThreads), 0, s, a);
+  else
+    BDH_LAUNCH("k_dq_sy", k_dq_sy<float>, gs, dim3(kSyThreads), 0, s, a);
+  return BDH_OK;
+}
+
+
+// dV for bf16 self attention without RoPE: the score tiles M by k_sy_scores
+// into ws, then k_dv_sy.  kNotEligible when the shapes fall outside it.
+size_t sy_bwd_workspace(int64_t B, int64_t H, int64_t T, int64_t N) {
+  const SyPlan p = sy_plan(B * H, T, N, true, false, 0);
+  return p.ok ? p.part_bytes : 0;
+}
+
+int sy_bwd_dv(const bdh_tensor4* q, const bdh_tensor4* v, const bdh_tensor4* dout, const bdh_tensor4* dv, void* ws,
+              size_t ws_bytes, hipStream_t s) {
+  const int64_t B = q->size[0], H = q->size[1], T = q->size[2], N = q->size[3];
+  const int64_t Hv = v->size[1], D = v->size[3];
+  if (q->dtype != BDH_BF16 || dout->dtype != BDH_BF16) return kNotEligible;
+  if (T < 1 || N < 64 || N % 64 != 0 || T > 65535 || !rows16(q) || !rows16(dout)) return kNotEligible;
+  if (D < 1 || D > 256 || D % 8 != 0) return kNotEligible;
+  if (((T - 1) * q->stride[2] + N) * 2 >= (int64_t(1) << 31)) return kNotEligible;
+  const int64_t nslab = B * H;
+  if (nslab > (int64_t(1) << 24) || B * Hv > 65535) return kNotEligible;
+  const SyPlan p = sy_plan(nslab, T, N, true, false, 0);
+  if (!p.ok) return kNotEligible;
+  const int64_t grid_scores = 8 * ((nslab + 7) / 8) * p.ips;
+  if (grid_scores >= (int64_t(1) << 31)) return kNotEligible;
+  if (ws == nullptr || ws_bytes < p.part_bytes) return BDH_ERR_WORKSPACE;
+  bf16_t* part = static_cast<bf16_t*>(ws);
+  SyArgs a;
+  a.q = a.k = static_cast<const bf16_t*>(q->data);
+  a.q0 = a.k0 = q->stride[0];
+  a.q1 = a.k1 = q->stride[1];
+  a.q2 = a.k2 = q->stride[2];
+  a.H = int(H);
+  a.T = int(T);
+  a.N = int(N);
+  a.nslab = int(nslab);
+  a.ips = p.ips;
+  a.nchunk = p.nchunk;
+  a.nsplit = p.nsplit;
+  a.ntl = p.ntl;
+  a.cs = nullptr;
+  a.part = part;
+  a.qr = nullptr;
+  a.r0 = a.r1 = a.r2 = 0;
+  for (int i = 0; i < p.ips; ++i) a.items[i] = p.items[i];
+  BDH_LAUNCH("k_sy_scores", (k_sy_scores<false, true>), dim3{unsigned(grid_scores)}, dim3(kSyThreads), 0, s, a);
+  if (numel4(dv) == 0) return BDH_OK;
+  DvsArgs d;
+  d.part = part;
+  d.ntl = p.ntl;
+  d.nsplit = p.nsplit;
+  d.dO = static_cast<const bf16_t*>(dout->data);
+  d.d0 = dout->stride[0];
+  d.d1 = dout->stride[1];
+  d.d2 = dout->stride[2];
+  d.o = dv->data;
+  d.o0 = dv->stride[0];
+  d.o1 = dv->stride[1];
+  d.o2 = dv->stride[2];
+  d.H = int(H);
+  d.Hv = int(Hv);
+  d.T = int(T);
+  d.D = int(D);
+  const dim3 gd(unsigned((T + 63) / 64), unsigned(B * Hv));
+  const bool o16 = dv->dtype == BDH_BF16;
+  if (p.nsplit <= 2) {
+    if (o16) BDH_LAUNCH("k_dv_sy", (k_dv_sy<bf16_t, 2>), gd, dim3(256), 0, s, d);
+    else BDH_LAUNCH("k_dv_sy", (k_dv_sy<float, 2>), gd, dim3(256), 0, s, d);
+  } else if (p.nsplit <= 4) {
+    if (o16) BDH_LAUNCH("k_dv_sy", (k_dv_sy<bf16_t, 4>), gd, dim3(256), 0, s, d);
+    else BDH_LAUNCH("k_dv_sy", (k_dv_sy<float, 4>), gd, dim3(256), 0, s, d);
+  } else {
+    if (o16) BDH_LAUNCH("k_dv_sy", (k_dv_sy<bf16_t, 8>), gd, dim3(256), 0, s, d);
+    else BDH_LAUNCH("k_dv_sy", (k_dv_sy<float, 8>), gd, dim3(256), 0, s, d);
+  }
+  return BDH_OK;
 }
 
 }  // namespace bdh
