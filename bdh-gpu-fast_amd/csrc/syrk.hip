@@ -1,36 +1,34 @@
-// bf16 prefill forward of BDH strict-tril attention for gfx950 (the hot path):
+// bf16 MFMA kernels of BDH strict-tril attention for gfx950 (the hot path):
 //
 //   out[b,h,i,:] = sum_{j<i} <R_i, R_j> V_j,   R = RoPE(x) (or R = q, k given)
 //
-// Three kernels per call:
-//  1. k_rope_table  (RoPE only): (cos, sin) of every (position, pair) as two
-//     bf16 halves of one dword, [T][N/2].  The same table serves every (b,h).
+// Forward, three kernels per call:
+//  1. k_rope_table  (RoPE only): (cos, sin) of every (row, pair) as two bf16
+//     halves of one dword, stage-major.  The same table serves every (b,h).
 //  2. k_sy_scores: partial score tiles S = R R^T.
-//     * 256x256 output tiles over the lower triangle of each (b,h) slab.  A
-//       diagonal tile with Q = K loads one row block and computes only its
-//       lower 32x32 blocks (each SIMD issues at most 10 MFMAs per k16 step,
-//       against 16 for a full tile).
-//     * split-K: split s of n handles the 64-wide k-chunks s, s+n, s+2n, ...,
-//       so the splits and tiles of a slab walk k in step and the row blocks
-//       re-read by neighbouring tiles are served by the XCD's L2.  Every item
-//       of a slab runs on one XCD (workgroup id % 8 selects the XCD).
+//     * 256x256 output tiles over the lower triangle of each (b,h) slab; with
+//       Q = K the diagonal tiles go in pairs, each computing its 36 lower
+//       32x32 blocks (four 9-block wave programs per tile).
+//     * split-K: split s of n handles the 64-wide k-chunks s, s+n, s+2n, ...;
+//       all items of a slab run the same number of stages on one XCD
+//       (workgroup id % 8 selects the XCD), so the tiles that load the same
+//       row blocks walk k in step and the second load is an L2 hit.
 //     * x streams HBM -> LDS through global_load_lds_dwordx4 into a ring of
-//       32-wide k stages (5 slots, issued four stages ahead; with RoPE 3 slots
-//       plus a 2-slot ring for the table entries of the same stages at the
-//       same offsets, issued two stages ahead).  The 16-byte chunk c of row r sits at position c ^ ((r >> 2) & 3)
-//       of its 64-byte LDS row, which makes the MFMA fragment reads
-//       bank-conflict free.
-//     * RoPE is applied in place at the end of the stage before its MFMAs:
-//       each lane rotates the chunks it loaded itself (per pair two
-//       v_dot2_f32_bf16, products exact in fp32, one v_cvt_pk_bf16_f32 and one
-//       v_alignbit_b32).  No vector-memory load of the main loop returns to
-//       registers, so the only waits on it are the explicit ones below.
+//       32-wide k stages (5 slots issued four stages ahead; with RoPE 4 slots
+//       and one slot for the next stage's table entries).  The 16-byte chunk
+//       c of row r sits at position c ^ ((r >> 2) & 3) of its 64-byte LDS
+//       row, which makes the MFMA fragment reads bank-conflict free.
+//     * RoPE is applied in place in the stage before its MFMAs: each lane
+//       rotates the chunks it loaded itself (per pair two v_dot2_f32_bf16,
+//       products exact in fp32, one v_cvt_pk_bf16_f32 and one v_alignbit_b32).
+//     * A barrier between the two k16 halves of a stage, fragments of the
+//       next half read before the current half's MFMAs.
 //     * v_mfma_f32_32x32x16_bf16 with fp32 accumulators; the epilogue stores
-//       the partial tiles [slab][item][256][256] as bf16.
-//  3. k_sy_vt + k_sy_sv: out = tril(sum over splits of S, -1) V.  V is
-//     transposed once (bf16, contiguous along the contraction); each wave then
-//     loads its MFMA fragments straight from global memory: the split sum of
-//     the partial score rows (formed in fp32, masked, rounded to bf16) and V^T.
+//       the partial tiles [slab][tile][split][256][256] as bf16.
+//  3. k_sy_sv: out = tril(sum over splits of S, -1) V, score blocks and V rows
+//     staged in LDS, V read as MFMA fragments with ds_read_b64_tr_b16.
+// Backward (bf16 self attention without RoPE): k_dq_sy (dQ = G X) and k_dv_sy
+// (dV from the score tiles of k_sy_scores), both with transposing LDS reads.
 #include <algorithm>
 #include <type_traits>
 #include <utility>
@@ -849,50 +847,30 @@ __global__ __launch_bounds__(256) void k_dv_sy(const DvsArgs a) {
       }
 }
 
-// ------------------------------------------------------ score x V (direct)
-// V^T, bf16: vt[bv][d][t] = v[b][hv][t][d] (bv = b * Hv + hv), t padded to tp
-// with zeros.  The score x V product contracts over t, and MFMA operands are
-// contiguous along the contraction, so V is transposed once per call.
-template <typename TV>
-__global__ __launch_bounds__(256) void k_sy_vt(View v, int Hv, int T, int D, int tp, bf16_t* __restrict__ vt) {
-  __shared__ float tile[32][33];
-  const int bv = blockIdx.z, b = bv / Hv, hv = bv - b * Hv;
-  const int t0 = blockIdx.x * 32, d0 = blockIdx.y * 32;
-  const TV* src = static_cast<const TV*>(v.p) + b * v.s0 + hv * v.s1;
-  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;  // 32 x 8
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int t = t0 + ty + 8 * r, d = d0 + tx;
-    tile[ty + 8 * r][tx] = (t < T && d < D) ? to_f(src[int64_t(t) * v.s2 + d]) : 0.f;
-  }
-  __syncthreads();
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int d = d0 + ty + 8 * r, t = t0 + tx;
-    if (d < D && t < tp) vt[(int64_t(bv) * D + d) * tp + t] = f2bf(tile[tx][ty + 8 * r]);
-  }
-}
-
+// ------------------------------------------------------------- score x V
+// out rows [64 rb, +64) of one (b,h) slab, all D (<= 256) columns.  Keys go
+// in chunks of 64.  The 256 threads first stage the chunk in LDS: the score
+// block (64 rows x 64 keys: the split sum of the partial rows in fp32, the
+// strict-lower mask, one rounding to bf16), each thread 16 keys of one row,
+// and the V rows of the chunk (64 x D, rounded to bf16), row-major as stored.
+// Wave w then multiplies them into columns [64 w, +64): 2 x 2 blocks of
+// 32 x 32, four k16 steps; A fragments are plain reads, B fragments (V,
+// contracting over its row index) ds_read_b64_tr_b16 reads.  The partial
+// rows and V rows of the next chunk are loaded before this chunk's MFMAs.
+// Score rows are 128 bytes with 16-byte chunk kc at kc ^ ((r >> 1) & 7); V
+// rows 512 bytes with chunk c at c ^ 4 (r & 3): both conflict free.
 struct SvArgs {
   const bf16_t* part;  // partial score tiles [slab][ntl][nsplit][256*256]
-  const bf16_t* vt;    // [B*Hv][D][tp]
-  int ntl, nsplit, H, Hv, T, D, tp;
+  View v;              // V (B, Hv, T, D)
+  int ntl, nsplit, H, Hv, T, D;
   View o;
 };
 
-// out rows [64 rb, +64) of one (b,h) slab, all D (<= 256) columns.  Keys go
-// in chunks of 64.  The 256 threads first form the chunk's score block in LDS
-// (64 rows x 64 keys: the split sum of the partial rows in fp32, the
-// strict-lower mask, one rounding to bf16), each thread 16 keys of one row,
-// read as two 16-byte loads per split; wave w then multiplies it with V^T
-// columns [64 w, +64): 2 x 2 blocks of 32 x 32, four k16 steps, B fragments
-// straight from V^T.  The partial rows and V^T fragments of the next chunk are
-// loaded before this chunk's MFMAs.  LDS rows are 128 bytes; the 16-byte
-// chunk kc of row r sits at kc ^ ((r >> 1) & 7), so the fragment reads (16
-// rows per pass) and the block writes are bank-conflict free.
-template <typename TO, int NS>
+template <typename TO, typename TV, int NS>
 __global__ __launch_bounds__(256) void k_sy_sv(const SvArgs a) {
-  __shared__ __attribute__((aligned(16))) uint8_t blk[2][64 * 128];
+  __shared__ __attribute__((aligned(16))) uint8_t blk[64 * 128];
+  __shared__ __attribute__((aligned(16))) uint8_t vblk[64 * 512];
+  constexpr int VL = sizeof(TV) == 2 ? 1 : 2;  // 16-byte loads per 8 V elements
   const int rb = blockIdx.x, slab = blockIdx.y;
   const int b = slab / a.H, h = slab - b * a.H, hv = a.Hv == 1 ? 0 : h;
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
@@ -900,24 +878,16 @@ __global__ __launch_bounds__(256) void k_sy_sv(const SvArgs a) {
   const int kend = min(a.T, r0 + 64);  // keys j < rows of this block
   const int nch = (kend + 63) / 64;
   const bf16_t* pslab = a.part + int64_t(slab) * a.ntl * a.nsplit * kSyTileElems;
-  const bf16_t* vtb = a.vt + (int64_t(b) * a.Hv + hv) * a.D * a.tp;
+  const TV* vb = static_cast<const TV*>(a.v.p) + b * a.v.s0 + hv * a.v.s1;
 
-  // block builder: row lr, keys [lk, +16) of the chunk
+  // block builder: row lr, keys [lk, +16) of the chunk; V chunks e = tid + 256 u
   const int lr = tid >> 2, lk = (tid & 3) * 16;
   const int gi = r0 + lr;
   const int ti = min(gi, a.T - 1) >> 8;
   const bool row_ok = gi < a.T;
-  // MFMA roles: output columns d = 64 w + 32 c + lane % 32
-  int dcol[2];
-  bool dok[2];
-#pragma unroll
-  for (int c = 0; c < 2; ++c) {
-    dcol[c] = 64 * w + 32 * c + (lane & 31);
-    dok[c] = dcol[c] < a.D;
-  }
 
-  uint4 pr[NS][2];       // partial rows of the next chunk
-  bf16x8 vb[2][4];       // V^T fragments of the next chunk [c][k16 step]
+  uint4 pr[NS][2];      // partial rows of the next chunk
+  uint4 vr[8][VL];      // V rows of the next chunk
   auto load_chunk = [&](int ck) {
     const int j0 = ck * 64;
     const int tile = ti * (ti + 1) / 2 + (j0 >> 8);
@@ -929,16 +899,17 @@ __global__ __launch_bounds__(256) void k_sy_sv(const SvArgs a) {
         pr[sp][e] = sp < a.nsplit ? *reinterpret_cast<const uint4*>(p + int64_t(sp) * kSyTileElems + 8 * e)
                                   : uint4{0u, 0u, 0u, 0u};
 #pragma unroll
-    for (int c = 0; c < 2; ++c)
+    for (int u = 0; u < 8; ++u) {
+      const int e = tid + 256 * u, r = e >> 5, c = e & 31;
+      const int j = j0 + r;
+      const bool ok = j < kend && 8 * c < a.D;
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        const int j = j0 + 16 * ks + 8 * (lane >> 5);
-        vb[c][ks] = (dok[c] && j < kend) ? *reinterpret_cast<const bf16x8*>(vtb + int64_t(dcol[c]) * a.tp + j)
-                                         : __builtin_bit_cast(bf16x8, u32x4{0u, 0u, 0u, 0u});
-      }
+      for (int l = 0; l < VL; ++l)
+        vr[u][l] = ok ? *reinterpret_cast<const uint4*>(vb + int64_t(j) * a.v.s2 + 8 * c + 4 * l) : uint4{0u, 0u, 0u, 0u};
+    }
   };
-  // split sum, mask (j < i, j < T), one rounding; two 16-byte LDS writes
-  auto build = [&](int ck, uint8_t* dst) {
+  // split sum, mask (j < i, j < T), one rounding; then the V block as bf16
+  auto store_chunk = [&](int ck) {
     const int j0 = ck * 64 + lk;
 #pragma unroll
     for (int e = 0; e < 2; ++e) {
@@ -963,9 +934,37 @@ __global__ __launch_bounds__(256) void k_sy_sv(const SvArgs a) {
         pk[q] = pack_bf2(lo, hi);
       }
       const int kc = (lk >> 3) + e;
-      *reinterpret_cast<u32x4*>(dst + lr * 128 + ((kc ^ ((lr >> 1) & 7)) * 16)) = u32x4{pk[0], pk[1], pk[2], pk[3]};
+      *reinterpret_cast<u32x4*>(blk + lr * 128 + ((kc ^ ((lr >> 1) & 7)) * 16)) = u32x4{pk[0], pk[1], pk[2], pk[3]};
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int e = tid + 256 * u, r = e >> 5, c = e & 31;
+      u32x4 y;
+      if constexpr (VL == 1) {
+        y = u32x4{vr[u][0].x, vr[u][0].y, vr[u][0].z, vr[u][0].w};
+      } else {
+        const uint32_t f[8] = {vr[u][0].x, vr[u][0].y, vr[u][0].z, vr[u][0].w,
+                               vr[u][1].x, vr[u][1].y, vr[u][1].z, vr[u][1].w};
+        y = u32x4{pack_bf2(__uint_as_float(f[0]), __uint_as_float(f[1])), pack_bf2(__uint_as_float(f[2]), __uint_as_float(f[3])),
+                  pack_bf2(__uint_as_float(f[4]), __uint_as_float(f[5])), pack_bf2(__uint_as_float(f[6]), __uint_as_float(f[7]))};
+      }
+      *reinterpret_cast<u32x4*>(vblk + r * 512 + ((c ^ (4 * (r & 3))) * 16)) = y;
     }
   };
+  // B fragments: group lane q addresses V row 16 ks + 8 (g / 2) + 4 t + q / 4,
+  // columns 64 w + 32 c + 16 (g % 2) + 4 (q % 4)
+  const int g4 = lane >> 4, q = lane & 15;
+  int boff[2];
+  int dcol[2];
+  bool dok[2];
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+    const int row = 8 * (g4 >> 1) + (q >> 2);
+    const int cd = 64 * w + 32 * c + 16 * (g4 & 1) + 4 * (q & 3);
+    boff[c] = row * 512 + (((cd >> 3) ^ (4 * (row & 3))) * 16) + ((cd >> 2) & 1) * 8;
+    dcol[c] = 64 * w + 32 * c + (lane & 31);
+    dok[c] = dcol[c] < a.D;
+  }
 
   f32x16 acc[2][2];
 #pragma unroll
@@ -977,29 +976,28 @@ __global__ __launch_bounds__(256) void k_sy_sv(const SvArgs a) {
 
   load_chunk(0);
   for (int ck = 0; ck < nch; ++ck) {
-    uint8_t* buf = blk[ck & 1];
-    build(ck, buf);
-    bf16x8 vcur[2][4];
-#pragma unroll
-    for (int c = 0; c < 2; ++c)
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) vcur[c][ks] = vb[c][ks];
+    __syncthreads();  // the previous chunk's fragment reads are done
+    store_chunk(ck);
     if (ck + 1 < nch) load_chunk(ck + 1);
-    // chunk ck's block is complete; buffer (ck+1) & 1 was last read before it
     __syncthreads();
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
-      bf16x8 fa[2];
+      bf16x8 fa[2], fb[2];
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
         const int row = 32 * i + (lane & 31);
         const int kc = 2 * ks + (lane >> 5);
-        fa[i] = *reinterpret_cast<const bf16x8*>(buf + row * 128 + ((kc ^ ((row >> 1) & 7)) * 16));
+        fa[i] = *reinterpret_cast<const bf16x8*>(blk + row * 128 + ((kc ^ ((row >> 1) & 7)) * 16));
+      }
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        const uint8_t* pb = vblk + boff[c] + ks * 16 * 512;
+        fb[c] = __builtin_shufflevector(lds_tr4(pb), lds_tr4(pb + 4 * 512), 0, 1, 2, 3, 4, 5, 6, 7);
       }
 #pragma unroll
       for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int c = 0; c < 2; ++c) acc[i][c] = mma(fa[i], vcur[c][ks], acc[i][c]);
+        for (int c = 0; c < 2; ++c) acc[i][c] = mma(fa[i], fb[c], acc[i][c]);
     }
   }
   TO* o = static_cast<TO*>(const_cast<void*>(a.o.p)) + b * a.o.s0 + h * a.o.s1;
@@ -1014,25 +1012,22 @@ __global__ __launch_bounds__(256) void k_sy_sv(const SvArgs a) {
       }
 }
 
-template <typename TO>
+template <typename TO, typename TV>
 int launch_sy_sv(const SvArgs& sa, dim3 grid, hipStream_t s) {
   const int ns = sa.nsplit;
   if (ns <= 2)
-    BDH_LAUNCH("k_sy_sv", (k_sy_sv<TO, 2>), grid, dim3(256), 0, s, sa);
+    BDH_LAUNCH("k_sy_sv", (k_sy_sv<TO, TV, 2>), grid, dim3(256), 0, s, sa);
   else if (ns <= 4)
-    BDH_LAUNCH("k_sy_sv", (k_sy_sv<TO, 4>), grid, dim3(256), 0, s, sa);
+    BDH_LAUNCH("k_sy_sv", (k_sy_sv<TO, TV, 4>), grid, dim3(256), 0, s, sa);
   else
-    BDH_LAUNCH("k_sy_sv", (k_sy_sv<TO, 8>), grid, dim3(256), 0, s, sa);
+    BDH_LAUNCH("k_sy_sv", (k_sy_sv<TO, TV, 8>), grid, dim3(256), 0, s, sa);
   return BDH_OK;
 }
 
 // ---------------------------------------------------------------- host plan
-// V^T rows hold the positions padded to a multiple of 32 (zeros beyond T).
-inline int sy_vt_pitch(int64_t T) { return int((T + 31) / 32 * 32); }
-
 struct SyPlan {
   int nt = 0, ntl = 0, ips = 0, nchunk = 0, nsplit = 1;
-  size_t table_bytes = 0, part_bytes = 0, vt_bytes = 0, ws_bytes = 0;
+  size_t table_bytes = 0, part_bytes = 0, ws_bytes = 0;
   uint32_t items[kSyMaxItems];
   bool ok = false;
 };
@@ -1075,9 +1070,8 @@ SyPlan sy_plan(int64_t nslab, int64_t T, int64_t N, bool self, bool rope, int64_
   p.ips = n;
   p.table_bytes = rope ? align_up(size_t(T) * size_t(N / 2) * 4, 256) : 0;
   p.part_bytes = size_t(nslab) * size_t(p.ntl) * size_t(S) * kSyTileElems * sizeof(bf16_t);
-  // V^T for the score x V product: at most one copy per (b, h) slab
-  p.vt_bytes = align_up(size_t(nslab) * size_t(Dv) * size_t(sy_vt_pitch(T)) * sizeof(bf16_t), 256);
-  p.ws_bytes = p.table_bytes + p.part_bytes + p.vt_bytes;
+  (void)Dv;
+  p.ws_bytes = p.table_bytes + p.part_bytes;
   p.ok = true;
   return p;
 }
@@ -1115,7 +1109,8 @@ int sy_cold(const bdh_tensor4* q, const bdh_tensor4* k, const bdh_tensor4* v, co
   const bool rope = freqs != nullptr;
   if (rope && !self) return kNotEligible;
   if (T < 1 || N < 64 || N % 64 != 0 || !rows16(q) || !rows16(k)) return kNotEligible;
-  if (v->size[3] > 256) return kNotEligible;  // score x V: four waves x 64 columns
+  // score x V: four waves x 64 columns, 8-element (16 / 32-byte) V row chunks
+  if (v->size[3] > 256 || v->size[3] % 8 != 0 || !rows16(v)) return kNotEligible;
   if (((T - 1) * std::max(q->stride[2], k->stride[2]) + N) * 2 >= (int64_t(1) << 31)) return kNotEligible;
   if (rope && int64_t(T) * N * 2 >= (int64_t(1) << 31)) return kNotEligible;
   if (T > 65535) return kNotEligible;
@@ -1173,34 +1168,22 @@ int sy_cold(const bdh_tensor4* q, const bdh_tensor4* k, const bdh_tensor4* v, co
     BDH_LAUNCH("k_sy_scores", (k_sy_scores<false, false>), gs, dim3(kSyThreads), 0, s, a);
   if (numel4(out) == 0) return BDH_OK;
 
-  // score x V: V^T once, then the direct-load MFMA kernel
-  const int tp = sy_vt_pitch(T);
-  bf16_t* vt = reinterpret_cast<bf16_t*>(wsb + p.table_bytes + p.part_bytes);
-  const int Hv = int(v->size[1]);
-  const int D = int(Dv);
-  {
-    View vv = view_of(v);
-    vv.s1 = v->stride[1];
-    const dim3 gv(unsigned((tp + 31) / 32), unsigned((D + 31) / 32), unsigned(B * Hv));
-    if (v->dtype == BDH_BF16)
-      BDH_LAUNCH("k_sy_vt", k_sy_vt<bf16_t>, gv, dim3(256), 0, s, vv, Hv, int(T), D, tp, vt);
-    else
-      BDH_LAUNCH("k_sy_vt", k_sy_vt<float>, gv, dim3(256), 0, s, vv, Hv, int(T), D, tp, vt);
-  }
+  // score x V
   SvArgs sa;
   sa.part = part;
-  sa.vt = vt;
+  sa.v = view_of(v);
   sa.ntl = p.ntl;
   sa.nsplit = p.nsplit;
   sa.H = int(H);
-  sa.Hv = Hv;
+  sa.Hv = int(v->size[1]);
   sa.T = int(T);
-  sa.D = D;
-  sa.tp = tp;
+  sa.D = int(Dv);
   sa.o = view_of(out);
   sa.o.s1 = out->stride[1];
   const dim3 gsv(unsigned((T + 63) / 64), unsigned(nslab));
-  return out->dtype == BDH_BF16 ? launch_sy_sv<bf16_t>(sa, gsv, s) : launch_sy_sv<float>(sa, gsv, s);
+  const bool o16 = out->dtype == BDH_BF16, v16 = v->dtype == BDH_BF16;
+  if (o16) return v16 ? launch_sy_sv<bf16_t, bf16_t>(sa, gsv, s) : launch_sy_sv<bf16_t, float>(sa, gsv, s);
+  return v16 ? launch_sy_sv<float, bf16_t>(sa, gsv, s) : launch_sy_sv<float, float>(sa, gsv, s);
 }
 
 
