@@ -9,12 +9,12 @@ F = B*nh*(N+D)*T*(T-1) flops per step (strict lower triangle; RoPE's
 elementwise work is not counted) divided by the measured step time.
 
 The JSON line also carries:
-  * ``roofline``: the dominant kernel (``k_scores``, the score tiles QR QR^T)
+  * ``roofline``: the dominant kernel (``k_sy_scores``, the score tiles QR QR^T)
     timed with HIP events on its launch stream over a timed region of the same
     K steps; achieved = its algorithmic flops B*nh*N*T*(T-1) / mean duration,
     against the 2.5 PFLOP/s bf16 dense MFMA peak.  ``traffic`` is the HBM
     bytes per launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE runs
-    (profiles/k_scores_c1_bf16_pmc.txt) when present, else null.
+    (profiles/<kernel>_c1_bf16_pmc.txt) when present, else null.
   * ``cpu_baseline``: the CPU oracle (numpy restatement of the reference CPU
     path, fp32, BLAS threads as reported) on a bounded sample of the same
     workload, in the same unit.
@@ -46,7 +46,7 @@ PEAK_HBM_GBS = 8000.0
 C1 = dict(B=8, nh=4, T=512, N=8192, D=256)
 C3 = dict(B=64, nh=4, N=8192, D=256, S=(256, 384, 511))
 C4 = dict(B=16, nh=4, T=1024, N=8192, D=256)
-CALIB_BYTES = 1 << 29  # plain copy used to scale the HBM byte counters
+CALIB_BYTES = 1 << 29  # reference elementwise pass that scales the HBM byte counters
 
 
 def log(msg: str) -> None:
@@ -150,8 +150,8 @@ def main() -> int:
     ap.add_argument(
         "--calibrate",
         action="store_true",
-        help="also run one plain device copy of CALIB_BYTES (the reference point that scales the "
-        "rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes)",
+        help="also run one elementwise multiply over CALIB_BYTES (the reference point that scales "
+        "the rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes)",
     )
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -183,11 +183,15 @@ def main() -> int:
         return kernels.bdh_attn_rope(x, v, freqs, 0, impl="hip")
 
     if args.calibrate:
+        # Reference kernel of known traffic for the HBM byte counters: one
+        # full-grid elementwise multiply (torch's vectorized_elementwise_kernel)
+        # reading and writing CALIB_BYTES, like the kernels it scales.
         src = torch.ones(CALIB_BYTES // 4, dtype=torch.float32, device=dev)
         dst = torch.empty_like(src)
-        dst.copy_(src)
         torch.cuda.synchronize()
-        log(f"[bench] calibration copy: {CALIB_BYTES} bytes read, {CALIB_BYTES} bytes written")
+        torch.mul(src, 2.0, out=dst)
+        torch.cuda.synchronize()
+        log(f"[bench] calibration multiply: {CALIB_BYTES} bytes read, {CALIB_BYTES} bytes written")
         del src, dst
 
     launches0 = ext.launch_count()
