@@ -44,7 +44,7 @@ constexpr int kSyThreads = 512;
 constexpr int kSyTile = 256;
 constexpr int kSyBlk = kSyTile * 64;   // bytes of one row block per stage (256 rows x 32 bf16)
 constexpr int kSySlot = 2 * kSyBlk;    // A and B row blocks
-constexpr int kSyLdsSlots = 5;    // 160 KB: x ring of 5 (plain) or 3 x + 2 RoPE table (fused)
+constexpr int kSyLdsSlots = 5;    // 160 KB: x ring of 5 (plain) or 4 x + 1 RoPE table (fused)
 constexpr int kSyMaxItems = 256;
 constexpr int kSyMaxTiles = 128;
 constexpr int kSyTileElems = kSyTile * kSyTile;
@@ -257,8 +257,6 @@ __global__ __launch_bounds__(kSyThreads, 1) void k_sy_scores(const SyArgs a) {
   const bool write_qr = ROPE && a.qr != nullptr && diag;
 
   auto kofs = [&](int s) { return (split + S * (s >> 1)) * 64 + (s & 1) * 32; };
-  // x ring depth; issuing runs NX - 1 stages ahead of the MFMAs.  With RoPE
-  // the two remaining slots hold the table entries of the next two stages.
   // LDS: an x ring of NX slots, issued lead = NX - 1 stages ahead; with RoPE
   // four x slots and one slot for the table entries of the next stage.
   constexpr int NX = ROPE ? 4 : 5;
