@@ -385,8 +385,14 @@ int run_bwd(const bdh_tensor4* q, const bdh_tensor4* k, const bdh_tensor4* v, co
   ga.vec_v = vec16_ok(v);
   ga.g = static_cast<char*>(ws) + p.g_off;
   ga.tpad = p.tpad;
-  BDH_TRY(bf ? run_g<true>(ga, p.f.nt, BH, dout->dtype, v->dtype, s)
-             : run_g<false>(ga, p.f.nt, BH, dout->dtype, v->dtype, s));
+  // bf16 G from bf16 dO and V: the MFMA score kernel with the G epilogue
+  // (syrk.hip); otherwise the generic tile kernel
+  const int gfast = bf ? sy_bwd_g(dout, v, ga.g, p.tpad, s) : kNotEligible;
+  if (gfast != kNotEligible)
+    BDH_TRY(gfast);
+  else
+    BDH_TRY(bf ? run_g<true>(ga, p.f.nt, BH, dout->dtype, v->dtype, s)
+               : run_g<false>(ga, p.f.nt, BH, dout->dtype, v->dtype, s));
 
   // 3. dQ (merged for self attention), dK.
   DqArgs da;

@@ -55,6 +55,9 @@ int sy_cold(const bdh_tensor4* q, const bdh_tensor4* k, const bdh_tensor4* v, co
 size_t sy_bwd_workspace(int64_t B, int64_t H, int64_t T, int64_t N);
 int sy_bwd_dv(const bdh_tensor4* q, const bdh_tensor4* v, const bdh_tensor4* dout, const bdh_tensor4* dv, void* ws,
               size_t ws_bytes, hipStream_t s);
+// Backward G = dS + dS^T (bf16, [B*H][tpad][tpad]) on the MFMA score kernel
+// (syrk.hip): bf16 dO and V, D a multiple of 64.
+int sy_bwd_g(const bdh_tensor4* dout, const bdh_tensor4* v, void* g, int64_t tpad, hipStream_t s);
 // Backward dQ = G X on the MFMA path (syrk.hip): bf16 X, self attention, no RoPE.
 int sy_dq(const void* g, int64_t tpad, const bdh_tensor4* x, const bdh_tensor4* out, hipStream_t s);
 

@@ -66,6 +66,9 @@ struct SyArgs {
   bf16_t* part;        // [nslab][ntl][nsplit][256*256] partial score tiles (bf16)
   bf16_t* qr;          // optional RoPE(x) copy
   int64_t r0, r1, r2;
+  bf16_t* g;           // G output [nslab][tpad][tpad] (G epilogue only)
+  int64_t tpad;
+  int tq;              // rows of the RoPE table
   uint32_t items[kSyMaxItems];
 };
 
@@ -112,50 +115,61 @@ __device__ __forceinline__ void sy_barrier() {
 // One asm block so the hazard spacing is explicit: a v_dot2 result is read
 // no sooner than three wait states after it is written (s_nop 2).  The
 // results overwrite the swapped copies, which are dead by then.
+// CONJ rotates by the negated angle, (x0 c + x1 s, x1 c - x0 s): the sign
+// modifier moves from the first pair of dot products to the second.
+#define SY_ROT_ASM(NA, NB)                                                                                   \
+  asm("v_alignbit_b32 %[s0], %[x0], %[x0], 16\n\t"                                                          \
+      "v_alignbit_b32 %[s1], %[x1], %[x1], 16\n\t"                                                          \
+      "v_alignbit_b32 %[s2], %[x2], %[x2], 16\n\t"                                                          \
+      "v_alignbit_b32 %[s3], %[x3], %[x3], 16\n\t"                                                          \
+      "v_dot2_f32_bf16 %[a0], %[x0], %[c0], 0" NA "\n\t"                                                    \
+      "v_dot2_f32_bf16 %[a1], %[x1], %[c1], 0" NA "\n\t"                                                    \
+      "v_dot2_f32_bf16 %[a2], %[x2], %[c2], 0" NA "\n\t"                                                    \
+      "v_dot2_f32_bf16 %[a3], %[x3], %[c3], 0" NA "\n\t"                                                    \
+      "v_dot2_f32_bf16 %[b0], %[s0], %[c0], 0" NB "\n\t"                                                    \
+      "v_dot2_f32_bf16 %[b1], %[s1], %[c1], 0" NB "\n\t"                                                    \
+      "v_dot2_f32_bf16 %[b2], %[s2], %[c2], 0" NB "\n\t"                                                    \
+      "v_dot2_f32_bf16 %[b3], %[s3], %[c3], 0" NB "\n\t"                                                    \
+      "s_nop 2\n\t"                                                                                         \
+      "v_cvt_pk_bf16_f32 %[s0], %[a0], %[b0]\n\t"                                                           \
+      "v_cvt_pk_bf16_f32 %[s1], %[a1], %[b1]\n\t"                                                           \
+      "v_cvt_pk_bf16_f32 %[s2], %[a2], %[b2]\n\t"                                                           \
+      "v_cvt_pk_bf16_f32 %[s3], %[a3], %[b3]"                                                                 \
+      : [s0] "=&v"(s0), [s1] "=&v"(s1), [s2] "=&v"(s2), [s3] "=&v"(s3), [a0] "=&v"(a0), [a1] "=&v"(a1),       \
+        [a2] "=&v"(a2), [a3] "=&v"(a3), [b0] "=&v"(b0), [b1] "=&v"(b1), [b2] "=&v"(b2), [b3] "=&v"(b3)         \
+      : [x0] "v"(x.x), [x1] "v"(x.y), [x2] "v"(x.z), [x3] "v"(x.w), [c0] "v"(cs.x), [c1] "v"(cs.y),           \
+        [c2] "v"(cs.z), [c3] "v"(cs.w))
+template <bool CONJ = false>
 __device__ __forceinline__ u32x4 rot_chunk(u32x4 x, u32x4 cs) {
   uint32_t s0, s1, s2, s3;
   float a0, a1, a2, a3, b0, b1, b2, b3;
-  asm("v_alignbit_b32 %[s0], %[x0], %[x0], 16\n\t"
-      "v_alignbit_b32 %[s1], %[x1], %[x1], 16\n\t"
-      "v_alignbit_b32 %[s2], %[x2], %[x2], 16\n\t"
-      "v_alignbit_b32 %[s3], %[x3], %[x3], 16\n\t"
-      "v_dot2_f32_bf16 %[a0], %[x0], %[c0], 0 neg_hi:[0,1,0]\n\t"
-      "v_dot2_f32_bf16 %[a1], %[x1], %[c1], 0 neg_hi:[0,1,0]\n\t"
-      "v_dot2_f32_bf16 %[a2], %[x2], %[c2], 0 neg_hi:[0,1,0]\n\t"
-      "v_dot2_f32_bf16 %[a3], %[x3], %[c3], 0 neg_hi:[0,1,0]\n\t"
-      "v_dot2_f32_bf16 %[b0], %[s0], %[c0], 0\n\t"
-      "v_dot2_f32_bf16 %[b1], %[s1], %[c1], 0\n\t"
-      "v_dot2_f32_bf16 %[b2], %[s2], %[c2], 0\n\t"
-      "v_dot2_f32_bf16 %[b3], %[s3], %[c3], 0\n\t"
-      "s_nop 2\n\t"
-      "v_cvt_pk_bf16_f32 %[s0], %[a0], %[b0]\n\t"
-      "v_cvt_pk_bf16_f32 %[s1], %[a1], %[b1]\n\t"
-      "v_cvt_pk_bf16_f32 %[s2], %[a2], %[b2]\n\t"
-      "v_cvt_pk_bf16_f32 %[s3], %[a3], %[b3]"
-      : [s0] "=&v"(s0), [s1] "=&v"(s1), [s2] "=&v"(s2), [s3] "=&v"(s3),
-        [a0] "=&v"(a0), [a1] "=&v"(a1), [a2] "=&v"(a2), [a3] "=&v"(a3),
-        [b0] "=&v"(b0), [b1] "=&v"(b1), [b2] "=&v"(b2), [b3] "=&v"(b3)
-      : [x0] "v"(x.x), [x1] "v"(x.y), [x2] "v"(x.z), [x3] "v"(x.w),
-        [c0] "v"(cs.x), [c1] "v"(cs.y), [c2] "v"(cs.z), [c3] "v"(cs.w));
+  if constexpr (CONJ)
+    SY_ROT_ASM("", " neg_hi:[0,1,0]");
+  else
+    SY_ROT_ASM(" neg_hi:[0,1,0]", "");
   return u32x4{s0, s1, s2, s3};
 }
+#undef SY_ROT_ASM
 
 __device__ __forceinline__ f32x16 mma(bf16x8 a, bf16x8 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
 // ------------------------------------------------------------------ kernels
-// RoPE table, stage-major: the (cos, sin) of pair m at position t sits in
-// dword ((m / 16) * T + t) * 16 + m % 16, so the table entries one k32 stage
-// of the score kernel needs for a 256-row block are one contiguous 16 KB run.
+// RoPE table, stage-major: the (cos, sin) of pair m at row t sits in dword
+// ((m / 16) * T + t) * 16 + m % 16, so the table entries one k32 stage of the
+// score kernel needs for a 256-row block are one contiguous 16 KB run.  Row t
+// is position rope_start + t (absolute table), or the half-integer distance
+// t + 0.5 (relative table: rows rotated about the centre of their tile).
 __global__ __launch_bounds__(256) void k_rope_table(const float* __restrict__ freqs, int64_t rope_start,
-                                                    int N2, int T, uint32_t* __restrict__ cs) {
+                                                    int N2, int T, bool half, uint32_t* __restrict__ cs) {
   const int t = blockIdx.y, m = blockIdx.x * 256 + threadIdx.x;
   if (m >= N2) return;
   // phase = fp32(pos) * freq, then cos/sin of 2 pi frac(phase); v_cos/v_sin
   // take the angle in revolutions, so frac(phase) goes in directly.  The
   // values are rounded to bf16, far above the hardware functions' error.
-  const float ph = __fmul_rn(float(rope_start + t), freqs[2 * m]);
+  const float pos = half ? float(t) + 0.5f : float(rope_start + t);
+  const float ph = __fmul_rn(pos, freqs[2 * m]);
   const float fr = ph - floorf(ph);
   cs[(int64_t(m >> 4) * T + t) * 16 + (m & 15)] = pack_bf2(__builtin_amdgcn_cosf(fr), __builtin_amdgcn_sinf(fr));
 }
@@ -203,10 +217,31 @@ struct SyProg {
   static constexpr int row(int k) { return WT == 0 ? 0 : kSyDiag[WT - 1].rows[k]; }
   static constexpr int bi(int m) { return WT == 0 ? 0 : kSyDiag[WT - 1].bi[m]; }
   static constexpr int bj(int m) { return WT == 0 ? 0 : kSyDiag[WT - 1].bj[m]; }
+  // Relative RoPE layout: the row group held by group slot g, and whether
+  // MFMA m runs with its operands swapped so its block stays below the
+  // diagonal.
+  static constexpr int grp(int g) { return g < 4 ? g : 11 - g; }
+  static constexpr bool swp(int m, bool rel) { return rel && WT != 0 && grp(bi(m)) < grp(bj(m)); }
 };
 
-template <bool ROPE, bool SELF>
+// RM: 0 no RoPE; 1 RoPE at absolute positions (table row t = position
+// rope_start + t); 2 RoPE relative to each tile's centre.  Scores depend only
+// on position differences, so rotating the rows of tile (ta, tb) by their
+// position minus c = (256 (ta + tb) + 255) / 2 leaves them unchanged; every
+// row then needs the angle of a half-integer distance q + 0.5, q < 128 nt,
+// and within a row block the row at LDS position P is block row P (P < 128)
+// or 383 - P (P >= 128), so the two rows a lane loads per block share q: one
+// table entry per lane and stage on diagonal items, two on full tiles (row
+// a of A and row 255 - a of B, rotated by the negated angle).  The table
+// moves at the lead of x through two 16 KB slots.
+// GOUT (with Q = dO, K = V, one split): instead of partial tiles, write the
+// backward's G = dS + dS^T, dS = tril(dO V^T, -1), into a.g.
+template <int RM, bool SELF, bool GOUT = false>
 __global__ __launch_bounds__(kSyThreads, 1) void k_sy_scores(const SyArgs a) {
+  constexpr bool ROPE = RM != 0;
+  constexpr bool REL = RM == 2;
+  static_assert(!GOUT || (!SELF && !ROPE), "G epilogue: distinct operands, no RoPE");
+  static_assert(!REL || SELF, "relative RoPE: self attention");
   const int bid = blockIdx.x;
   const int xcd = bid & 7, kk = bid >> 3;
   const int grp = kk / a.ips;
@@ -237,33 +272,53 @@ __global__ __launch_bounds__(kSyThreads, 1) void k_sy_scores(const SyArgs a) {
     const int q = (u * 8 + w) * 1024 + lane * 16;
     const int blk = q >> 14;
     const int ob = q & (kSyBlk - 1);
-    const int row = ob >> 6;
+    const int row = ob >> 6;  // LDS row position
     const int c = ((ob >> 4) & 3) ^ ((row >> 2) & 3);
-    const int rg = (blk == 0 ? ta : tb) * kSyTile + row;
+    const int brow = (REL && row >= 128) ? 383 - row : row;
+    const int rg = (blk == 0 ? ta : tb) * kSyTile + brow;
     const int rc = rg < a.T ? rg : a.T - 1;
     xoff[u] = uint32_t((int64_t(rc) * (blk == 0 ? a.q2 : (SELF ? a.q2 : a.k2)) + 8 * c) * 2);
     toff[u] = uint32_t(rc * 64 + 16 * c);
   }
-  // MFMA fragment offsets within a row block for the two k16 halves of a stage.
-  uint32_t loff[2];
+  // Relative table rows of this lane's chunks (rho: LDS row of chunk 0):
+  // diagonal items q = 127 - rho for all four chunks; full tiles
+  // q = 128 (ta - tb - 1) + rho (chunks 0 and 3) and + 255 - rho (1 and 2).
+  uint32_t trel[2] = {0u, 0u};
+  if constexpr (REL) {
+    const int rho = 16 * w + (lane >> 2);
+    const int cq = (lane & 3) ^ ((lane >> 4) & 3);
+    const int q0 = diag ? 127 - rho : 128 * (ta - tb - 1) + rho;
+    const int q1 = diag ? q0 : 128 * (ta - tb - 1) + 255 - rho;
+    trel[0] = uint32_t(q0 * 64 + 16 * cq);
+    trel[1] = uint32_t(q1 * 64 + 16 * cq);
+  }
+  // MFMA fragment offsets within a row block for the two k16 halves of a
+  // stage; lrev reads a 32-row group stored in reverse (REL upper half), so
+  // the fragment rows come out in block order.
+  uint32_t loff[2], lrev[2];
 #pragma unroll
   for (int kk2 = 0; kk2 < 2; ++kk2) {
     const int c = (2 * kk2 + (lane >> 5)) ^ ((lane >> 2) & 3);
     loff[kk2] = uint32_t((lane & 31) * 64 + c * 16);
+    const int ir = 31 - (lane & 31);
+    const int cr = (2 * kk2 + (lane >> 5)) ^ ((ir >> 2) & 3);
+    lrev[kk2] = uint32_t(ir * 64 + cr * 16);
   }
   // RoPE(x) copy: each row of a slab belongs to exactly one diagonal tile and
   // each k chunk to one split, so the diagonal items write it (the first row
   // block only for a single diagonal tile, which loads it twice).
-  const bool write_qr = ROPE && a.qr != nullptr && diag;
+  const bool write_qr = RM == 1 && a.qr != nullptr && diag;
 
   auto kofs = [&](int s) { return (split + S * (s >> 1)) * 64 + (s & 1) * 32; };
   // LDS: an x ring of NX slots, issued lead = NX - 1 stages ahead; with RoPE
-  // four x slots and one slot for the table entries of the next stage.
+  // four x slots and one slot for the table entries of the next stage
+  // (relative tables: two 16 KB slots, stage s in slot s & 1).
   constexpr int NX = ROPE ? 4 : 5;
   constexpr int lead = NX - 1;
   auto xslot_ofs = [&](int s) { return (s % NX) * kSySlot; };
   auto slot = [&](int s) { return sy_lds + xslot_ofs(s); };
-  auto tslot = [&](int) { return sy_lds + NX * kSySlot; };
+  auto tslot_ofs = [&](int s) { return NX * kSySlot + (REL ? (s & 1) * 16384 : 0); };
+  auto tslot = [&](int s) { return sy_lds + tslot_ofs(s); };
   // The DMA instructions of one stage: per-stage scalar bases, per-instruction
   // immediates (instruction u of wave w fills LDS bytes [(8u + w) KB, +1 KB)
   // of its slot).
@@ -278,9 +333,9 @@ __global__ __launch_bounds__(kSyThreads, 1) void k_sy_scores(const SyArgs a) {
     StageDma d;
     const int ko = kofs(min(st, nst - 1));
     d.xm0 = wl + uint32_t(xslot_ofs(st));
-    d.tm0 = wl + uint32_t(NX * kSySlot);
+    d.tm0 = wl + uint32_t(tslot_ofs(st));
     d.kx = uint32_t(ko * 2);
-    d.kt = uint32_t(ko >> 5) * uint32_t(a.T) * 64u;
+    d.kt = uint32_t(ko >> 5) * uint32_t(a.tq) * 64u;
     return d;
   };
   auto dma_x = [&](const StageDma& d, auto uc) {
@@ -289,15 +344,23 @@ __global__ __launch_bounds__(kSyThreads, 1) void k_sy_scores(const SyArgs a) {
   };
   auto dma_t = [&](const StageDma& d, auto ic) {
     constexpr int i = decltype(ic)::value;
-    dma16<i * 8192>(d.tm0, tbase, toff[i] + d.kt);
+    if constexpr (REL)
+      dma16<i * 8192>(d.tm0, tbase, trel[i] + d.kt);
+    else
+      dma16<i * 8192>(d.tm0, tbase, toff[i] + d.kt);
   };
   // RoPE in place of chunk u of stage s (this lane's own DMA chunk)
   // (the row and chunk of instruction u follow from the lane: row
   // (u & 1) * 128 + 16 w + lane / 4 of the block of tile row ta (u < 2) or tb,
   // chunk (lane & 3) ^ ((lane >> 4) & 3) of the 64-byte row)
+  // (REL: wave program WT 0 is a full tile, whose B rows (chunks 2, 3) turn by
+  // the negated angle; the others are diagonal tiles, whose rows below the
+  // centre (chunks 0, 2) do.)
   const int vrot = w * 1024 + lane * 16;
-  auto rot_store = [&](int s, int u, u32x4 x, u32x4 t) {
-    const u32x4 y = rot_chunk(x, t);
+  auto rot_store = [&](int s, auto wtc, auto uc, u32x4 x, u32x4 t) {
+    constexpr int u = decltype(uc)::value;
+    constexpr bool conj = REL && (decltype(wtc)::value == 0 ? u >= 2 : (u & 1) == 0);
+    const u32x4 y = rot_chunk<conj>(x, t);
     *reinterpret_cast<u32x4*>(slot(s) + vrot + u * 8192) = y;
     if (write_qr && (kind == kSyDiag2 || u < 2)) {
       const int rg = (u < 2 ? ta : tb) * kSyTile + (u & 1) * 128 + 16 * w + (lane >> 2);
@@ -306,9 +369,13 @@ __global__ __launch_bounds__(kSyThreads, 1) void k_sy_scores(const SyArgs a) {
         *reinterpret_cast<u32x4*>(a.qr + b * a.r0 + h * a.r1 + int64_t(rg) * a.r2 + kofs(s) + 8 * c) = y;
     }
   };
-  auto rot_load = [&](int s, int u, u32x4& x, u32x4& t) {
+  auto rot_load = [&](int s, auto wtc, auto uc, u32x4& x, u32x4& t) {
+    constexpr int u = decltype(uc)::value;
+    // table entry of chunk u: its own (absolute); REL full tiles 0, 1, 1, 0;
+    // REL diagonal tiles 0
+    constexpr int ti = !REL ? u : (decltype(wtc)::value == 0 ? ((u == 1 || u == 2) ? 1 : 0) : 0);
     x = *reinterpret_cast<const u32x4*>(slot(s) + vrot + u * 8192);
-    t = *reinterpret_cast<const u32x4*>(tslot(s) + vrot + u * 8192);
+    t = *reinterpret_cast<const u32x4*>(tslot(s) + vrot + ti * 8192);
   };
 
   // The wave program selects one of five instantiations of the whole pipeline
@@ -319,22 +386,27 @@ __global__ __launch_bounds__(kSyThreads, 1) void k_sy_scores(const SyArgs a) {
     using P = SyProg<WT>;
     constexpr int NF = P::nf, NM = P::nm;
     // Fragment addresses: a per-wave base (with the lane's offset) in a
-    // register, the fragment's row block as an immediate.  Full tile: A rows
-    // 4 wm + k at fbase[0], B rows 2 wn + j at fbase[1]; diagonal: row
-    // block P::row(k) of the wave's tile at fbase[0].
+    // register, the fragment's 32-row group slot g as an immediate.  Full
+    // tile: A slots 4 wm + k at fbase[0], B slots 2 wn + j at fbase[1];
+    // diagonal: slot P::row(k) of the wave's tile at fbase[0] (REL: slots
+    // g >= 4 at fbase[1]).  With REL, slot g >= 4 holds the row group
+    // 11 - g of the block, read through lrev.
     int fbase[2][2];  // [half][A, B]
     int tile_out;     // partial tile this wave writes (-1: none)
     if constexpr (WT == 0) {
       const int wm = w >> 2, wn = w & 3;
 #pragma unroll
       for (int hf = 0; hf < 2; ++hf) {
-        fbase[hf][0] = 4 * wm * 2048 + int(loff[hf]);
-        fbase[hf][1] = kSyBlk + 2 * wn * 2048 + int(loff[hf]);
+        fbase[hf][0] = 4 * wm * 2048 + int((REL && wm == 1) ? lrev[hf] : loff[hf]);
+        fbase[hf][1] = kSyBlk + 2 * wn * 2048 + int((REL && wn >= 2) ? lrev[hf] : loff[hf]);
       }
       tile_out = ta * (ta + 1) / 2 + tb;
     } else {
 #pragma unroll
-      for (int hf = 0; hf < 2; ++hf) fbase[hf][0] = fbase[hf][1] = (w >> 2) * kSyBlk + int(loff[hf]);
+      for (int hf = 0; hf < 2; ++hf) {
+        fbase[hf][0] = (w >> 2) * kSyBlk + int(loff[hf]);
+        fbase[hf][1] = (w >> 2) * kSyBlk + int(REL ? lrev[hf] : loff[hf]);
+      }
       const int t = w < 4 ? ta : tb;
       tile_out = (w < 4 || kind == kSyDiag2) ? t * (t + 1) / 2 + t : -1;
     }
@@ -344,6 +416,11 @@ __global__ __launch_bounds__(kSyThreads, 1) void k_sy_scores(const SyArgs a) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][r] = 0.f;
     bf16x8 f0[NF], f1[NF];
+    auto mfma_m = [&](bf16x8(&f)[NF], auto mc) {
+      constexpr int m = decltype(mc)::value;
+      constexpr bool sw = P::swp(m, REL);
+      acc[m] = mma(f[sw ? P::fb(m) : P::fa(m)], f[sw ? P::fa(m) : P::fb(m)], acc[m]);
+    };
     auto read_frags = [&](bf16x8(&f)[NF], int s, int half) {
       const uint8_t* pa = slot(s) + fbase[half][0];
       const uint8_t* pb = slot(s) + fbase[half][1];
@@ -352,7 +429,7 @@ __global__ __launch_bounds__(kSyThreads, 1) void k_sy_scores(const SyArgs a) {
         if constexpr (WT == 0)
           f[k] = *reinterpret_cast<const bf16x8*>(k < 4 ? pa + k * 2048 : pb + (k - 4) * 2048);
         else
-          f[k] = *reinterpret_cast<const bf16x8*>(pa + P::row(k) * 2048);
+          f[k] = *reinterpret_cast<const bf16x8*>((P::row(k) >= 4 ? pb : pa) + P::row(k) * 2048);
       });
     };
 
@@ -365,23 +442,46 @@ __global__ __launch_bounds__(kSyThreads, 1) void k_sy_scores(const SyArgs a) {
     using I1 = std::integral_constant<int, 1>;
     using I2 = std::integral_constant<int, 2>;
     using I3 = std::integral_constant<int, 3>;
-    for (int st = 0; st < lead - 1; ++st) {
-      const StageDma d = stage_dma(st);
-      sy_static_for<4>([&](auto uc) { dma_x(d, uc); });
-    }
-    {
+    // REL: per stage k the order is x chunks 0-1, the NT table entries of k,
+    // x chunks 2-3, so the table runs at the lead of x.
+    constexpr int NT = WT == 0 ? 2 : 1;
+    auto rotate_all = [&](int st) {
+      sy_static_for<4>([&](auto uc) {
+        u32x4 x, t;
+        rot_load(st, wt_tag, uc, x, t);
+        rot_store(st, wt_tag, uc, x, t);
+      });
+    };
+    if constexpr (REL) {
+      for (int st = 0; st < lead - 1; ++st) {
+        const StageDma d = stage_dma(st);
+        dma_x(d, I0());
+        dma_x(d, I1());
+        sy_static_for<NT>([&](auto ic) { dma_t(d, ic); });
+        dma_x(d, I2());
+        dma_x(d, I3());
+      }
+      const StageDma d = stage_dma(lead - 1);
+      dma_x(d, I0());
+      dma_x(d, I1());
+      sy_wait<(lead - 2) * (4 + NT) + 2>();  // stage 0 and its table landed
+      rotate_all(0);
+      sy_barrier();
+      sy_static_for<NT>([&](auto ic) { dma_t(d, ic); });
+      dma_x(d, I2());
+      dma_x(d, I3());
+    } else {
+      for (int st = 0; st < lead - 1; ++st) {
+        const StageDma d = stage_dma(st);
+        sy_static_for<4>([&](auto uc) { dma_x(d, uc); });
+      }
       const StageDma d = stage_dma(lead - 1);
       dma_x(d, I0());
       dma_x(d, I1());
       if constexpr (ROPE) {
         sy_static_for<4>([&](auto ic) { dma_t(stage_dma(0), ic); });
         sy_wait<0>();  // stage 0 and its table landed
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          u32x4 x, t;
-          rot_load(0, u, x, t);
-          rot_store(0, u, x, t);
-        }
+        rotate_all(0);
         sy_barrier();
         sy_static_for<4>([&](auto ic) { dma_t(stage_dma(1), ic); });
         dma_x(d, I2());
@@ -411,7 +511,9 @@ __global__ __launch_bounds__(kSyThreads, 1) void k_sy_scores(const SyArgs a) {
     // operations issued after the awaited ones at that wait: RoPE, after the
     // table of s+1: x chunks 2-3 of s + lead - 1 and 0-1 of s + lead; else,
     // after x of s+1: x of s+2 .. s+lead-1 and chunks 0-1 of s + lead
-    constexpr int NWAIT = ROPE ? 4 : (lead - 2) * 4 + 2;
+    // (REL: after x chunks 2-3 of s+1, stage s+2 with its table and chunks
+    // 0-1 of s + lead)
+    constexpr int NWAIT = REL ? (lead - 2) * (4 + NT) + 2 : ROPE ? 4 : (lead - 2) * 4 + 2;
     for (int s = 0; s + 1 < nst; ++s) {
       read_frags(f1, s, 1);
       __builtin_amdgcn_sched_barrier(0);
@@ -419,21 +521,21 @@ __global__ __launch_bounds__(kSyThreads, 1) void k_sy_scores(const SyArgs a) {
       u32x4 x[2], t[2];
       sy_static_for<NM>([&](auto mc) {
         constexpr int m = decltype(mc)::value;
-        acc[m] = mma(f0[P::fa(m)], f0[P::fb(m)], acc[m]);
+        mfma_m(f0, mc);
         if constexpr (m == 0) dma_x(d, I0());
         if constexpr (m == 2) dma_x(d, I1());
         if constexpr (m == KW) {
           sy_wait<NWAIT>();
           if constexpr (ROPE) {
-            rot_load(s + 1, 0, x[0], t[0]);
-            rot_load(s + 1, 1, x[1], t[1]);
+            rot_load(s + 1, wt_tag, I0(), x[0], t[0]);
+            rot_load(s + 1, wt_tag, I1(), x[1], t[1]);
           }
         }
         // rotation: chunk u after MFMA KW + 1 + u, two chunks in flight
         constexpr int u = m - KW - 1;
         if constexpr (ROPE && u >= 0 && u < 4) {
-          rot_store(s + 1, u, x[u & 1], t[u & 1]);
-          if constexpr (u + 2 < 4) rot_load(s + 1, u + 2, x[u & 1], t[u & 1]);
+          rot_store(s + 1, wt_tag, std::integral_constant<int, u>(), x[u & 1], t[u & 1]);
+          if constexpr (u + 2 < 4) rot_load(s + 1, wt_tag, std::integral_constant<int, u + 2>(), x[u & 1], t[u & 1]);
         }
       });
       if constexpr (ROPE && NM - KW - 1 < 4) {
@@ -441,40 +543,77 @@ __global__ __launch_bounds__(kSyThreads, 1) void k_sy_scores(const SyArgs a) {
         sy_static_for<4>([&](auto uc) {
           constexpr int u = decltype(uc)::value;
           if constexpr (u >= NM - KW - 1) {
-            rot_store(s + 1, u, x[u & 1], t[u & 1]);
-            if constexpr (u + 2 < 4) rot_load(s + 1, u + 2, x[u & 1], t[u & 1]);
+            rot_store(s + 1, wt_tag, uc, x[u & 1], t[u & 1]);
+            if constexpr (u + 2 < 4) rot_load(s + 1, wt_tag, std::integral_constant<int, u + 2>(), x[u & 1], t[u & 1]);
           }
         });
       }
       __builtin_amdgcn_sched_barrier(0);
       sy_barrier();
       read_frags(f0, s + 1, 0);
-      if constexpr (ROPE) {
+      if constexpr (REL) {
+        sy_static_for<NT>([&](auto ic) { dma_t(d, ic); });  // table of stage s + lead
+      } else if constexpr (ROPE) {
         const StageDma dt = stage_dma(s + 2);
         sy_static_for<4>([&](auto ic) { dma_t(dt, ic); });
       }
       __builtin_amdgcn_sched_barrier(0);
       sy_static_for<NM>([&](auto mc) {
         constexpr int m = decltype(mc)::value;
-        acc[m] = mma(f1[P::fa(m)], f1[P::fb(m)], acc[m]);
+        mfma_m(f1, mc);
         if constexpr (m == 1) dma_x(d, I2());
         if constexpr (m == 3) dma_x(d, I3());
       });
     }
     // last stage: nothing left to load or rotate
     read_frags(f1, nst - 1, 1);
-    sy_static_for<NM>([&](auto mc) {
-      constexpr int m = decltype(mc)::value;
-      acc[m] = mma(f0[P::fa(m)], f0[P::fb(m)], acc[m]);
-    });
-    sy_static_for<NM>([&](auto mc) {
-      constexpr int m = decltype(mc)::value;
-      acc[m] = mma(f1[P::fa(m)], f1[P::fb(m)], acc[m]);
-    });
+    sy_static_for<NM>([&](auto mc) { mfma_m(f0, mc); });
+    sy_static_for<NM>([&](auto mc) { mfma_m(f1, mc); });
     // the re-loads past the end must land before the workgroup's LDS is freed
     sy_wait<0>();
 
     // ------------------------------------------------------------ epilogue
+    if constexpr (GOUT) {
+      // Tile (ta, tb), ta >= tb, of dO V^T gives G's block (ta, tb) as stored
+      // and block (tb, ta) transposed.  On a diagonal tile only the elements
+      // below the diagonal count: blocks above it are written from their
+      // mirror, and the 32x32 blocks on it are masked per element.  Rows and
+      // columns at or past T are zero (G's padding); nothing at or past tpad
+      // is written.  Each element of G below tpad has exactly one writer.
+      bf16_t* g = a.g + int64_t(slab) * a.tpad * a.tpad;
+      const int tpad = int(a.tpad);
+      const bool dtile = ta == tb;
+      sy_static_for<NM>([&](auto mc) {
+        constexpr int m = decltype(mc)::value;
+        const int rb = 4 * (w >> 2) + (m >> 1), cb = 2 * (w & 3) + (m & 1);
+        if (dtile && rb < cb) return;
+        const bool dblk = dtile && rb == cb;
+        const int gc = tb * kSyTile + cb * 32 + (lane & 31);
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4) {
+          const int gr0 = ta * kSyTile + rb * 32 + 8 * q4 + 4 * (lane >> 5);
+          float v[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int gr = gr0 + e;
+            v[e] = (gr < a.T && gc < a.T && gc < gr) ? acc[m][4 * q4 + e] : 0.f;
+            if (gr < tpad && gc < tpad && (!dblk || gc <= gr)) g[int64_t(gr) * tpad + gc] = f2bf(v[e]);
+          }
+          if (gc < tpad && gr0 < tpad) {  // tpad % 4 == 0: all four rows in range
+            bf16_t* gt = g + int64_t(gc) * tpad + gr0;
+            if (!dblk) {
+              uint32_t wv[2] = {pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3])};
+              *reinterpret_cast<uint2*>(gt) = make_uint2(wv[0], wv[1]);
+            } else {
+#pragma unroll
+              for (int e = 0; e < 4; ++e)
+                if (gc < gr0 + e) gt[e] = f2bf(v[e]);
+            }
+          }
+        }
+      });
+      return;
+    }
     if (tile_out < 0) return;
     bf16_t* dst = a.part + ((int64_t(slab) * a.ntl + tile_out) * S + split) * kSyTileElems;
     // Partial tiles are stored as bf16 (halving their traffic; the scores are
@@ -485,11 +624,14 @@ __global__ __launch_bounds__(kSyThreads, 1) void k_sy_scores(const SyArgs a) {
       constexpr int m = decltype(mc)::value;
       int rb, cb;
       if constexpr (WT == 0) {
-        rb = 4 * (w >> 2) + (m >> 1);
-        cb = 2 * (w & 3) + (m & 1);
+        const int wm = w >> 2, wn = w & 3;
+        rb = (REL && wm == 1) ? 7 - (m >> 1) : 4 * wm + (m >> 1);
+        cb = (REL && wn >= 2) ? 11 - 2 * wn - (m & 1) : 2 * wn + (m & 1);
       } else {
-        rb = P::bi(m);
-        cb = P::bj(m);
+        constexpr int gi = REL ? P::grp(P::bi(m)) : P::bi(m);
+        constexpr int gj = REL ? P::grp(P::bj(m)) : P::bj(m);
+        rb = gi > gj ? gi : gj;
+        cb = gi > gj ? gj : gi;
       }
 #pragma unroll
       for (int r = 0; r < 16; r += 2) {
@@ -847,16 +989,18 @@ __global__ __launch_bounds__(256) void k_dv_sy(const DvsArgs a) {
 
 // ------------------------------------------------------------- score x V
 // out rows [64 rb, +64) of one (b,h) slab, all D (<= 256) columns.  Keys go
-// in chunks of 64.  The 256 threads first stage the chunk in LDS: the score
+// in chunks of 64.  The 512 threads first stage the chunk in LDS: the score
 // block (64 rows x 64 keys: the split sum of the partial rows in fp32, the
-// strict-lower mask, one rounding to bf16), each thread 16 keys of one row,
+// strict-lower mask, one rounding to bf16), each thread 8 keys of one row,
 // and the V rows of the chunk (64 x D, rounded to bf16), row-major as stored.
-// Wave w then multiplies them into columns [64 w, +64): 2 x 2 blocks of
-// 32 x 32, four k16 steps; A fragments are plain reads, B fragments (V,
-// contracting over its row index) ds_read_b64_tr_b16 reads.  The partial
-// rows and V rows of the next chunk are loaded before this chunk's MFMAs.
-// Score rows are 128 bytes with 16-byte chunk kc at kc ^ ((r >> 1) & 7); V
-// rows 512 bytes with chunk c at c ^ 4 (r & 3): both conflict free.
+// Wave w then multiplies keys [32 (w / 4), +32) of the chunk into columns
+// [64 (w % 4), +64): 2 x 2 blocks of 32 x 32, two k16 steps; A fragments are
+// plain reads, B fragments (V, contracting over its row index)
+// ds_read_b64_tr_b16 reads.  The two wave groups' sums are added through LDS
+// at the end.  The loads of the next PF chunks are in flight while a chunk is
+// processed.  Score rows are 128 bytes with 16-byte chunk kc at
+// kc ^ ((r >> 1) & 7); V rows 512 bytes with chunk c at c ^ 4 (r & 3): both
+// conflict free.
 struct SvArgs {
   const bf16_t* part;  // partial score tiles [slab][ntl][nsplit][256*256]
   View v;              // V (B, Hv, T, D)
@@ -865,9 +1009,10 @@ struct SvArgs {
 };
 
 template <typename TO, typename TV, int NS>
-__global__ __launch_bounds__(256) void k_sy_sv(const SvArgs a) {
+__global__ __launch_bounds__(512, 1) void k_sy_sv(const SvArgs a) {
   __shared__ __attribute__((aligned(16))) uint8_t blk[64 * 128];
   __shared__ __attribute__((aligned(16))) uint8_t vblk[64 * 512];
+  __shared__ __attribute__((aligned(16))) float red[4 * 64 * 64];  // group 1 sums [wave][value][lane]
   constexpr int VL = sizeof(TV) == 2 ? 1 : 2;  // 16-byte loads per 8 V elements
   const int rb = blockIdx.x, slab = blockIdx.y;
   const int b = slab / a.H, h = slab - b * a.H, hv = a.Hv == 1 ? 0 : h;
@@ -878,79 +1023,83 @@ __global__ __launch_bounds__(256) void k_sy_sv(const SvArgs a) {
   const bf16_t* pslab = a.part + int64_t(slab) * a.ntl * a.nsplit * kSyTileElems;
   const TV* vb = static_cast<const TV*>(a.v.p) + b * a.v.s0 + hv * a.v.s1;
 
-  // block builder: row lr, keys [lk, +16) of the chunk; V chunks e = tid + 256 u
-  const int lr = tid >> 2, lk = (tid & 3) * 16;
+  // block builder: row lr, keys [lk, +8) of the chunk; V rows vr0 + 16 u,
+  // 16-byte chunk vc of each (u = 0..3)
+  const int lr = tid >> 3, lk = (tid & 7) * 8;
   const int gi = r0 + lr;
   const int ti = min(gi, a.T - 1) >> 8;
   const bool row_ok = gi < a.T;
+  const int vr0 = tid >> 5, vc = tid & 31;
+  // Loads are unconditional, from clamped addresses: splits past nsplit
+  // re-read the last split (not summed), V rows past T re-read row T - 1 (their
+  // scores are zero), V chunks past D re-read the last chunk (their output
+  // columns are not stored).
+  const int vcc = min(vc, a.D / 8 - 1);
 
-  uint4 pr[NS][2];      // partial rows of the next chunk
-  uint4 vr[8][VL];      // V rows of the next chunk
-  auto load_chunk = [&](int ck) {
+  constexpr int PF = 2;
+  uint4 pr[PF][NS];    // partial rows of the chunks in flight
+  uint4 vr[PF][4][VL];  // V rows of the chunks in flight
+  auto load_chunk = [&](int ck, auto slotc) {
+    constexpr int k = decltype(slotc)::value;
     const int j0 = ck * 64;
     const int tile = ti * (ti + 1) / 2 + (j0 >> 8);
     const bf16_t* p = pslab + int64_t(tile) * a.nsplit * kSyTileElems + (gi & 255) * kSyTile + ((j0 + lk) & 255);
 #pragma unroll
     for (int sp = 0; sp < NS; ++sp)
+      pr[k][sp] = *reinterpret_cast<const uint4*>(p + int64_t(min(sp, a.nsplit - 1)) * kSyTileElems);
 #pragma unroll
-      for (int e = 0; e < 2; ++e)
-        pr[sp][e] = sp < a.nsplit ? *reinterpret_cast<const uint4*>(p + int64_t(sp) * kSyTileElems + 8 * e)
-                                  : uint4{0u, 0u, 0u, 0u};
+    for (int u = 0; u < 4; ++u) {
+      const TV* vp = vb + int64_t(min(j0 + vr0 + 16 * u, a.T - 1)) * a.v.s2 + 8 * vcc;
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const int e = tid + 256 * u, r = e >> 5, c = e & 31;
-      const int j = j0 + r;
-      const bool ok = j < kend && 8 * c < a.D;
-#pragma unroll
-      for (int l = 0; l < VL; ++l)
-        vr[u][l] = ok ? *reinterpret_cast<const uint4*>(vb + int64_t(j) * a.v.s2 + 8 * c + 4 * l) : uint4{0u, 0u, 0u, 0u};
+      for (int l = 0; l < VL; ++l) vr[k][u][l] = *reinterpret_cast<const uint4*>(vp + 4 * l);
     }
   };
   // split sum, mask (j < i, j < T), one rounding; then the V block as bf16
-  auto store_chunk = [&](int ck) {
+  auto store_chunk = [&](int ck, auto slotc) {
+    constexpr int k = decltype(slotc)::value;
     const int j0 = ck * 64 + lk;
+    float sacc[8];
 #pragma unroll
-    for (int e = 0; e < 2; ++e) {
-      float sacc[8];
+    for (int q = 0; q < 8; ++q) sacc[q] = 0.f;
 #pragma unroll
-      for (int q = 0; q < 8; ++q) sacc[q] = 0.f;
-#pragma unroll
-      for (int sp = 0; sp < NS; ++sp) {
-        const uint32_t xw[4] = {pr[sp][e].x, pr[sp][e].y, pr[sp][e].z, pr[sp][e].w};
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          sacc[2 * q] += __uint_as_float(xw[q] << 16);
-          sacc[2 * q + 1] += __uint_as_float(xw[q] & 0xffff0000u);
-        }
-      }
-      uint32_t pk[4];
+    for (int sp = 0; sp < NS; ++sp) {
+      if (sp >= a.nsplit) break;  // uniform
+      const uint32_t xw[4] = {pr[k][sp].x, pr[k][sp].y, pr[k][sp].z, pr[k][sp].w};
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const int j = j0 + 8 * e + 2 * q;
-        const float lo = (row_ok && j < gi) ? sacc[2 * q] : 0.f;
-        const float hi = (row_ok && j + 1 < gi) ? sacc[2 * q + 1] : 0.f;
-        pk[q] = pack_bf2(lo, hi);
+        sacc[2 * q] += __uint_as_float(xw[q] << 16);
+        sacc[2 * q + 1] += __uint_as_float(xw[q] & 0xffff0000u);
       }
-      const int kc = (lk >> 3) + e;
-      *reinterpret_cast<u32x4*>(blk + lr * 128 + ((kc ^ ((lr >> 1) & 7)) * 16)) = u32x4{pk[0], pk[1], pk[2], pk[3]};
     }
+    uint32_t pk[4];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const int e = tid + 256 * u, r = e >> 5, c = e & 31;
+    for (int q = 0; q < 4; ++q) {
+      const int j = j0 + 2 * q;
+      const float lo = (row_ok && j < gi) ? sacc[2 * q] : 0.f;
+      const float hi = (row_ok && j + 1 < gi) ? sacc[2 * q + 1] : 0.f;
+      pk[q] = pack_bf2(lo, hi);
+    }
+    const int kc = lk >> 3;
+    *reinterpret_cast<u32x4*>(blk + lr * 128 + ((kc ^ ((lr >> 1) & 7)) * 16)) = u32x4{pk[0], pk[1], pk[2], pk[3]};
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int r = vr0 + 16 * u, c = vc;
       u32x4 y;
       if constexpr (VL == 1) {
-        y = u32x4{vr[u][0].x, vr[u][0].y, vr[u][0].z, vr[u][0].w};
+        y = u32x4{vr[k][u][0].x, vr[k][u][0].y, vr[k][u][0].z, vr[k][u][0].w};
       } else {
-        const uint32_t f[8] = {vr[u][0].x, vr[u][0].y, vr[u][0].z, vr[u][0].w,
-                               vr[u][1].x, vr[u][1].y, vr[u][1].z, vr[u][1].w};
+        const uint32_t f[8] = {vr[k][u][0].x, vr[k][u][0].y, vr[k][u][0].z, vr[k][u][0].w,
+                               vr[k][u][1].x, vr[k][u][1].y, vr[k][u][1].z, vr[k][u][1].w};
         y = u32x4{pack_bf2(__uint_as_float(f[0]), __uint_as_float(f[1])), pack_bf2(__uint_as_float(f[2]), __uint_as_float(f[3])),
                   pack_bf2(__uint_as_float(f[4]), __uint_as_float(f[5])), pack_bf2(__uint_as_float(f[6]), __uint_as_float(f[7]))};
       }
       *reinterpret_cast<u32x4*>(vblk + r * 512 + ((c ^ (4 * (r & 3))) * 16)) = y;
     }
   };
+  // MFMA roles: key half kh of each chunk, output columns [64 wc, +64).
   // B fragments: group lane q addresses V row 16 ks + 8 (g / 2) + 4 t + q / 4,
-  // columns 64 w + 32 c + 16 (g % 2) + 4 (q % 4)
+  // columns 64 wc + 32 c + 16 (g % 2) + 4 (q % 4)
+  const int kh = w >> 2, wc = w & 3;
   const int g4 = lane >> 4, q = lane & 15;
   int boff[2];
   int dcol[2];
@@ -958,9 +1107,9 @@ __global__ __launch_bounds__(256) void k_sy_sv(const SvArgs a) {
 #pragma unroll
   for (int c = 0; c < 2; ++c) {
     const int row = 8 * (g4 >> 1) + (q >> 2);
-    const int cd = 64 * w + 32 * c + 16 * (g4 & 1) + 4 * (q & 3);
+    const int cd = 64 * wc + 32 * c + 16 * (g4 & 1) + 4 * (q & 3);
     boff[c] = row * 512 + (((cd >> 3) ^ (4 * (row & 3))) * 16) + ((cd >> 2) & 1) * 8;
-    dcol[c] = 64 * w + 32 * c + (lane & 31);
+    dcol[c] = 64 * wc + 32 * c + (lane & 31);
     dok[c] = dcol[c] < a.D;
   }
 
@@ -972,20 +1121,25 @@ __global__ __launch_bounds__(256) void k_sy_sv(const SvArgs a) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][c][r] = 0.f;
 
-  load_chunk(0);
-  for (int ck = 0; ck < nch; ++ck) {
+  sy_static_for<PF>([&](auto kc) {
+    if (int(decltype(kc)::value) < nch) load_chunk(int(decltype(kc)::value), kc);
+  });
+  for (int c0 = 0; c0 < nch; c0 += PF) sy_static_for<PF>([&](auto kc) {
+    const int ck = c0 + int(decltype(kc)::value);
+    if (ck >= nch) return;
     __syncthreads();  // the previous chunk's fragment reads are done
-    store_chunk(ck);
-    if (ck + 1 < nch) load_chunk(ck + 1);
+    store_chunk(ck, kc);
+    if (ck + PF < nch) load_chunk(ck + PF, kc);
     __syncthreads();
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
+    for (int k2 = 0; k2 < 2; ++k2) {
+      const int ks = 2 * kh + k2;
       bf16x8 fa[2], fb[2];
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
         const int row = 32 * i + (lane & 31);
-        const int kc = 2 * ks + (lane >> 5);
-        fa[i] = *reinterpret_cast<const bf16x8*>(blk + row * 128 + ((kc ^ ((row >> 1) & 7)) * 16));
+        const int kc2 = 2 * ks + (lane >> 5);
+        fa[i] = *reinterpret_cast<const bf16x8*>(blk + row * 128 + ((kc2 ^ ((row >> 1) & 7)) * 16));
       }
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
@@ -997,7 +1151,18 @@ __global__ __launch_bounds__(256) void k_sy_sv(const SvArgs a) {
 #pragma unroll
         for (int c = 0; c < 2; ++c) acc[i][c] = mma(fa[i], fb[c], acc[i][c]);
     }
+  });
+  // add the second key half's sums (waves 4-7) into the first's (waves 0-3)
+  if (kh == 1) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) red[(wc * 64 + (i * 2 + c) * 16 + r) * 64 + lane] = acc[i][c][r];
   }
+  __syncthreads();
+  if (kh == 1) return;
   TO* o = static_cast<TO*>(const_cast<void*>(a.o.p)) + b * a.o.s0 + h * a.o.s1;
 #pragma unroll
   for (int i = 0; i < 2; ++i)
@@ -1006,7 +1171,8 @@ __global__ __launch_bounds__(256) void k_sy_sv(const SvArgs a) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int row = r0 + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-        if (row < a.T && dok[c]) o[int64_t(row) * a.o.s2 + dcol[c]] = from_f<TO>(acc[i][c][r]);
+        const float val = acc[i][c][r] + red[(wc * 64 + (i * 2 + c) * 16 + r) * 64 + lane];
+        if (row < a.T && dok[c]) o[int64_t(row) * a.o.s2 + dcol[c]] = from_f<TO>(val);
       }
 }
 
@@ -1014,11 +1180,11 @@ template <typename TO, typename TV>
 int launch_sy_sv(const SvArgs& sa, dim3 grid, hipStream_t s) {
   const int ns = sa.nsplit;
   if (ns <= 2)
-    BDH_LAUNCH("k_sy_sv", (k_sy_sv<TO, TV, 2>), grid, dim3(256), 0, s, sa);
+    BDH_LAUNCH("k_sy_sv", (k_sy_sv<TO, TV, 2>), grid, dim3(512), 0, s, sa);
   else if (ns <= 4)
-    BDH_LAUNCH("k_sy_sv", (k_sy_sv<TO, TV, 4>), grid, dim3(256), 0, s, sa);
+    BDH_LAUNCH("k_sy_sv", (k_sy_sv<TO, TV, 4>), grid, dim3(512), 0, s, sa);
   else
-    BDH_LAUNCH("k_sy_sv", (k_sy_sv<TO, TV, 8>), grid, dim3(256), 0, s, sa);
+    BDH_LAUNCH("k_sy_sv", (k_sy_sv<TO, TV, 8>), grid, dim3(512), 0, s, sa);
   return BDH_OK;
 }
 
@@ -1038,7 +1204,7 @@ struct SyPlan {
 // the same two row blocks then load the same bytes at the same time and the
 // second load is served by the XCD's L2.  The split count is the smallest
 // that gives every CU a work item.
-SyPlan sy_plan(int64_t nslab, int64_t T, int64_t N, bool self, bool rope, int64_t Dv = 0) {
+SyPlan sy_plan(int64_t nslab, int64_t T, int64_t N, bool self, bool rope, int64_t Dv = 0, int max_split = 8) {
   SyPlan p;
   if (T <= 0 || N <= 0 || N % 64 != 0 || nslab <= 0) return p;
   p.nt = int((T + kSyTile - 1) / kSyTile);
@@ -1049,7 +1215,7 @@ SyPlan sy_plan(int64_t nslab, int64_t T, int64_t N, bool self, bool rope, int64_
   // one item per CU if that takes at most 8 splits, else the fewest that fill
   // every CU once
   const int64_t per_pass = nslab * per_split;
-  int S = int(std::max<int64_t>(1, std::min<int64_t>(8, 256 / per_pass)));
+  int S = int(std::max<int64_t>(1, std::min<int64_t>(max_split, 256 / per_pass)));
   S = std::min(S, p.nchunk);
   if (per_split * S > kSyMaxItems) return p;
   p.nsplit = S;
@@ -1066,7 +1232,8 @@ SyPlan sy_plan(int64_t nslab, int64_t T, int64_t N, bool self, bool rope, int64_
     }
   }
   p.ips = n;
-  p.table_bytes = rope ? align_up(size_t(T) * size_t(N / 2) * 4, 256) : 0;
+  // table rows: T positions (absolute) or 128 nt distances (relative)
+  p.table_bytes = rope ? align_up(size_t(std::max<int64_t>(T, 128 * p.nt)) * size_t(N / 2) * 4, 256) : 0;
   p.part_bytes = size_t(nslab) * size_t(p.ntl) * size_t(S) * kSyTileElems * sizeof(bf16_t);
   (void)Dv;
   p.ws_bytes = p.table_bytes + p.part_bytes;
@@ -1110,7 +1277,7 @@ int sy_cold(const bdh_tensor4* q, const bdh_tensor4* k, const bdh_tensor4* v, co
   // score x V: four waves x 64 columns, 8-element (16 / 32-byte) V row chunks
   if (v->size[3] > 256 || v->size[3] % 8 != 0 || !rows16(v)) return kNotEligible;
   if (((T - 1) * std::max(q->stride[2], k->stride[2]) + N) * 2 >= (int64_t(1) << 31)) return kNotEligible;
-  if (rope && int64_t(T) * N * 2 >= (int64_t(1) << 31)) return kNotEligible;
+  if (rope && std::max<int64_t>(T, 128 * ((T + kSyTile - 1) / kSyTile)) * N * 2 >= (int64_t(1) << 31)) return kNotEligible;
   if (T > 65535) return kNotEligible;
   if (qr != nullptr && (qr->dtype != BDH_BF16 || !rows16(qr))) return kNotEligible;
   const int64_t nslab = B * H;
@@ -1125,11 +1292,18 @@ int sy_cold(const bdh_tensor4* q, const bdh_tensor4* k, const bdh_tensor4* v, co
   uint8_t* wsb = static_cast<uint8_t*>(ws);
   uint32_t* table = rope ? reinterpret_cast<uint32_t*>(wsb) : nullptr;
   bf16_t* part = reinterpret_cast<bf16_t*>(wsb + p.table_bytes);
+  // Without the RoPE(x) copy the scores use the relative table (rows rotated
+  // about their tile's centre); the copy needs absolute positions.
+  const bool want_qr = qr != nullptr && numel4(qr) > 0;
+  const bool rel = rope && !want_qr;
+  const int tq = rel ? 128 * p.nt : int(T);
   if (rope) {
-    BDH_LAUNCH("k_rope_table", k_rope_table, dim3(unsigned((N / 2 + 255) / 256), unsigned(T)), dim3(256), 0, s,
-               freqs, rope_start, int(N / 2), int(T), table);
+    BDH_LAUNCH("k_rope_table", k_rope_table, dim3(unsigned((N / 2 + 255) / 256), unsigned(tq)), dim3(256), 0, s,
+               freqs, rope_start, int(N / 2), tq, rel, table);
   }
   SyArgs a;
+  a.g = nullptr;
+  a.tpad = 0;
   a.q = static_cast<const bf16_t*>(q->data);
   a.k = static_cast<const bf16_t*>(k->data);
   a.q0 = q->stride[0];
@@ -1147,10 +1321,11 @@ int sy_cold(const bdh_tensor4* q, const bdh_tensor4* k, const bdh_tensor4* v, co
   a.nsplit = p.nsplit;
   a.ntl = p.ntl;
   a.cs = table;
+  a.tq = tq;
   a.part = part;
   a.qr = nullptr;
   a.r0 = a.r1 = a.r2 = 0;
-  if (qr != nullptr && numel4(qr) > 0) {
+  if (want_qr) {
     a.qr = static_cast<bf16_t*>(qr->data);
     a.r0 = qr->stride[0];
     a.r1 = qr->stride[1];
@@ -1158,12 +1333,14 @@ int sy_cold(const bdh_tensor4* q, const bdh_tensor4* k, const bdh_tensor4* v, co
   }
   for (int i = 0; i < p.ips; ++i) a.items[i] = p.items[i];
   const dim3 gs{unsigned(grid_scores)};
-  if (rope)
-    BDH_LAUNCH("k_sy_scores", (k_sy_scores<true, true>), gs, dim3(kSyThreads), 0, s, a);
+  if (rel)
+    BDH_LAUNCH("k_sy_scores", (k_sy_scores<2, true>), gs, dim3(kSyThreads), 0, s, a);
+  else if (rope)
+    BDH_LAUNCH("k_sy_scores", (k_sy_scores<1, true>), gs, dim3(kSyThreads), 0, s, a);
   else if (self)
-    BDH_LAUNCH("k_sy_scores", (k_sy_scores<false, true>), gs, dim3(kSyThreads), 0, s, a);
+    BDH_LAUNCH("k_sy_scores", (k_sy_scores<0, true>), gs, dim3(kSyThreads), 0, s, a);
   else
-    BDH_LAUNCH("k_sy_scores", (k_sy_scores<false, false>), gs, dim3(kSyThreads), 0, s, a);
+    BDH_LAUNCH("k_sy_scores", (k_sy_scores<0, false>), gs, dim3(kSyThreads), 0, s, a);
   if (numel4(out) == 0) return BDH_OK;
 
   // score x V
@@ -1225,6 +1402,54 @@ int sy_dq(const void* g, int64_t tpad, const bdh_tensor4* x, const bdh_tensor4* 
 
 // dV for bf16 self attention without RoPE: the score tiles M by k_sy_scores
 // into ws, then k_dv_sy.  kNotEligible when the shapes fall outside it.
+// G = dS + dS^T with dS = tril(dO V^T, -1), bf16, into g [B*H][tpad][tpad]
+// (zero padding): the score kernel on Q = dO, K = V with one split (K = D)
+// and the G epilogue.  kNotEligible outside its shapes.
+int sy_bwd_g(const bdh_tensor4* dout, const bdh_tensor4* v, void* g, int64_t tpad, hipStream_t s) {
+  const int64_t B = dout->size[0], H = dout->size[1], T = dout->size[2], D = dout->size[3];
+  const int64_t Hv = v->size[1];
+  if (dout->dtype != BDH_BF16 || v->dtype != BDH_BF16) return kNotEligible;
+  if (v->size[0] != B || v->size[2] != T || v->size[3] != D || (Hv != 1 && Hv != H)) return kNotEligible;
+  if (T < 1 || T > 65535 || D < 64 || D % 64 != 0 || !rows16(dout) || !rows16(v)) return kNotEligible;
+  if (tpad < T || tpad % 4 != 0 || tpad > 65536) return kNotEligible;
+  if (((T - 1) * std::max(dout->stride[2], v->stride[2]) + D) * 2 >= (int64_t(1) << 31)) return kNotEligible;
+  const int64_t nslab = B * H;
+  if (nslab > (int64_t(1) << 24)) return kNotEligible;
+  const SyPlan p = sy_plan(nslab, T, D, false, false, 0, 1);
+  if (!p.ok || p.nsplit != 1) return kNotEligible;
+  const int64_t grid = 8 * ((nslab + 7) / 8) * p.ips;
+  if (grid >= (int64_t(1) << 31)) return kNotEligible;
+  SyArgs a;
+  a.g = nullptr;
+  a.tpad = 0;
+  a.q = static_cast<const bf16_t*>(dout->data);
+  a.q0 = dout->stride[0];
+  a.q1 = dout->stride[1];
+  a.q2 = dout->stride[2];
+  a.k = static_cast<const bf16_t*>(v->data);
+  a.k0 = v->stride[0];
+  a.k1 = Hv == 1 ? 0 : v->stride[1];
+  a.k2 = v->stride[2];
+  a.H = int(H);
+  a.T = int(T);
+  a.N = int(D);
+  a.nslab = int(nslab);
+  a.ips = p.ips;
+  a.nchunk = p.nchunk;
+  a.nsplit = 1;
+  a.ntl = p.ntl;
+  a.cs = nullptr;
+  a.part = nullptr;
+  a.qr = nullptr;
+  a.r0 = a.r1 = a.r2 = 0;
+  a.g = static_cast<bf16_t*>(g);
+  a.tpad = tpad;
+  a.tq = 0;
+  for (int i = 0; i < p.ips; ++i) a.items[i] = p.items[i];
+  BDH_LAUNCH("k_sy_scores_g", (k_sy_scores<0, false, true>), dim3{unsigned(grid)}, dim3(kSyThreads), 0, s, a);
+  return BDH_OK;
+}
+
 size_t sy_bwd_workspace(int64_t B, int64_t H, int64_t T, int64_t N) {
   const SyPlan p = sy_plan(B * H, T, N, true, false, 0);
   return p.ok ? p.part_bytes : 0;
@@ -1247,6 +1472,9 @@ int sy_bwd_dv(const bdh_tensor4* q, const bdh_tensor4* v, const bdh_tensor4* dou
   if (ws == nullptr || ws_bytes < p.part_bytes) return BDH_ERR_WORKSPACE;
   bf16_t* part = static_cast<bf16_t*>(ws);
   SyArgs a;
+  a.g = nullptr;
+  a.tpad = 0;
+  a.tq = 0;
   a.q = a.k = static_cast<const bf16_t*>(q->data);
   a.q0 = a.k0 = q->stride[0];
   a.q1 = a.k1 = q->stride[1];
@@ -1264,7 +1492,7 @@ int sy_bwd_dv(const bdh_tensor4* q, const bdh_tensor4* v, const bdh_tensor4* dou
   a.qr = nullptr;
   a.r0 = a.r1 = a.r2 = 0;
   for (int i = 0; i < p.ips; ++i) a.items[i] = p.items[i];
-  BDH_LAUNCH("k_sy_scores", (k_sy_scores<false, true>), dim3{unsigned(grid_scores)}, dim3(kSyThreads), 0, s, a);
+  BDH_LAUNCH("k_sy_scores", (k_sy_scores<0, true>), dim3{unsigned(grid_scores)}, dim3(kSyThreads), 0, s, a);
   if (numel4(dv) == 0) return BDH_OK;
   DvsArgs d;
   d.part = part;

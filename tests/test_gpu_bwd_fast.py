@@ -2,8 +2,9 @@
 (dQ = G X with transposing LDS reads of X) against the CPU oracle.
 
 Shapes qualify for that path (bf16, N a multiple of 256, no RoPE): ragged T
-(1, 31, 257, 520), several N tiles, per-head V, the permuted x_sparse view and
-an fp32 output.  Tolerance: bf16 2e-2 relative Frobenius.  At the C4 shape
+(1, 31, 130, 257, 520, 600), several N tiles, per-head V, the permuted x_sparse
+view and an fp32 output; with D a multiple of 64, G = dS + dS^T comes from the
+MFMA score kernel as well.  Tolerance: bf16 2e-2 relative Frobenius.  At the C4 shape
 (B=16 nh=4 T=1024 N=8192 D=256): exact homogeneity in dO and one slab against
 the oracle.
 """
@@ -33,6 +34,11 @@ SHAPES = [
     (2, 2, 31, 512, 24, 1),
     (1, 2, 257, 256, 64, 2),
     (1, 1, 520, 768, 32, 1),
+    # D a multiple of 64: G on the MFMA score kernel too (one 256-tile past tpad
+    # at T = 600, a single row at T = 1, D below 256)
+    (1, 2, 600, 256, 128, 2),
+    (2, 1, 1, 256, 64, 1),
+    (1, 1, 130, 512, 192, 1),
 ]
 
 

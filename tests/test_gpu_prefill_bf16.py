@@ -97,6 +97,23 @@ def test_bf16_fused_rope_matches_oracle(shape, start):
     assert rel_fro(np_of(qr), qr_want) <= 8e-3
 
 
+@pytest.mark.parametrize("shape,start", [((1, 2, 300, 256, 64), 0), ((2, 1, 520, 512, 32), 17), ((1, 1, 1, 64, 8), 3),
+                                         ((1, 1, 700, 256, 16), 5), ((1, 1, 1100, 128, 8), 2)])
+def test_bf16_fused_rope_relative_table_matches_oracle(shape, start):
+    """Without the RoPE(x) copy the kernel rotates each tile's rows about the
+    tile's centre (scores depend only on position differences): single and
+    paired diagonal tiles, full tiles at distances 1 to 4, rope_start > 0."""
+    B, H, T, N, D = shape
+    x = _bf(latent((B, H, T, N), 5))
+    v = _bf(normal((B, 1, T, D), 6))
+    freqs = O.get_freqs(N)
+    want, _ = O.tril_rope_score_v(x, v, freqs, start, bf16=True)
+    got = np_of(ext.tril_rope_score_v(to_dev(x, BF), to_dev(v, BF), torch.from_numpy(freqs).to(DEV), start))
+    print(f"rope relative {shape} start {start}: rel {rel_fro(got, want):.3e}", flush=True)
+    assert rel_fro(got, want) <= TOL[BF]
+    assert not got[:, :, 0].any()
+
+
 def test_bf16_fused_rope_full_c1_properties():
     """C1 at full size (B=8 nh=4 T=512 N=8192 D=256): size-independent checks.
 
