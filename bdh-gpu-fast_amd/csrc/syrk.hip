@@ -151,6 +151,31 @@ __device__ __forceinline__ u32x4 rot_chunk(u32x4 x, u32x4 cs) {
 }
 #undef SY_ROT_ASM
 
+// Two pairs of the rotation above (dwords x0, x1 with table dwords c0, c1),
+// so a chunk's rotation can be split between two MFMAs.
+#define SY_ROT2_ASM(NA, NB)                                                                          \
+  asm("v_alignbit_b32 %[s0], %[x0], %[x0], 16\n\t"                                                  \
+      "v_alignbit_b32 %[s1], %[x1], %[x1], 16\n\t"                                                  \
+      "v_dot2_f32_bf16 %[a0], %[x0], %[c0], 0" NA "\n\t"                                            \
+      "v_dot2_f32_bf16 %[a1], %[x1], %[c1], 0" NA "\n\t"                                            \
+      "v_dot2_f32_bf16 %[b0], %[s0], %[c0], 0" NB "\n\t"                                            \
+      "v_dot2_f32_bf16 %[b1], %[s1], %[c1], 0" NB "\n\t"                                            \
+      "s_nop 2\n\t"                                                                                 \
+      "v_cvt_pk_bf16_f32 %[s0], %[a0], %[b0]\n\t"                                                   \
+      "v_cvt_pk_bf16_f32 %[s1], %[a1], %[b1]"                                                         \
+      : [s0] "=&v"(y0), [s1] "=&v"(y1), [a0] "=&v"(a0), [a1] "=&v"(a1), [b0] "=&v"(b0), [b1] "=&v"(b1) \
+      : [x0] "v"(x0), [x1] "v"(x1), [c0] "v"(c0), [c1] "v"(c1))
+template <bool CONJ = false>
+__device__ __forceinline__ void rot_pairs(uint32_t x0, uint32_t x1, uint32_t c0, uint32_t c1, uint32_t& y0,
+                                          uint32_t& y1) {
+  float a0, a1, b0, b1;
+  if constexpr (CONJ)
+    SY_ROT2_ASM("", " neg_hi:[0,1,0]");
+  else
+    SY_ROT2_ASM(" neg_hi:[0,1,0]", "");
+}
+#undef SY_ROT2_ASM
+
 __device__ __forceinline__ f32x16 mma(bf16x8 a, bf16x8 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
@@ -223,6 +248,14 @@ struct SyProg {
   static constexpr int grp(int g) { return g < 4 ? g : 11 - g; }
   static constexpr bool swp(int m, bool rel) { return rel && WT != 0 && grp(bi(m)) < grp(bj(m)); }
 };
+
+// Relative RoPE: chunk u of wave program wt turns by the negated angle (full
+// tile B rows; diagonal rows below the centre), and reads table entry
+// sy_rot_tidx (absolute tables: one entry per chunk).
+template <bool REL>
+constexpr bool sy_rot_conj(int wt, int u) { return REL && (wt == 0 ? u >= 2 : (u & 1) == 0); }
+template <bool REL>
+constexpr int sy_rot_tidx(int wt, int u) { return !REL ? u : (wt == 0 ? ((u == 1 || u == 2) ? 1 : 0) : 0); }
 
 // RM: 0 no RoPE; 1 RoPE at absolute positions (table row t = position
 // rope_start + t); 2 RoPE relative to each tile's centre.  Scores depend only
@@ -357,10 +390,8 @@ __global__ __launch_bounds__(kSyThreads, 1) void k_sy_scores(const SyArgs a) {
   // the negated angle; the others are diagonal tiles, whose rows below the
   // centre (chunks 0, 2) do.)
   const int vrot = w * 1024 + lane * 16;
-  auto rot_store = [&](int s, auto wtc, auto uc, u32x4 x, u32x4 t) {
+  auto put_rot = [&](int s, auto uc, u32x4 y) {
     constexpr int u = decltype(uc)::value;
-    constexpr bool conj = REL && (decltype(wtc)::value == 0 ? u >= 2 : (u & 1) == 0);
-    const u32x4 y = rot_chunk<conj>(x, t);
     *reinterpret_cast<u32x4*>(slot(s) + vrot + u * 8192) = y;
     if (write_qr && (kind == kSyDiag2 || u < 2)) {
       const int rg = (u < 2 ? ta : tb) * kSyTile + (u & 1) * 128 + 16 * w + (lane >> 2);
@@ -369,13 +400,16 @@ __global__ __launch_bounds__(kSyThreads, 1) void k_sy_scores(const SyArgs a) {
         *reinterpret_cast<u32x4*>(a.qr + b * a.r0 + h * a.r1 + int64_t(rg) * a.r2 + kofs(s) + 8 * c) = y;
     }
   };
+  auto rot_store = [&](int s, auto wtc, auto uc, u32x4 x, u32x4 t) {
+    constexpr bool conj = sy_rot_conj<REL>(decltype(wtc)::value, decltype(uc)::value);
+    put_rot(s, uc, rot_chunk<conj>(x, t));
+  };
+  // (table entry of chunk u: its own (absolute); REL full tiles 0, 1, 1, 0;
+  // REL diagonal tiles 0)
   auto rot_load = [&](int s, auto wtc, auto uc, u32x4& x, u32x4& t) {
     constexpr int u = decltype(uc)::value;
-    // table entry of chunk u: its own (absolute); REL full tiles 0, 1, 1, 0;
-    // REL diagonal tiles 0
-    constexpr int ti = !REL ? u : (decltype(wtc)::value == 0 ? ((u == 1 || u == 2) ? 1 : 0) : 0);
     x = *reinterpret_cast<const u32x4*>(slot(s) + vrot + u * 8192);
-    t = *reinterpret_cast<const u32x4*>(tslot(s) + vrot + ti * 8192);
+    t = *reinterpret_cast<const u32x4*>(tslot(s) + vrot + sy_rot_tidx<REL>(decltype(wtc)::value, u) * 8192);
   };
 
   // The wave program selects one of five instantiations of the whole pipeline
@@ -514,38 +548,63 @@ __global__ __launch_bounds__(kSyThreads, 1) void k_sy_scores(const SyArgs a) {
     // (REL: after x chunks 2-3 of s+1, stage s+2 with its table and chunks
     // 0-1 of s + lead)
     constexpr int NWAIT = REL ? (lead - 2) * (4 + NT) + 2 : ROPE ? 4 : (lead - 2) * 4 + 2;
+    // RoPE: the wait for stage s+1 comes first, all four chunks and their
+    // table entries are read at once, and half a chunk is rotated after each
+    // of the first eight MFMAs (scheduling barriers keep that order, so the
+    // rotation's VALU work runs under the MFMAs).  Operations issued after
+    // the awaited ones: REL, stages s+2 .. s+lead-1 with their tables;
+    // absolute, x chunks 2-3 of s+2 after the table of s+1.
+    constexpr int NWAITR = REL ? (lead - 2) * (4 + NT) : 2;
+    constexpr int NTD = REL ? NT : 4;  // distinct table entries per lane and stage
     for (int s = 0; s + 1 < nst; ++s) {
       read_frags(f1, s, 1);
       __builtin_amdgcn_sched_barrier(0);
       const StageDma d = stage_dma(s + lead);
-      u32x4 x[2], t[2];
-      sy_static_for<NM>([&](auto mc) {
-        constexpr int m = decltype(mc)::value;
-        mfma_m(f0, mc);
-        if constexpr (m == 0) dma_x(d, I0());
-        if constexpr (m == 2) dma_x(d, I1());
-        if constexpr (m == KW) {
-          sy_wait<NWAIT>();
-          if constexpr (ROPE) {
-            rot_load(s + 1, wt_tag, I0(), x[0], t[0]);
-            rot_load(s + 1, wt_tag, I1(), x[1], t[1]);
-          }
-        }
-        // rotation: chunk u after MFMA KW + 1 + u, two chunks in flight
-        constexpr int u = m - KW - 1;
-        if constexpr (ROPE && u >= 0 && u < 4) {
-          rot_store(s + 1, wt_tag, std::integral_constant<int, u>(), x[u & 1], t[u & 1]);
-          if constexpr (u + 2 < 4) rot_load(s + 1, wt_tag, std::integral_constant<int, u + 2>(), x[u & 1], t[u & 1]);
-        }
-      });
-      if constexpr (ROPE && NM - KW - 1 < 4) {
-        // fewer MFMAs after the wait than chunks: rotate the rest here
+      if constexpr (ROPE) {
+        sy_wait<NWAITR>();
+        u32x4 x[4], t[NTD];
         sy_static_for<4>([&](auto uc) {
-          constexpr int u = decltype(uc)::value;
-          if constexpr (u >= NM - KW - 1) {
-            rot_store(s + 1, wt_tag, uc, x[u & 1], t[u & 1]);
-            if constexpr (u + 2 < 4) rot_load(s + 1, wt_tag, std::integral_constant<int, u + 2>(), x[u & 1], t[u & 1]);
+          x[decltype(uc)::value] = *reinterpret_cast<const u32x4*>(slot(s + 1) + vrot + decltype(uc)::value * 8192);
+        });
+        sy_static_for<NTD>([&](auto ic) {
+          t[decltype(ic)::value] = *reinterpret_cast<const u32x4*>(tslot(s + 1) + vrot + decltype(ic)::value * 8192);
+        });
+        __builtin_amdgcn_sched_barrier(0);
+        sy_static_for<NM>([&](auto mc) {
+          constexpr int m = decltype(mc)::value;
+          mfma_m(f0, mc);
+          if constexpr (m == 0) dma_x(d, I0());
+          if constexpr (m == 2) dma_x(d, I1());
+          if constexpr (m < 8) {
+            constexpr int u = m >> 1, hh = m & 1;
+            constexpr bool conj = sy_rot_conj<REL>(WT, u);
+            const u32x4 tt = t[sy_rot_tidx<REL>(WT, u)];
+            // (vector elements go through scalars: this clang lowers some
+            // element accesses of u32x4 as element 0)
+            if constexpr (hh == 0) {
+              const uint32_t x0 = x[u].x, x1 = x[u].y, c0 = tt.x, c1 = tt.y;
+              uint32_t y0, y1;
+              rot_pairs<conj>(x0, x1, c0, c1, y0, y1);
+              x[u].x = y0;
+              x[u].y = y1;
+            } else {
+              const uint32_t x2 = x[u].z, x3 = x[u].w, c2 = tt.z, c3 = tt.w;
+              uint32_t y2, y3;
+              rot_pairs<conj>(x2, x3, c2, c3, y2, y3);
+              x[u].z = y2;
+              x[u].w = y3;
+              put_rot(s + 1, std::integral_constant<int, u>(), x[u]);
+            }
           }
+          __builtin_amdgcn_sched_barrier(0);
+        });
+      } else {
+        sy_static_for<NM>([&](auto mc) {
+          constexpr int m = decltype(mc)::value;
+          mfma_m(f0, mc);
+          if constexpr (m == 0) dma_x(d, I0());
+          if constexpr (m == 2) dma_x(d, I1());
+          if constexpr (m == KW) sy_wait<NWAIT>();
         });
       }
       __builtin_amdgcn_sched_barrier(0);
