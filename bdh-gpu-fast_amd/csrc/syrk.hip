@@ -1069,9 +1069,12 @@ struct SvArgs {
 
 template <typename TO, typename TV, int NS>
 __global__ __launch_bounds__(512, 1) void k_sy_sv(const SvArgs a) {
-  __shared__ __attribute__((aligned(16))) uint8_t blk[64 * 128];
-  __shared__ __attribute__((aligned(16))) uint8_t vblk[64 * 512];
-  __shared__ __attribute__((aligned(16))) float red[4 * 64 * 64];  // group 1 sums [wave][value][lane]
+  // 64 KB: the score and V blocks during the chunk loop, then the second wave
+  // group's sums [wave][value][lane] (two workgroups fit a CU)
+  __shared__ __attribute__((aligned(16))) uint8_t sv_lds[4 * 64 * 64 * 4];
+  uint8_t* const blk = sv_lds;               // 64 x 128 bytes
+  uint8_t* const vblk = sv_lds + 64 * 128;   // 64 x 512 bytes
+  float* const red = reinterpret_cast<float*>(sv_lds);
   constexpr int VL = sizeof(TV) == 2 ? 1 : 2;  // 16-byte loads per 8 V elements
   const int rb = blockIdx.x, slab = blockIdx.y;
   const int b = slab / a.H, h = slab - b * a.H, hv = a.Hv == 1 ? 0 : h;
@@ -1212,6 +1215,7 @@ __global__ __launch_bounds__(512, 1) void k_sy_sv(const SvArgs a) {
     }
   });
   // add the second key half's sums (waves 4-7) into the first's (waves 0-3)
+  __syncthreads();  // the blocks' last fragment reads are done
   if (kh == 1) {
 #pragma unroll
     for (int i = 0; i < 2; ++i)
