@@ -35,6 +35,9 @@ __all__ = [
     "tril_decode",
     "tril_decode_hip",
     "tril_score_v_bwd",
+    "keeps_scores",
+    "tril_score_v_save",
+    "tril_score_v_bwd_saved",
     "tril_rope_score_v_bwd",
     "rope_rotate",
     "profile_enable",
@@ -57,6 +60,9 @@ EXPORTED_SYMBOLS = (
     "bdh_rope_rotate",
     "bdh_tril_score_v_bwd_workspace",
     "bdh_tril_score_v_bwd",
+    "bdh_tril_score_v_keeps_scores",
+    "bdh_tril_score_v_bwd_saved_workspace",
+    "bdh_tril_score_v_bwd_saved",
     "bdh_tril_rope_score_v_bwd_workspace",
     "bdh_tril_rope_score_v_bwd",
     "bdh_profile_enable",
@@ -106,6 +112,9 @@ def _load():
         "bdh_rope_rotate": (ctypes.c_int, [P, P, P, P, i32, vp]),
         "bdh_tril_score_v_bwd_workspace": (sz, [i64, i64, i64, i64, i64, i64, i32]),
         "bdh_tril_score_v_bwd": (ctypes.c_int, [P, P, P, P, P, P, P, vp, sz, vp]),
+        "bdh_tril_score_v_keeps_scores": (ctypes.c_int, [P, P, ctypes.POINTER(sz)]),
+        "bdh_tril_score_v_bwd_saved_workspace": (sz, [i64, i64, i64, i64, i64, i64, i32]),
+        "bdh_tril_score_v_bwd_saved": (ctypes.c_int, [P, P, P, P, P, vp, sz, vp, sz, vp]),
         "bdh_tril_rope_score_v_bwd_workspace": (sz, [i64, i64, i64, i64, i64, i64, i32]),
         "bdh_tril_rope_score_v_bwd": (ctypes.c_int, [P, P, P, fp, i64, P, P, vp, sz, vp]),
         "bdh_profile_enable": (None, [i32]),
@@ -223,6 +232,31 @@ def tril_score_v(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Ten
 tril_score_v_hip = tril_score_v
 
 
+def keeps_scores(x: torch.Tensor, v: torch.Tensor) -> bool:
+    """Whether ``tril_score_v(x, x, v)`` leaves reusable score tiles in its workspace."""
+    if not (x.is_cuda and v.is_cuda) or x.dim() != 4 or v.dim() != 4:
+        return False
+    return bool(_lib.bdh_tril_score_v_keeps_scores(ctypes.byref(_t4(x)), ctypes.byref(_t4(v)), None))
+
+
+def tril_score_v_save(x: torch.Tensor, v: torch.Tensor) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
+    """Self attention ``tril(x x^T, -1) v`` that also returns its workspace when
+    it holds the score tiles (:func:`keeps_scores`), for
+    :func:`tril_score_v_bwd_saved`; else ``(out, None)``."""
+    dev = _require_device(x, v)
+    B, H, T, N = x.shape
+    out = torch.empty(B, H, T, v.size(-1), dtype=x.dtype, device=dev)
+    with torch.cuda.device(dev):
+        need = _lib.bdh_tril_score_v_workspace(B, H, T, N, v.size(-1), _dtype_code(x))
+        ws, nb = _workspace(need, dev)
+        rc = _lib.bdh_tril_score_v(
+            ctypes.byref(_t4(x)), ctypes.byref(_t4(x)), ctypes.byref(_t4(v)), ctypes.byref(_t4(out)),
+            ws.data_ptr() if ws is not None else None, nb, _stream(dev),
+        )
+    _check(rc, "tril_score_v")
+    return out, (ws if keeps_scores(x, v) else None)
+
+
 def tril_rope_score_v(
     x: torch.Tensor,
     v: torch.Tensor,
@@ -313,6 +347,35 @@ def tril_score_v_bwd(
         )
     _check(rc, "tril_score_v_bwd")
     return dq, dk, dv
+
+
+def tril_score_v_bwd_saved(
+    x: torch.Tensor,
+    v: torch.Tensor,
+    dout: torch.Tensor,
+    scores: torch.Tensor,
+    *,
+    dx: Optional[torch.Tensor] = None,
+    dv: Optional[torch.Tensor] = None,
+) -> Tuple[torch.Tensor, torch.Tensor]:
+    """``(dx, dv)`` of self attention from the score tiles saved by
+    :func:`tril_score_v_save` on the same ``x`` (no recompute)."""
+    dev = _require_device(x, v, dout, scores, dx, dv)
+    B, H, T, N = x.shape
+    if dx is None:
+        dx = torch.empty_like(x, memory_format=torch.contiguous_format)
+    if dv is None:
+        dv = torch.empty_like(v, memory_format=torch.contiguous_format)
+    with torch.cuda.device(dev):
+        need = _lib.bdh_tril_score_v_bwd_saved_workspace(B, H, v.size(1), T, N, v.size(-1), _dtype_code(x))
+        ws, nb = _workspace(need, dev)
+        rc = _lib.bdh_tril_score_v_bwd_saved(
+            ctypes.byref(_t4(x)), ctypes.byref(_t4(v)), ctypes.byref(_t4(dout)), ctypes.byref(_t4(dx)),
+            ctypes.byref(_t4(dv)), scores.data_ptr(), scores.numel() * scores.element_size(),
+            ws.data_ptr() if ws is not None else None, nb, _stream(dev),
+        )
+    _check(rc, "tril_score_v_bwd_saved")
+    return dx, dv
 
 
 def tril_rope_score_v_bwd(

@@ -233,13 +233,15 @@ struct BwdPlan {
   size_t g_off, ws_bytes;
 };
 
-BwdPlan plan_bwd(int64_t B, int64_t H, int64_t T, int64_t K, bool bf) {
+// saved: the score tiles come from the forward's workspace, so the first
+// region is not needed.
+BwdPlan plan_bwd(int64_t B, int64_t H, int64_t T, int64_t K, bool bf, bool saved = false) {
   BwdPlan p;
   p.f = plan_fwd(B, H, T, K, bf);
   p.tpad = p.f.nt * kTile;
   // the first region holds the generic M^T partials or the bf16 score tiles
   // of the MFMA path, whichever is larger
-  p.g_off = align_up(std::max(p.f.ws_bytes, bf ? sy_bwd_workspace(B, H, T, K) : size_t(0)), 256);
+  p.g_off = saved ? 0 : align_up(std::max(p.f.ws_bytes, bf ? sy_bwd_workspace(B, H, T, K) : size_t(0)), 256);
   p.ws_bytes = p.g_off + size_t(B * H) * size_t(p.tpad) * size_t(p.tpad) * (bf ? 2 : 4);
   return p;
 }
@@ -334,21 +336,24 @@ int check_bwd(const bdh_tensor4* q, const bdh_tensor4* k, const bdh_tensor4* v, 
 
 int run_bwd(const bdh_tensor4* q, const bdh_tensor4* k, const bdh_tensor4* v, const bdh_tensor4* dout,
             const bdh_tensor4* dq, const bdh_tensor4* dk, const bdh_tensor4* dv, const float* freqs,
-            int64_t rope_start, void* ws, size_t ws_bytes, hipStream_t s) {
+            int64_t rope_start, void* ws, size_t ws_bytes, hipStream_t s, const void* saved = nullptr) {
   const int64_t B = q->size[0], H = q->size[1], T = q->size[2], N = q->size[3];
   const int64_t Hv = v->size[1], Dv = v->size[3];
   const bool bf = q->dtype == BDH_BF16;
   const bool self = (k == nullptr);
   const bool rope = freqs != nullptr;
   if (numel4(dq) == 0 && numel4(dv) == 0) return BDH_OK;
-  const BwdPlan p = plan_bwd(B, H, T, N, bf);
+  if (saved != nullptr && !(self && bf && !rope)) return BDH_ERR_ARG;
+  const BwdPlan p = plan_bwd(B, H, T, N, bf, saved != nullptr);
   if (ws == nullptr || ws_bytes < p.ws_bytes) return BDH_ERR_WORKSPACE;
   const int64_t BH = B * H;
 
   // bf16 self attention without RoPE: score tiles by the forward score kernel
-  // and dV from them (syrk.hip), in place of steps 1 and 4 below
+  // (or saved by the forward) and dV from them (syrk.hip), in place of steps
+  // 1 and 4 below
   int fast_dv = kNotEligible;
-  if (self && bf && !rope) fast_dv = sy_bwd_dv(q, v, dout, dv, ws, p.g_off, s);
+  if (self && bf && !rope) fast_dv = sy_bwd_dv(q, v, dout, dv, ws, p.g_off, s, saved);
+  if (saved != nullptr && fast_dv == kNotEligible) return BDH_ERR_ARG;  // the saved tiles are unusable here
   if (fast_dv != kNotEligible && fast_dv != BDH_OK) return fast_dv;
 
   // 1. M^T partial tiles.
@@ -480,6 +485,34 @@ extern "C" int bdh_tril_score_v_bwd(const bdh_tensor4* q, const bdh_tensor4* k, 
   BDH_TRY(check_bwd(q, k, v, dout, dq, dk, dv));
   return run_bwd(q, k, v, dout, dq, dk, dv, nullptr, 0, workspace, workspace_bytes,
                  static_cast<hipStream_t>(stream));
+}
+
+extern "C" int bdh_tril_score_v_keeps_scores(const bdh_tensor4* q, const bdh_tensor4* v, size_t* scores_bytes) {
+  size_t nb = 0;
+  const bool keep = check_view(q) == BDH_OK && check_view(v) == BDH_OK && v->size[0] == q->size[0] &&
+                    v->size[2] == q->size[2] && (v->size[1] == 1 || v->size[1] == q->size[1]) &&
+                    sy_keeps_scores(q, v, &nb);
+  if (scores_bytes) *scores_bytes = keep ? nb : 0;
+  return keep ? 1 : 0;
+}
+
+extern "C" size_t bdh_tril_score_v_bwd_saved_workspace(int64_t B, int64_t H, int64_t Hv, int64_t T, int64_t N,
+                                                       int64_t Dv, int32_t x_dtype) {
+  (void)Hv;
+  (void)Dv;
+  return plan_bwd(B, H, T, N, x_dtype == BDH_BF16, true).ws_bytes;
+}
+
+extern "C" int bdh_tril_score_v_bwd_saved(const bdh_tensor4* x, const bdh_tensor4* v, const bdh_tensor4* dout,
+                                          const bdh_tensor4* dx, const bdh_tensor4* dv, const void* scores,
+                                          size_t scores_bytes, void* workspace, size_t workspace_bytes,
+                                          bdh_stream stream) {
+  BDH_TRY(check_bwd(x, nullptr, v, dout, dx, nullptr, dv));
+  size_t need = 0;
+  if (scores == nullptr || !sy_keeps_scores(x, v, &need)) return BDH_ERR_ARG;
+  if (scores_bytes < need) return BDH_ERR_WORKSPACE;
+  return run_bwd(x, nullptr, v, dout, dx, nullptr, dv, nullptr, 0, workspace, workspace_bytes,
+                 static_cast<hipStream_t>(stream), scores);
 }
 
 extern "C" size_t bdh_tril_rope_score_v_bwd_workspace(int64_t B, int64_t H, int64_t Hv, int64_t T,

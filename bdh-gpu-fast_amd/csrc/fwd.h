@@ -53,8 +53,13 @@ int sy_cold(const bdh_tensor4* q, const bdh_tensor4* k, const bdh_tensor4* v, co
 // Backward dV on the MFMA path (syrk.hip): score tiles recomputed by the
 // forward score kernel into ws (sy_bwd_workspace bytes), then dV from them.
 size_t sy_bwd_workspace(int64_t B, int64_t H, int64_t T, int64_t N);
+// saved: the score tiles left by the forward on the same q (its workspace), used
+// instead of recomputing them (then ws may be NULL).
 int sy_bwd_dv(const bdh_tensor4* q, const bdh_tensor4* v, const bdh_tensor4* dout, const bdh_tensor4* dv, void* ws,
-              size_t ws_bytes, hipStream_t s);
+              size_t ws_bytes, hipStream_t s, const void* saved = nullptr);
+// Whether bdh_tril_score_v(q, q, v) runs the MFMA path; its workspace then
+// starts with the score tiles (*scores_bytes of them) that sy_bwd_dv can reuse.
+bool sy_keeps_scores(const bdh_tensor4* q, const bdh_tensor4* v, size_t* scores_bytes);
 // Backward G = dS + dS^T (bf16, [B*H][tpad][tpad]) on the MFMA score kernel
 // (syrk.hip): bf16 dO and V, D a multiple of 64.
 int sy_bwd_g(const bdh_tensor4* dout, const bdh_tensor4* v, void* g, int64_t tpad, hipStream_t s);

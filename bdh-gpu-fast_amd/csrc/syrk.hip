@@ -1327,29 +1327,51 @@ size_t sy_workspace(int64_t B, int64_t H, int64_t T, int64_t N, int64_t Dv, bool
   return p.ok ? std::max(p.ws_bytes, p2.ok ? p2.ws_bytes : size_t(0)) : 0;
 }
 
+namespace {
+
+// Eligibility of the MFMA forward path, and its plan.
+bool sy_cold_check(const bdh_tensor4* q, const bdh_tensor4* k, const bdh_tensor4* v, bool rope,
+                   const bdh_tensor4* qr, SyPlan& p, bool& self) {
+  const int64_t B = q->size[0], H = q->size[1], T = q->size[2], N = q->size[3];
+  if (q->dtype != BDH_BF16 || k->dtype != BDH_BF16) return false;
+  self = q->data == k->data && q->stride[0] == k->stride[0] && q->stride[1] == k->stride[1] &&
+         q->stride[2] == k->stride[2];
+  if (rope && !self) return false;
+  if (T < 1 || N < 64 || N % 64 != 0 || !rows16(q) || !rows16(k)) return false;
+  // score x V: 8-element (16 / 32-byte) V row chunks, at most 256 columns
+  if (v->size[3] > 256 || v->size[3] % 8 != 0 || !rows16(v)) return false;
+  if (((T - 1) * std::max(q->stride[2], k->stride[2]) + N) * 2 >= (int64_t(1) << 31)) return false;
+  if (rope && std::max<int64_t>(T, 128 * ((T + kSyTile - 1) / kSyTile)) * N * 2 >= (int64_t(1) << 31)) return false;
+  if (T > 65535) return false;
+  if (qr != nullptr && (qr->dtype != BDH_BF16 || !rows16(qr))) return false;
+  const int64_t nslab = B * H;
+  if (nslab > (int64_t(1) << 24)) return false;
+  p = sy_plan(nslab, T, N, self, rope, v->size[3]);
+  if (!p.ok) return false;
+  return 8 * ((nslab + 7) / 8) * p.ips < (int64_t(1) << 31);
+}
+
+}  // namespace
+
+bool sy_keeps_scores(const bdh_tensor4* q, const bdh_tensor4* v, size_t* scores_bytes) {
+  SyPlan p;
+  bool self = false;
+  if (v->size[3] < 1 || !sy_cold_check(q, q, v, false, nullptr, p, self) || !self) return false;
+  if (scores_bytes) *scores_bytes = p.part_bytes;
+  return true;
+}
+
 int sy_cold(const bdh_tensor4* q, const bdh_tensor4* k, const bdh_tensor4* v, const bdh_tensor4* out,
             const float* freqs, int64_t rope_start, const bdh_tensor4* qr, void* ws, size_t ws_bytes,
             hipStream_t s) {
   const int64_t B = q->size[0], H = q->size[1], T = q->size[2], N = q->size[3];
-  if (q->dtype != BDH_BF16 || k->dtype != BDH_BF16) return kNotEligible;
-  const bool self = q->data == k->data && q->stride[0] == k->stride[0] && q->stride[1] == k->stride[1] &&
-                    q->stride[2] == k->stride[2];
   const bool rope = freqs != nullptr;
-  if (rope && !self) return kNotEligible;
-  if (T < 1 || N < 64 || N % 64 != 0 || !rows16(q) || !rows16(k)) return kNotEligible;
-  // score x V: four waves x 64 columns, 8-element (16 / 32-byte) V row chunks
-  if (v->size[3] > 256 || v->size[3] % 8 != 0 || !rows16(v)) return kNotEligible;
-  if (((T - 1) * std::max(q->stride[2], k->stride[2]) + N) * 2 >= (int64_t(1) << 31)) return kNotEligible;
-  if (rope && std::max<int64_t>(T, 128 * ((T + kSyTile - 1) / kSyTile)) * N * 2 >= (int64_t(1) << 31)) return kNotEligible;
-  if (T > 65535) return kNotEligible;
-  if (qr != nullptr && (qr->dtype != BDH_BF16 || !rows16(qr))) return kNotEligible;
+  SyPlan p;
+  bool self = false;
+  if (!sy_cold_check(q, k, v, rope, qr, p, self)) return kNotEligible;
   const int64_t nslab = B * H;
-  if (nslab > (int64_t(1) << 24)) return kNotEligible;
   const int64_t Dv = v->size[3];
-  SyPlan p = sy_plan(nslab, T, N, self, rope, Dv);
-  if (!p.ok) return kNotEligible;
   const int64_t grid_scores = 8 * ((nslab + 7) / 8) * p.ips;
-  if (grid_scores >= (int64_t(1) << 31)) return kNotEligible;
   if (ws == nullptr || ws_bytes < p.ws_bytes) return BDH_ERR_WORKSPACE;
 
   uint8_t* wsb = static_cast<uint8_t*>(ws);
@@ -1519,7 +1541,7 @@ size_t sy_bwd_workspace(int64_t B, int64_t H, int64_t T, int64_t N) {
 }
 
 int sy_bwd_dv(const bdh_tensor4* q, const bdh_tensor4* v, const bdh_tensor4* dout, const bdh_tensor4* dv, void* ws,
-              size_t ws_bytes, hipStream_t s) {
+              size_t ws_bytes, hipStream_t s, const void* saved) {
   const int64_t B = q->size[0], H = q->size[1], T = q->size[2], N = q->size[3];
   const int64_t Hv = v->size[1], D = v->size[3];
   if (q->dtype != BDH_BF16 || dout->dtype != BDH_BF16) return kNotEligible;
@@ -1532,30 +1554,34 @@ int sy_bwd_dv(const bdh_tensor4* q, const bdh_tensor4* v, const bdh_tensor4* dou
   if (!p.ok) return kNotEligible;
   const int64_t grid_scores = 8 * ((nslab + 7) / 8) * p.ips;
   if (grid_scores >= (int64_t(1) << 31)) return kNotEligible;
-  if (ws == nullptr || ws_bytes < p.part_bytes) return BDH_ERR_WORKSPACE;
-  bf16_t* part = static_cast<bf16_t*>(ws);
-  SyArgs a;
-  a.g = nullptr;
-  a.tpad = 0;
-  a.tq = 0;
-  a.q = a.k = static_cast<const bf16_t*>(q->data);
-  a.q0 = a.k0 = q->stride[0];
-  a.q1 = a.k1 = q->stride[1];
-  a.q2 = a.k2 = q->stride[2];
-  a.H = int(H);
-  a.T = int(T);
-  a.N = int(N);
-  a.nslab = int(nslab);
-  a.ips = p.ips;
-  a.nchunk = p.nchunk;
-  a.nsplit = p.nsplit;
-  a.ntl = p.ntl;
-  a.cs = nullptr;
-  a.part = part;
-  a.qr = nullptr;
-  a.r0 = a.r1 = a.r2 = 0;
-  for (int i = 0; i < p.ips; ++i) a.items[i] = p.items[i];
-  BDH_LAUNCH("k_sy_scores", (k_sy_scores<0, true>), dim3{unsigned(grid_scores)}, dim3(kSyThreads), 0, s, a);
+  // saved: the score tiles of the forward on the same q (its workspace),
+  // used in place of a recompute
+  if (saved == nullptr && (ws == nullptr || ws_bytes < p.part_bytes)) return BDH_ERR_WORKSPACE;
+  bf16_t* part = saved ? static_cast<bf16_t*>(const_cast<void*>(saved)) : static_cast<bf16_t*>(ws);
+  if (saved == nullptr) {
+    SyArgs a;
+    a.g = nullptr;
+    a.tpad = 0;
+    a.tq = 0;
+    a.q = a.k = static_cast<const bf16_t*>(q->data);
+    a.q0 = a.k0 = q->stride[0];
+    a.q1 = a.k1 = q->stride[1];
+    a.q2 = a.k2 = q->stride[2];
+    a.H = int(H);
+    a.T = int(T);
+    a.N = int(N);
+    a.nslab = int(nslab);
+    a.ips = p.ips;
+    a.nchunk = p.nchunk;
+    a.nsplit = p.nsplit;
+    a.ntl = p.ntl;
+    a.cs = nullptr;
+    a.part = part;
+    a.qr = nullptr;
+    a.r0 = a.r1 = a.r2 = 0;
+    for (int i = 0; i < p.ips; ++i) a.items[i] = p.items[i];
+    BDH_LAUNCH("k_sy_scores", (k_sy_scores<0, true>), dim3{unsigned(grid_scores)}, dim3(kSyThreads), 0, s, a);
+  }
   if (numel4(dv) == 0) return BDH_OK;
   DvsArgs d;
   d.part = part;

@@ -87,18 +87,42 @@ class StrictTrilAttnFn(torch.autograd.Function):
         return dQ, dK, dV, None
 
 
+def _save_scores() -> bool:
+    """``BDH_ATTN_SAVE_SCORES`` (default on): the hip forward keeps its score
+    tiles for the backward instead of the backward recomputing them."""
+    return os.environ.get("BDH_ATTN_SAVE_SCORES", "1").strip().lower() not in ("0", "false", "no", "off")
+
+
 class StrictTrilSelfAttnFn(torch.autograd.Function):
-    """Self-attention form (K is Q): returns dQ + dK for Q (reference :259-291)."""
+    """Self-attention form (K is Q): returns dQ + dK for Q (reference :259-291).
+
+    With ``impl="hip"`` the forward's bf16 score tiles are kept for the
+    backward when the shapes allow it (the reference's default autograd path
+    keeps S too); otherwise the backward recomputes them.
+    """
 
     @staticmethod
     def forward(ctx, Q, V, impl: str):  # type: ignore[override]
         ctx.impl = impl
-        ctx.save_for_backward(Q, V)
+        scores = None
         with torch.no_grad():
-            return _forward_impl(Q, Q, V, impl)
+            if _use_blocked_analytic_bwd(impl) and _save_scores():
+                out, scores = hip_attn.tril_score_v_save(Q, V)
+            else:
+                out = _forward_impl(Q, Q, V, impl)
+        ctx.has_scores = scores is not None
+        if scores is not None:
+            ctx.save_for_backward(Q, V, scores)
+        else:
+            ctx.save_for_backward(Q, V)
+        return out
 
     @staticmethod
     def backward(ctx, dO):  # type: ignore[override]
+        if ctx.has_scores:
+            Q, V, scores = ctx.saved_tensors
+            dQm, dV = hip_attn.tril_score_v_bwd_saved(Q, V, dO.to(Q.dtype), scores)
+            return dQm, dV.to(V.dtype), None
         Q, V = ctx.saved_tensors
         if _use_blocked_analytic_bwd(ctx.impl):
             dQm, _, dV = hip_attn.tril_score_v_bwd(Q, None, V, dO.to(Q.dtype))

@@ -139,6 +139,20 @@ def tril_score_v_bwd(q, k, v, dout):
     )
 
 
+def tril_score_v_save(x: torch.Tensor, v: torch.Tensor):
+    """Self-attention forward that also returns its score tiles for the backward
+    (``(out, scores)``; ``scores`` is None when the shapes take another path)."""
+    _check_cold_shapes(x, x, v)
+    ext = _require(x, v)
+    return ext.tril_score_v_save(_last_dim_unit(x), _last_dim_unit(v))
+
+
+def tril_score_v_bwd_saved(x, v, dout, scores):
+    """Merged dx and dv from the score tiles saved by :func:`tril_score_v_save`."""
+    ext = _require(x, v, dout, scores)
+    return ext.tril_score_v_bwd_saved(_last_dim_unit(x), _last_dim_unit(v), _last_dim_unit(dout), scores)
+
+
 def tril_rope_score_v_bwd(x, v, dout, freqs, rope_start: int = 0):
     ext = _require(x, v, dout)
     return ext.tril_rope_score_v_bwd(

@@ -134,6 +134,31 @@ int bdh_tril_score_v_bwd(const bdh_tensor4* q, const bdh_tensor4* k,
                          size_t workspace_bytes, bdh_stream stream);
 
 /*
+ * Self-attention backward from saved scores: the save-S side of the
+ * reference's save-or-recompute choice.  Its default autograd path
+ * (tril_(-1) then matmul, kernels/attention.py:27-40) keeps S for the
+ * backward; analytic_tril_attn_backward (kernels/attention_bwd.py:45-83)
+ * recomputes it.
+ * bdh_tril_score_v_keeps_scores returns 1 when bdh_tril_score_v(x, x, v, ...)
+ * on these views runs the bf16 MFMA path, whose workspace then starts with the
+ * score tiles of tril(x x^T, -1) (*scores_bytes bytes); else 0.
+ * bdh_tril_score_v_bwd_saved computes the gradients of bdh_tril_score_v_bwd
+ * with k == NULL (dx = merged dq + dk, dv) from that workspace, passed as
+ * `scores`, instead of recomputing the tiles.  x must be the forward's x,
+ * unchanged since; other views give BDH_ERR_ARG.
+ */
+int bdh_tril_score_v_keeps_scores(const bdh_tensor4* x, const bdh_tensor4* v,
+                                  size_t* scores_bytes);
+size_t bdh_tril_score_v_bwd_saved_workspace(int64_t B, int64_t H, int64_t Hv,
+                                            int64_t T, int64_t N, int64_t Dv,
+                                            int32_t x_dtype);
+int bdh_tril_score_v_bwd_saved(const bdh_tensor4* x, const bdh_tensor4* v,
+                               const bdh_tensor4* dout, const bdh_tensor4* dx,
+                               const bdh_tensor4* dv, const void* scores,
+                               size_t scores_bytes, void* workspace,
+                               size_t workspace_bytes, bdh_stream stream);
+
+/*
  * Backward of bdh_tril_rope_score_v: dx = RoPE^-1((dS + dS^T) RoPE(x)) and
  * dv = sum_h M_h^T dout_h, M = tril(RoPE(x) RoPE(x)^T, -1).
  * Replaces the autograd chain of bdh.py:405-412 under BDH_ATTN_AUTOGRAD

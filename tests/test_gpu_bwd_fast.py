@@ -87,3 +87,51 @@ def test_self_backward_c4_properties():
     # slab (0, 0): its gradient depends only on q[0,0], v[0], dO[0,0] for dQ
     wq, _ = O.self_attn_backward(np_of(q[:1, :1]), np_of(v[:1]), np_of(d[:1, :1]))
     assert rel_fro(np_of(dq1[:1, :1]), wq) <= TOL[BF]
+
+
+@pytest.mark.parametrize("shape", SHAPES)
+def test_saved_scores_backward_is_bit_exact(shape):
+    """The forward keeps its score tiles; the backward from them equals the
+    recompute path bit for bit (same kernel, same inputs) and the oracle."""
+    B, H, T, N, D, Hv = shape
+    q = to_dev(O.bf16_round(latent((B, H, T, N), 7)), BF)
+    v = to_dev(O.bf16_round(normal((B, Hv, T, D), 8)), BF)
+    d = to_dev(O.bf16_round(normal((B, H, T, D), 9)), BF)
+    assert ext.keeps_scores(q, v)
+    out, scores = ext.tril_score_v_save(q, v)
+    assert scores is not None
+    assert torch.equal(out, ext.tril_score_v(q, q, v))
+    dq_s, dv_s = ext.tril_score_v_bwd_saved(q, v, d, scores)
+    dq_r, _, dv_r = ext.tril_score_v_bwd(q, None, v, d)
+    assert torch.equal(dq_s, dq_r)
+    assert torch.equal(dv_s, dv_r)
+    wq, wv = O.self_attn_backward(np_of(q), np_of(v), np_of(d))
+    assert rel_fro(np_of(dq_s), wq) <= TOL[BF]
+    assert rel_fro(np_of(dv_s), wv) <= TOL[BF]
+
+
+def test_saved_scores_autograd_and_refusals(monkeypatch):
+    """strict_tril_attn(x, x, v, impl="hip") saves the tiles; gradients equal
+    those of the recompute path.  fp32 keeps no tiles; a different x is refused."""
+    import kernels as K
+
+    B, H, T, N, D = 2, 2, 300, 512, 64
+    x0 = to_dev(O.bf16_round(latent((B, H, T, N), 11)), BF)
+    v0 = to_dev(O.bf16_round(normal((B, 1, T, D), 12)), BF)
+    g = to_dev(O.bf16_round(normal((B, H, T, D), 13)), BF)
+
+    def grads(save: str):
+        monkeypatch.setenv("BDH_ATTN_SAVE_SCORES", save)
+        x = x0.clone().requires_grad_(True)
+        v = v0.clone().requires_grad_(True)
+        K.strict_tril_attn(x, x, v, impl="hip", use_fn=True).backward(g)
+        return x.grad, v.grad
+
+    gx1, gv1 = grads("1")
+    gx0, gv0 = grads("0")
+    assert torch.equal(gx1, gx0)
+    assert torch.equal(gv1, gv0)
+    assert not ext.keeps_scores(x0.float(), v0.float())
+    _, scores = ext.tril_score_v_save(x0, v0)
+    with pytest.raises(RuntimeError):  # narrower x: the saved tiles do not belong to it
+        ext.tril_score_v_bwd_saved(x0[..., :64].contiguous().float(), v0, g, scores)
