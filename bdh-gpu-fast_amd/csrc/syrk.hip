@@ -1485,8 +1485,6 @@ int sy_dq(const void* g, int64_t tpad, const bdh_tensor4* x, const bdh_tensor4* 
 }
 
 
-// dV for bf16 self attention without RoPE: the score tiles M by k_sy_scores
-// into ws, then k_dv_sy.  kNotEligible when the shapes fall outside it.
 // G = dS + dS^T with dS = tril(dO V^T, -1), bf16, into g [B*H][tpad][tpad]
 // (zero padding): the score kernel on Q = dO, K = V with one split (K = D)
 // and the G epilogue.  kNotEligible outside its shapes.
@@ -1540,6 +1538,9 @@ size_t sy_bwd_workspace(int64_t B, int64_t H, int64_t T, int64_t N) {
   return p.ok ? p.part_bytes : 0;
 }
 
+// dV for bf16 self attention without RoPE: the score tiles M by k_sy_scores
+// into ws (or saved by the forward), then k_dv_sy.  kNotEligible when the
+// shapes fall outside it.
 int sy_bwd_dv(const bdh_tensor4* q, const bdh_tensor4* v, const bdh_tensor4* dout, const bdh_tensor4* dv, void* ws,
               size_t ws_bytes, hipStream_t s, const void* saved) {
   const int64_t B = q->size[0], H = q->size[1], T = q->size[2], N = q->size[3];
