@@ -31,6 +31,7 @@ __all__ = [
     "version",
     "tril_score_v",
     "tril_score_v_hip",
+    "tril_score_v_past",
     "tril_rope_score_v",
     "tril_decode",
     "tril_decode_hip",
@@ -54,6 +55,8 @@ EXPORTED_SYMBOLS = (
     "bdh_error_string",
     "bdh_tril_score_v_workspace",
     "bdh_tril_score_v",
+    "bdh_tril_score_v_past_workspace",
+    "bdh_tril_score_v_past",
     "bdh_tril_rope_score_v",
     "bdh_tril_decode_workspace",
     "bdh_tril_decode",
@@ -106,6 +109,8 @@ def _load():
         "bdh_error_string": (ctypes.c_char_p, [ctypes.c_int]),
         "bdh_tril_score_v_workspace": (sz, [i64, i64, i64, i64, i64, i32]),
         "bdh_tril_score_v": (ctypes.c_int, [P, P, P, P, vp, sz, vp]),
+        "bdh_tril_score_v_past_workspace": (sz, [i64, i64, i64, i64, i64, i64, i32]),
+        "bdh_tril_score_v_past": (ctypes.c_int, [P, P, P, P, i64, vp, sz, vp]),
         "bdh_tril_rope_score_v": (ctypes.c_int, [P, P, P, fp, i64, P, vp, sz, vp]),
         "bdh_tril_decode_workspace": (sz, [i64, i64, i64, i64, i64, i64]),
         "bdh_tril_decode": (ctypes.c_int, [P, P, P, P, vp, sz, vp]),
@@ -230,6 +235,27 @@ def tril_score_v(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Ten
 
 
 tril_score_v_hip = tril_score_v
+
+
+def tril_score_v_past(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, past: int) -> torch.Tensor:
+    """Queries at an offset: ``out[..., i, :] = sum_{j < past+i} <q_i, k_j> v_j``.
+
+    q ``(B,H,T,Dk)`` are rows ``past..past+T-1`` of the sequence k ``(B,H,past+T,Dk)``
+    and v ``(B,1|H,past+T,Dv)`` cover; out ``(B,H,T,Dv)`` in q's dtype.
+    """
+    dev = _require_device(q, k, v)
+    B, H, T, Dk = q.shape
+    past = int(past)
+    out = torch.empty(B, H, T, v.size(-1), dtype=q.dtype, device=dev)
+    with torch.cuda.device(dev):
+        need = _lib.bdh_tril_score_v_past_workspace(B, H, T, past, Dk, v.size(-1), _dtype_code(q))
+        ws, nb = _workspace(need, dev)
+        rc = _lib.bdh_tril_score_v_past(
+            ctypes.byref(_t4(q)), ctypes.byref(_t4(k)), ctypes.byref(_t4(v)), ctypes.byref(_t4(out)),
+            past, ws.data_ptr() if ws is not None else None, nb, _stream(dev),
+        )
+    _check(rc, "tril_score_v_past")
+    return out
 
 
 def keeps_scores(x: torch.Tensor, v: torch.Tensor) -> bool:

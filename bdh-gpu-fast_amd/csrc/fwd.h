@@ -10,7 +10,9 @@ constexpr int64_t kTargetWorkgroups = 1024;
 
 struct FwdPlan {
   int64_t nt = 0;      // 128-row tiles per slab
-  int64_t ntl = 0;     // packed lower tiles per slab
+  int64_t s0 = 0;      // first row tile computed (queries at an offset)
+  int64_t t0 = 0;      // packed index of its first tile
+  int64_t ntl = 0;     // packed lower tiles per slab, from t0 on
   int64_t splits = 1;  // split-K factor
   int64_t kc = 0;      // k extent of one split (multiple of the K stage)
   size_t ws_bytes = 0; // partial score tiles
@@ -23,11 +25,16 @@ struct ScoresArgs {
   bool vec_q, vec_k;
   const float* freqs;
   int64_t rope_start;
-  float* sp;  // partial tiles [split][slab][tile][128*128]
+  float* sp;  // partial tiles [split][slab][tile - t0][128*128]
   int64_t kc;
   int ntl;
   View qr;    // optional RoPE(x) output (diagonal tiles write it)
   bool qr_bf;
+  // Queries at an offset (chunked prefill): query row i is global row
+  // past + i over keys [0, T); the launch covers the packed lower tiles from
+  // t0 on (row tiles >= past / 128).  0 for the ordinary op.
+  int64_t past = 0;
+  int t0 = 0;
 };
 
 struct ScoreVArgs {
@@ -39,6 +46,8 @@ struct ScoreVArgs {
   int64_t H, Hv, T, Dv;
   bool vec4_v;
   View o;
+  int64_t past = 0;  // output row i is global row past + i (chunked prefill)
+  int s0 = 0, t0 = 0;  // first row tile; packed index of its first tile
 };
 
 // bf16 fast path of the cold op (syrk.hip).  sy_cold returns kNotEligible
@@ -49,6 +58,11 @@ size_t sy_workspace(int64_t B, int64_t H, int64_t T, int64_t N, int64_t Dv, bool
 int sy_cold(const bdh_tensor4* q, const bdh_tensor4* k, const bdh_tensor4* v, const bdh_tensor4* out,
             const float* freqs, int64_t rope_start, const bdh_tensor4* qr, void* ws, size_t ws_bytes,
             hipStream_t s);
+// Queries at an offset on the same path, when q is rows past.. of k (same
+// storage and strides, bf16): only the row tiles that hold new rows.
+size_t sy_past_workspace(int64_t B, int64_t H, int64_t Tk, int64_t past, int64_t N, int64_t Dv);
+int sy_past(const bdh_tensor4* q, const bdh_tensor4* k, const bdh_tensor4* v, const bdh_tensor4* out,
+            int64_t past, void* ws, size_t ws_bytes, hipStream_t s);
 
 // Backward dV on the MFMA path (syrk.hip): score tiles recomputed by the
 // forward score kernel into ws (sy_bwd_workspace bytes), then dV from them.
@@ -66,7 +80,7 @@ int sy_bwd_g(const bdh_tensor4* dout, const bdh_tensor4* v, void* g, int64_t tpa
 // Backward dQ = G X on the MFMA path (syrk.hip): bf16 X, self attention, no RoPE.
 int sy_dq(const void* g, int64_t tpad, const bdh_tensor4* x, const bdh_tensor4* out, hipStream_t s);
 
-FwdPlan plan_fwd(int64_t B, int64_t H, int64_t T, int64_t K, bool bf);
+FwdPlan plan_fwd(int64_t B, int64_t H, int64_t T, int64_t K, bool bf, int64_t past = 0);
 int run_scores(const ScoresArgs& a, const FwdPlan& p, int64_t BH, bool bf, bool rope, bool trans,
                hipStream_t s);
 

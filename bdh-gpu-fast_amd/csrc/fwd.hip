@@ -18,7 +18,7 @@ __global__ __launch_bounds__(kNT) void k_scores(ScoresArgs a) {
   constexpr bool BF = std::is_same<TIn, bf16_t>::value;
   __shared__ Smem<BF> sm;
   int ti, tj;
-  lower_tile_coords(blockIdx.x, ti, tj);
+  lower_tile_coords(int(blockIdx.x) + a.t0, ti, tj);
   const int slab = blockIdx.y;
   const int b = slab / a.H, h = slab % a.H;
   const int split = blockIdx.z;
@@ -30,6 +30,7 @@ __global__ __launch_bounds__(kNT) void k_scores(ScoresArgs a) {
   la.rs = a.q.s2;
   la.r0 = ti * kTile;
   la.nrows = int(a.T);
+  la.rlo = int(a.past);  // query rows are global rows past ..
   la.K = int(a.K);
   la.vec = a.vec_q;
   lb.base = static_cast<const TIn*>(a.k.p) + b * a.k.s0 + h * a.k.s1;
@@ -48,7 +49,7 @@ __global__ __launch_bounds__(kNT) void k_scores(ScoresArgs a) {
       la.qr_bf = a.qr_bf;
     }
   }
-  const bool b_is_a = (ti == tj) && a.q_is_k;
+  const bool b_is_a = (ti == tj) && a.q_is_k && a.past == 0;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int wm = wave >> 1, wn = wave & 1;
   // In a diagonal tile the wave at (rows 0-63, cols 64-127) sees only j > i.
@@ -86,7 +87,7 @@ __global__ __launch_bounds__(kNT) void k_scores(ScoresArgs a) {
 template <bool BF, typename TV, typename TO>
 __global__ __launch_bounds__(kNT) void k_score_v(ScoreVArgs a) {
   __shared__ Smem<BF> sm;
-  const int R = blockIdx.x, Dt = blockIdx.y, slab = blockIdx.z;
+  const int R = int(blockIdx.x) + a.s0, Dt = blockIdx.y, slab = blockIdx.z;
   const int b = slab / a.H, h = slab % a.H;
   const int hv = a.Hv == 1 ? 0 : h;
 
@@ -95,6 +96,7 @@ __global__ __launch_bounds__(kNT) void k_score_v(ScoreVArgs a) {
   la.split_stride = a.split_stride;
   la.nsplit = a.nsplit;
   la.R = R;
+  la.t0 = a.t0;
   NRows<TV, BF, false> lb;
   lb.base = static_cast<const TV*>(a.v.p) + b * a.v.s0 + hv * a.v.s1;
   lb.rs = a.v.s2;
@@ -126,16 +128,20 @@ __global__ __launch_bounds__(kNT) void k_score_v(ScoreVArgs a) {
         int row, col;
         acc_coord<false>(wm, wn, lane, i, j, r, row, col);
         const int gi = R * kTile + row, gd = Dt * kTile + col;
-        if (gi < a.T && gd < a.Dv) o[int64_t(gi) * a.o.s2 + gd] = from_f<TO>(acc[i][j][r]);
+        if (gi >= a.past && gi < a.T && gd < a.Dv) o[int64_t(gi - a.past) * a.o.s2 + gd] = from_f<TO>(acc[i][j][r]);
       }
 }
 
 // ---------------------------------------------------------------- host side
-FwdPlan plan_fwd(int64_t B, int64_t H, int64_t T, int64_t K, bool bf) {
+// past > 0: only the row tiles from past / 128 on (their packed lower tiles
+// are the suffix from t0 = s0 (s0 + 1) / 2); ntl counts the tiles launched.
+FwdPlan plan_fwd(int64_t B, int64_t H, int64_t T, int64_t K, bool bf, int64_t past) {
   FwdPlan p;
   const int64_t BK = bf ? Mode<true>::BK : Mode<false>::BK;
   p.nt = (T + kTile - 1) / kTile;
-  p.ntl = p.nt * (p.nt + 1) / 2;
+  p.s0 = past / kTile;
+  p.t0 = p.s0 * (p.s0 + 1) / 2;
+  p.ntl = p.nt * (p.nt + 1) / 2 - p.t0;
   const int64_t wgs = B * H * p.ntl;
   int64_t splits = 1;
   if (wgs > 0 && wgs < kTargetWorkgroups) splits = (kTargetWorkgroups + wgs - 1) / wgs;
@@ -152,6 +158,7 @@ FwdPlan plan_fwd(int64_t B, int64_t H, int64_t T, int64_t K, bool bf) {
 
 template <typename TIn, bool ROPE, bool TRANS>
 int launch_scores(const ScoresArgs& a, const FwdPlan& p, int64_t BH, hipStream_t s) {
+  if (p.ntl == 0) return BDH_OK;
   dim3 grid((unsigned)(p.ntl), unsigned(BH), unsigned(p.splits));
   BDH_LAUNCH("k_scores", (k_scores<TIn, ROPE, TRANS>), grid, dim3(kNT), 0, s, a);
   return BDH_OK;
@@ -173,7 +180,8 @@ int run_scores(const ScoresArgs& a, const FwdPlan& p, int64_t BH, bool bf, bool 
 
 template <bool BF, typename TV, typename TO>
 int launch_score_v(const ScoreVArgs& a, int64_t nt, int64_t BH, hipStream_t s) {
-  dim3 grid((unsigned)(nt), unsigned((a.Dv + kTile - 1) / kTile), unsigned(BH));
+  if (nt - a.s0 <= 0) return BDH_OK;
+  dim3 grid((unsigned)(nt - a.s0), unsigned((a.Dv + kTile - 1) / kTile), unsigned(BH));
   BDH_LAUNCH("k_score_v", (k_score_v<BF, TV, TO>), grid, dim3(kNT), 0, s, a);
   return BDH_OK;
 }
@@ -283,9 +291,101 @@ static int run_cold(const bdh_tensor4* q, const bdh_tensor4* k, const bdh_tensor
   return run_score_v(va, p.nt, B * H, bf, v->dtype, out->dtype, s);
 }
 
+// Queries at an offset (chunked prefill): q (B,H,T,N) are global rows
+// past .. past+T-1 over k (B,H,past+T,N), v (B,1|H,past+T,Dv); out (B,H,T,Dv).
+static int check_past(const bdh_tensor4* q, const bdh_tensor4* k, const bdh_tensor4* v,
+                      const bdh_tensor4* out, int64_t past) {
+  BDH_TRY(check_view(q));
+  BDH_TRY(check_view(k));
+  BDH_TRY(check_view(v));
+  BDH_TRY(check_view(out));
+  const int64_t B = q->size[0], H = q->size[1], T = q->size[2], N = q->size[3];
+  if (past < 0) return BDH_ERR_ARG;
+  if (k->size[0] != B || k->size[1] != H || k->size[2] != past + T || k->size[3] != N) return BDH_ERR_SHAPE;
+  if (q->dtype != k->dtype) return BDH_ERR_DTYPE;
+  if (v->size[0] != B || v->size[2] != past + T || (v->size[1] != 1 && v->size[1] != H)) return BDH_ERR_SHAPE;
+  if (out->size[0] != B || out->size[1] != H || out->size[2] != T || out->size[3] != v->size[3])
+    return BDH_ERR_SHAPE;
+  if (views_overlap(out, q) || views_overlap(out, k) || views_overlap(out, v)) return BDH_ERR_ALIAS;
+  const int64_t lim = int64_t(1) << 30;
+  for (int i = 0; i < 4; ++i)
+    if (k->size[i] >= lim || v->size[i] >= lim || q->size[i] >= lim) return BDH_ERR_SHAPE;
+  if (B * H > 65535) return BDH_ERR_SHAPE;
+  return BDH_OK;
+}
+
+static int run_past(const bdh_tensor4* q, const bdh_tensor4* k, const bdh_tensor4* v, const bdh_tensor4* out,
+                    int64_t past, void* ws, size_t ws_bytes, hipStream_t s) {
+  const int64_t B = q->size[0], H = q->size[1], T = q->size[2], K = q->size[3];
+  const int64_t Tk = past + T;
+  if (numel4(out) == 0) return BDH_OK;
+  const bool bf = q->dtype == BDH_BF16;
+  const FwdPlan p = plan_fwd(B, H, Tk, K, bf, past);
+  if (ws == nullptr || ws_bytes < p.ws_bytes) return BDH_ERR_WORKSPACE;
+
+  ScoresArgs sa;
+  sa.q = view_of(q);
+  sa.k = view_of(k);
+  sa.q.s1 = q->stride[1];
+  sa.k.s1 = k->stride[1];
+  sa.H = H;
+  sa.T = Tk;
+  sa.K = K;
+  sa.q_is_k = 0;
+  sa.vec_q = vec16_ok(q);
+  sa.vec_k = vec16_ok(k);
+  sa.freqs = nullptr;
+  sa.rope_start = 0;
+  sa.sp = static_cast<float*>(ws);
+  sa.kc = p.kc;
+  sa.ntl = int(p.ntl);
+  sa.qr.p = nullptr;
+  sa.qr_bf = false;
+  sa.past = past;
+  sa.t0 = int(p.t0);
+  BDH_TRY(run_scores(sa, p, B * H, bf, false, false, s));
+
+  ScoreVArgs va;
+  va.sp = sa.sp;
+  va.split_stride = (B * H) * p.ntl * int64_t(kTileElems);
+  va.nsplit = int(p.splits);
+  va.ntl = int(p.ntl);
+  va.v = view_of(v);
+  va.H = H;
+  va.Hv = v->size[1];
+  va.T = Tk;
+  va.Dv = v->size[3];
+  va.vec4_v = vec4_rows(v);
+  va.o = view_of(out);
+  va.o.s1 = out->stride[1];
+  va.past = past;
+  va.s0 = int(p.s0);
+  va.t0 = int(p.t0);
+  return run_score_v(va, p.nt, B * H, bf, v->dtype, out->dtype, s);
+}
+
 }  // namespace bdh
 
 using namespace bdh;
+
+extern "C" size_t bdh_tril_score_v_past_workspace(int64_t B, int64_t H, int64_t T, int64_t past, int64_t Dk,
+                                                  int64_t Dv, int32_t qk_dtype) {
+  if (past <= 0) return bdh_tril_score_v_workspace(B, H, T, Dk, Dv, qk_dtype);
+  const size_t generic = plan_fwd(B, H, past + T, Dk, qk_dtype == BDH_BF16, past).ws_bytes;
+  const size_t fast = qk_dtype == BDH_BF16 ? sy_past_workspace(B, H, past + T, past, Dk, Dv) : 0;
+  return generic > fast ? generic : fast;
+}
+
+extern "C" int bdh_tril_score_v_past(const bdh_tensor4* q, const bdh_tensor4* k, const bdh_tensor4* v,
+                                     const bdh_tensor4* out, int64_t past, void* workspace,
+                                     size_t workspace_bytes, bdh_stream stream) {
+  BDH_TRY(check_past(q, k, v, out, past));
+  if (past == 0) return bdh_tril_score_v(q, k, v, out, workspace, workspace_bytes, stream);
+  if (numel4(out) == 0) return BDH_OK;
+  const int rc = sy_past(q, k, v, out, past, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
+  if (rc != kNotEligible) return rc;
+  return run_past(q, k, v, out, past, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
+}
 
 extern "C" size_t bdh_tril_score_v_workspace(int64_t B, int64_t H, int64_t T, int64_t Dk,
                                              int64_t Dv, int32_t qk_dtype) {

@@ -45,16 +45,15 @@ constexpr int kSyTile = 256;
 constexpr int kSyBlk = kSyTile * 64;   // bytes of one row block per stage (256 rows x 32 bf16)
 constexpr int kSySlot = 2 * kSyBlk;    // A and B row blocks
 constexpr int kSyLdsSlots = 5;    // 160 KB: x ring of 5 (plain) or 4 x + 1 RoPE table (fused)
-constexpr int kSyMaxItems = 256;
-constexpr int kSyMaxTiles = 128;
 constexpr int kSyTileElems = kSyTile * kSyTile;
 
 typedef __attribute__((address_space(3))) uint8_t lds_u8;
 
-// Work item word: ta | tb << 8 | split << 16 | kind << 24.  kSyFull: tile
-// (ta, tb), ta > tb, or any tile when Q != K; kSyDiag2: diagonal tiles ta and
-// tb; kSyDiag1: diagonal tile ta alone (tb = ta: loaded twice, stored once).
+// Work item kinds.  kSyFull: tile (ta, tb), ta > tb, or any tile when Q != K;
+// kSyDiag2: diagonal tiles ta and tb; kSyDiag1: diagonal tile ta alone (tb =
+// ta: loaded twice, stored once).
 enum : int { kSyFull = 0, kSyDiag2 = 1, kSyDiag1 = 2 };
+
 
 struct SyArgs {
   const bf16_t* q;
@@ -62,6 +61,10 @@ struct SyArgs {
   int64_t q0, q1, q2;  // element strides of q over (b, h, t)
   int64_t k0, k1, k2;
   int H, T, N, nslab, ips, nchunk, nsplit, ntl;
+  int t0 = 0;          // packed index of the first stored tile (row tiles from s0: s0 (s0 + 1) / 2)
+  int s0 = 0;          // first row tile with work
+  int per_split;       // work items per split of a slab
+  int nfull;           // of which full tiles (the rest: diagonal pairs)
   const uint32_t* cs;  // RoPE table, stage-major [N/32][T][16] (cos, sin) dwords, or null
   bf16_t* part;        // [nslab][ntl][nsplit][256*256] partial score tiles (bf16)
   bf16_t* qr;          // optional RoPE(x) copy
@@ -69,8 +72,39 @@ struct SyArgs {
   bf16_t* g;           // G output [nslab][tpad][tpad] (G epilogue only)
   int64_t tpad;
   int tq;              // rows of the RoPE table
-  uint32_t items[kSyMaxItems];
 };
+
+// Work item itx of a slab: split-major; within a split the full tiles row by
+// row from row tile s0, then (Q = K) the diagonal tiles of row tiles s0.. in
+// pairs, the last one alone when their count is odd.  Returned as one word,
+// ta | tb << 8 | split << 16 | kind << 24, so a single scalar register stays
+// live.  Uniform scalar loops (at most nsplit and nt steps).
+template <bool SELF>
+__device__ inline uint32_t sy_item(const SyArgs& a, int itx) {
+  int r = itx, split = 0;
+  while (r >= a.per_split) {
+    r -= a.per_split;
+    ++split;
+  }
+  int ta, tb, kind;
+  if (!SELF || r < a.nfull) {
+    int t = a.s0;
+    while (r >= (SELF ? t : t + 1)) {  // row t holds t (Q = K) or t + 1 full tiles
+      r -= SELF ? t : t + 1;
+      ++t;
+    }
+    ta = t;
+    tb = r;
+    kind = kSyFull;
+  } else {
+    const int nt = (a.T + kSyTile - 1) / kSyTile;
+    ta = a.s0 + 2 * (r - a.nfull);
+    tb = ta + 1 < nt ? ta + 1 : ta;
+    kind = tb == ta ? kSyDiag1 : kSyDiag2;
+  }
+  return __builtin_amdgcn_readfirstlane(uint32_t(ta) | (uint32_t(tb) << 8) | (uint32_t(split) << 16) |
+                                        (uint32_t(kind) << 24));
+}
 
 __shared__ __attribute__((aligned(1024))) uint8_t sy_lds[kSyLdsSlots * kSySlot];  // 160 KB
 
@@ -281,7 +315,7 @@ __global__ __launch_bounds__(kSyThreads, 1) void k_sy_scores(const SyArgs a) {
   const int slab = grp * 8 + xcd;
   if (slab >= a.nslab) return;
   const int itx = kk - grp * a.ips;
-  const uint32_t item = a.items[itx];
+  const uint32_t item = sy_item<SELF>(a, itx);
   const int ta = item & 255, tb = (item >> 8) & 255, split = (item >> 16) & 255;
   const int kind = int(item >> 24);
   const bool diag = SELF && kind != kSyFull;
@@ -434,7 +468,7 @@ __global__ __launch_bounds__(kSyThreads, 1) void k_sy_scores(const SyArgs a) {
         fbase[hf][0] = 4 * wm * 2048 + int((REL && wm == 1) ? lrev[hf] : loff[hf]);
         fbase[hf][1] = kSyBlk + 2 * wn * 2048 + int((REL && wn >= 2) ? lrev[hf] : loff[hf]);
       }
-      tile_out = ta * (ta + 1) / 2 + tb;
+      tile_out = ta * (ta + 1) / 2 + tb - a.t0;
     } else {
 #pragma unroll
       for (int hf = 0; hf < 2; ++hf) {
@@ -442,7 +476,7 @@ __global__ __launch_bounds__(kSyThreads, 1) void k_sy_scores(const SyArgs a) {
         fbase[hf][1] = (w >> 2) * kSyBlk + int(REL ? lrev[hf] : loff[hf]);
       }
       const int t = w < 4 ? ta : tb;
-      tile_out = (w < 4 || kind == kSyDiag2) ? t * (t + 1) / 2 + t : -1;
+      tile_out = (w < 4 || kind == kSyDiag2) ? t * (t + 1) / 2 + t - a.t0 : -1;
     }
     f32x16 acc[NM];
 #pragma unroll
@@ -1065,6 +1099,9 @@ struct SvArgs {
   View v;              // V (B, Hv, T, D)
   int ntl, nsplit, H, Hv, T, D;
   View o;
+  int t0 = 0;          // packed index of the first stored tile
+  int rb0 = 0;         // first 64-row block (queries at an offset)
+  int past = 0;        // rows below past are not stored; row i is stored at i - past
 };
 
 template <typename TO, typename TV, int NS>
@@ -1076,7 +1113,7 @@ __global__ __launch_bounds__(512, 1) void k_sy_sv(const SvArgs a) {
   uint8_t* const vblk = sv_lds + 64 * 128;   // 64 x 512 bytes
   float* const red = reinterpret_cast<float*>(sv_lds);
   constexpr int VL = sizeof(TV) == 2 ? 1 : 2;  // 16-byte loads per 8 V elements
-  const int rb = blockIdx.x, slab = blockIdx.y;
+  const int rb = int(blockIdx.x) + a.rb0, slab = blockIdx.y;
   const int b = slab / a.H, h = slab - b * a.H, hv = a.Hv == 1 ? 0 : h;
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   const int r0 = rb * 64;
@@ -1104,7 +1141,7 @@ __global__ __launch_bounds__(512, 1) void k_sy_sv(const SvArgs a) {
   auto load_chunk = [&](int ck, auto slotc) {
     constexpr int k = decltype(slotc)::value;
     const int j0 = ck * 64;
-    const int tile = ti * (ti + 1) / 2 + (j0 >> 8);
+    const int tile = ti * (ti + 1) / 2 + (j0 >> 8) - a.t0;
     const bf16_t* p = pslab + int64_t(tile) * a.nsplit * kSyTileElems + (gi & 255) * kSyTile + ((j0 + lk) & 255);
 #pragma unroll
     for (int sp = 0; sp < NS; ++sp)
@@ -1235,7 +1272,7 @@ __global__ __launch_bounds__(512, 1) void k_sy_sv(const SvArgs a) {
       for (int r = 0; r < 16; ++r) {
         const int row = r0 + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
         const float val = acc[i][c][r] + red[(wc * 64 + (i * 2 + c) * 16 + r) * 64 + lane];
-        if (row < a.T && dok[c]) o[int64_t(row) * a.o.s2 + dcol[c]] = from_f<TO>(val);
+        if (row >= a.past && row < a.T && dok[c]) o[int64_t(row - a.past) * a.o.s2 + dcol[c]] = from_f<TO>(val);
       }
 }
 
@@ -1254,8 +1291,9 @@ int launch_sy_sv(const SvArgs& sa, dim3 grid, hipStream_t s) {
 // ---------------------------------------------------------------- host plan
 struct SyPlan {
   int nt = 0, ntl = 0, ips = 0, nchunk = 0, nsplit = 1;
+  int s0 = 0, t0 = 0;  // first row tile and its packed index (queries at an offset)
+  int per_split = 0, nfull = 0;
   size_t table_bytes = 0, part_bytes = 0, ws_bytes = 0;
-  uint32_t items[kSyMaxItems];
   bool ok = false;
 };
 
@@ -1266,35 +1304,29 @@ struct SyPlan {
 // number of stages and walk k in step: a full tile and the diagonal pair of
 // the same two row blocks then load the same bytes at the same time and the
 // second load is served by the XCD's L2.  The split count is the smallest
-// that gives every CU a work item.
-SyPlan sy_plan(int64_t nslab, int64_t T, int64_t N, bool self, bool rope, int64_t Dv = 0, int max_split = 8) {
+// that gives every CU a work item.  s0 > 0 keeps the row tiles from s0 on
+// (queries at an offset); their tiles are stored from packed index t0.
+SyPlan sy_plan(int64_t nslab, int64_t T, int64_t N, bool self, bool rope, int64_t Dv = 0, int max_split = 8,
+               int s0 = 0) {
   SyPlan p;
-  if (T <= 0 || N <= 0 || N % 64 != 0 || nslab <= 0) return p;
+  if (T <= 0 || N <= 0 || N % 64 != 0 || nslab <= 0 || s0 < 0 || (s0 > 0 && rope)) return p;
   p.nt = int((T + kSyTile - 1) / kSyTile);
-  p.ntl = p.nt * (p.nt + 1) / 2;
+  if (s0 >= p.nt) return p;
+  p.s0 = s0;
+  p.t0 = s0 * (s0 + 1) / 2;
+  p.ntl = p.nt * (p.nt + 1) / 2 - p.t0;
   p.nchunk = int(N / 64);
-  if (p.ntl > kSyMaxTiles) return p;
-  const int per_split = self ? (p.ntl - p.nt) + (p.nt + 1) / 2 : p.ntl;
+  const int nrow = p.nt - s0;  // row tiles kept
+  p.nfull = self ? p.ntl - nrow : p.ntl;
+  const int per_split = self ? p.nfull + (nrow + 1) / 2 : p.ntl;
   // one item per CU if that takes at most 8 splits, else the fewest that fill
   // every CU once
   const int64_t per_pass = nslab * per_split;
   int S = int(std::max<int64_t>(1, std::min<int64_t>(max_split, 256 / per_pass)));
   S = std::min(S, p.nchunk);
-  if (per_split * S > kSyMaxItems) return p;
   p.nsplit = S;
-  int n = 0;
-  auto add = [&](int ta, int tb, int sp, int kind) {
-    p.items[n++] = uint32_t(ta) | (uint32_t(tb) << 8) | (uint32_t(sp) << 16) | (uint32_t(kind) << 24);
-  };
-  for (int sp = 0; sp < S; ++sp) {
-    for (int ti = 0; ti < p.nt; ++ti)
-      for (int tj = 0; tj < ti + (self ? 0 : 1); ++tj) add(ti, tj, sp, kSyFull);
-    if (self) {
-      for (int t = 0; t + 1 < p.nt; t += 2) add(t, t + 1, sp, kSyDiag2);
-      if (p.nt % 2) add(p.nt - 1, p.nt - 1, sp, kSyDiag1);
-    }
-  }
-  p.ips = n;
+  p.per_split = per_split;
+  p.ips = per_split * S;
   // table rows: T positions (absolute) or 128 nt distances (relative)
   p.table_bytes = rope ? align_up(size_t(std::max<int64_t>(T, 128 * p.nt)) * size_t(N / 2) * 4, 256) : 0;
   p.part_bytes = size_t(nslab) * size_t(p.ntl) * size_t(S) * kSyTileElems * sizeof(bf16_t);
@@ -1331,7 +1363,7 @@ namespace {
 
 // Eligibility of the MFMA forward path, and its plan.
 bool sy_cold_check(const bdh_tensor4* q, const bdh_tensor4* k, const bdh_tensor4* v, bool rope,
-                   const bdh_tensor4* qr, SyPlan& p, bool& self) {
+                   const bdh_tensor4* qr, SyPlan& p, bool& self, int s0 = 0) {
   const int64_t B = q->size[0], H = q->size[1], T = q->size[2], N = q->size[3];
   if (q->dtype != BDH_BF16 || k->dtype != BDH_BF16) return false;
   self = q->data == k->data && q->stride[0] == k->stride[0] && q->stride[1] == k->stride[1] &&
@@ -1346,7 +1378,7 @@ bool sy_cold_check(const bdh_tensor4* q, const bdh_tensor4* k, const bdh_tensor4
   if (qr != nullptr && (qr->dtype != BDH_BF16 || !rows16(qr))) return false;
   const int64_t nslab = B * H;
   if (nslab > (int64_t(1) << 24)) return false;
-  p = sy_plan(nslab, T, N, self, rope, v->size[3]);
+  p = sy_plan(nslab, T, N, self, rope, v->size[3], 8, s0);
   if (!p.ok) return false;
   return 8 * ((nslab + 7) / 8) * p.ips < (int64_t(1) << 31);
 }
@@ -1361,14 +1393,19 @@ bool sy_keeps_scores(const bdh_tensor4* q, const bdh_tensor4* v, size_t* scores_
   return true;
 }
 
-int sy_cold(const bdh_tensor4* q, const bdh_tensor4* k, const bdh_tensor4* v, const bdh_tensor4* out,
-            const float* freqs, int64_t rope_start, const bdh_tensor4* qr, void* ws, size_t ws_bytes,
-            hipStream_t s) {
+namespace {
+
+// past > 0 (no RoPE): out holds rows past.. only, and the score tiles of the
+// row tiles below past / 256 are neither computed nor stored.
+int sy_run(const bdh_tensor4* q, const bdh_tensor4* k, const bdh_tensor4* v, const bdh_tensor4* out,
+           const float* freqs, int64_t rope_start, const bdh_tensor4* qr, int64_t past, void* ws,
+           size_t ws_bytes, hipStream_t s) {
   const int64_t B = q->size[0], H = q->size[1], T = q->size[2], N = q->size[3];
   const bool rope = freqs != nullptr;
   SyPlan p;
   bool self = false;
-  if (!sy_cold_check(q, k, v, rope, qr, p, self)) return kNotEligible;
+  if (past < 0 || past >= T || (past > 0 && rope)) return kNotEligible;
+  if (!sy_cold_check(q, k, v, rope, qr, p, self, int(past / kSyTile))) return kNotEligible;
   const int64_t nslab = B * H;
   const int64_t Dv = v->size[3];
   const int64_t grid_scores = 8 * ((nslab + 7) / 8) * p.ips;
@@ -1405,6 +1442,7 @@ int sy_cold(const bdh_tensor4* q, const bdh_tensor4* k, const bdh_tensor4* v, co
   a.nchunk = p.nchunk;
   a.nsplit = p.nsplit;
   a.ntl = p.ntl;
+  a.t0 = p.t0;
   a.cs = table;
   a.tq = tq;
   a.part = part;
@@ -1416,7 +1454,9 @@ int sy_cold(const bdh_tensor4* q, const bdh_tensor4* k, const bdh_tensor4* v, co
     a.r1 = qr->stride[1];
     a.r2 = qr->stride[2];
   }
-  for (int i = 0; i < p.ips; ++i) a.items[i] = p.items[i];
+  a.s0 = p.s0;
+  a.per_split = p.per_split;
+  a.nfull = p.nfull;
   const dim3 gs{unsigned(grid_scores)};
   if (rel)
     BDH_LAUNCH("k_sy_scores", (k_sy_scores<2, true>), gs, dim3(kSyThreads), 0, s, a);
@@ -1440,10 +1480,38 @@ int sy_cold(const bdh_tensor4* q, const bdh_tensor4* k, const bdh_tensor4* v, co
   sa.D = int(Dv);
   sa.o = view_of(out);
   sa.o.s1 = out->stride[1];
-  const dim3 gsv(unsigned((T + 63) / 64), unsigned(nslab));
+  sa.t0 = p.t0;
+  sa.rb0 = int(past / 64);
+  sa.past = int(past);
+  const dim3 gsv(unsigned((T + 63) / 64 - sa.rb0), unsigned(nslab));
   const bool o16 = out->dtype == BDH_BF16, v16 = v->dtype == BDH_BF16;
   if (o16) return v16 ? launch_sy_sv<bf16_t, bf16_t>(sa, gsv, s) : launch_sy_sv<bf16_t, float>(sa, gsv, s);
   return v16 ? launch_sy_sv<float, bf16_t>(sa, gsv, s) : launch_sy_sv<float, float>(sa, gsv, s);
+}
+
+}  // namespace
+
+int sy_cold(const bdh_tensor4* q, const bdh_tensor4* k, const bdh_tensor4* v, const bdh_tensor4* out,
+            const float* freqs, int64_t rope_start, const bdh_tensor4* qr, void* ws, size_t ws_bytes,
+            hipStream_t s) {
+  return sy_run(q, k, v, out, freqs, rope_start, qr, 0, ws, ws_bytes, s);
+}
+
+size_t sy_past_workspace(int64_t B, int64_t H, int64_t Tk, int64_t past, int64_t N, int64_t Dv) {
+  if (past <= 0 || past >= Tk) return 0;
+  const SyPlan p = sy_plan(B * H, Tk, N, true, false, Dv, 8, int(past / kSyTile));
+  return p.ok ? p.ws_bytes : 0;
+}
+
+// q is rows past.. of k (same storage and strides): the self-attention plan
+// over k, restricted to the new rows.
+int sy_past(const bdh_tensor4* q, const bdh_tensor4* k, const bdh_tensor4* v, const bdh_tensor4* out,
+            int64_t past, void* ws, size_t ws_bytes, hipStream_t s) {
+  if (q->dtype != BDH_BF16 || k->dtype != BDH_BF16 || past <= 0) return kNotEligible;
+  for (int i = 0; i < 3; ++i)
+    if (q->stride[i] != k->stride[i]) return kNotEligible;
+  if (q->data != static_cast<const char*>(k->data) + past * k->stride[2] * 2) return kNotEligible;
+  return sy_run(k, k, v, out, nullptr, 0, nullptr, past, ws, ws_bytes, s);
 }
 
 
@@ -1528,7 +1596,9 @@ int sy_bwd_g(const bdh_tensor4* dout, const bdh_tensor4* v, void* g, int64_t tpa
   a.g = static_cast<bf16_t*>(g);
   a.tpad = tpad;
   a.tq = 0;
-  for (int i = 0; i < p.ips; ++i) a.items[i] = p.items[i];
+  a.s0 = p.s0;
+  a.per_split = p.per_split;
+  a.nfull = p.nfull;
   BDH_LAUNCH("k_sy_scores_g", (k_sy_scores<0, false, true>), dim3{unsigned(grid)}, dim3(kSyThreads), 0, s, a);
   return BDH_OK;
 }
@@ -1580,7 +1650,9 @@ int sy_bwd_dv(const bdh_tensor4* q, const bdh_tensor4* v, const bdh_tensor4* dou
     a.part = part;
     a.qr = nullptr;
     a.r0 = a.r1 = a.r2 = 0;
-    for (int i = 0; i < p.ips; ++i) a.items[i] = p.items[i];
+    a.s0 = p.s0;
+    a.per_split = p.per_split;
+    a.nfull = p.nfull;
     BDH_LAUNCH("k_sy_scores", (k_sy_scores<0, true>), dim3{unsigned(grid_scores)}, dim3(kSyThreads), 0, s, a);
   }
   if (numel4(dv) == 0) return BDH_OK;

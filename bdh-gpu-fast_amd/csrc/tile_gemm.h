@@ -190,6 +190,7 @@ struct KRows {
   int64_t rs = 0;    // row stride (elements)
   int r0 = 0;        // first row of the tile
   int nrows = 0;     // rows < nrows are valid
+  int rlo = 0;       // rows < rlo are zero; row gr reads source row gr - rlo
   int K = 0;         // k < K is valid
   bool vec = false;  // 16-byte row access is legal
   const float* freqs = nullptr;
@@ -208,8 +209,9 @@ struct KRows {
       const int ch = threadIdx.x + c * kNT;
       const int row = ch / CPR, kc = (ch % CPR) * E;
       const int gr = r0 + row, gk = k0 + kc;
-      const TIn* p = base + int64_t(gr) * rs + gk;
-      if (gr < nrows && vec && gk + E <= K) {
+      const bool rok = gr >= rlo && gr < nrows;
+      const TIn* p = base + int64_t(rok ? gr - rlo : 0) * rs + gk;
+      if (rok && vec && gk + E <= K) {
         if constexpr (sizeof(TIn) * E == 16) {
           *reinterpret_cast<uint4*>(v[c]) = *reinterpret_cast<const uint4*>(p);
         } else if constexpr (sizeof(TIn) * E == 32) {
@@ -220,7 +222,7 @@ struct KRows {
         }
       } else {
 #pragma unroll
-        for (int e = 0; e < E; ++e) v[c][e] = (gr < nrows && gk + e < K) ? p[e] : TIn(0);
+        for (int e = 0; e < E; ++e) v[c][e] = (rok && gk + e < K) ? p[e] : TIn(0);
       }
       if constexpr (ROPE) {
 #pragma unroll
@@ -370,12 +372,13 @@ struct SplitRows {
   int64_t split_stride = 0;     // floats between splits
   int nsplit = 1;
   int R = 0;                    // A row-tile index
+  int t0 = 0;                   // packed index of the first stored tile
 
   float v[CPT][E];
 
   __device__ __forceinline__ void load(int k0) {
     const int C = k0 / kTile;
-    const int tile = DV ? lower_tile_index(C, R) : lower_tile_index(R, C);
+    const int tile = (DV ? lower_tile_index(C, R) : lower_tile_index(R, C)) - t0;
     const float* t = slab + int64_t(tile) * kTileElems + (k0 % kTile);
 #pragma unroll
     for (int c = 0; c < CPT; ++c) {

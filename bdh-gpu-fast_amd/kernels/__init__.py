@@ -8,7 +8,13 @@ Drop-in counterpart of the reference package ``kernels`` (kernels/__init__.py):
 the reference's PyTorch semantics.
 """
 
-from .attention import DEFAULT_BLOCK_COLD, DEFAULT_BLOCK_DECODE, eager_decode_attn, eager_tril_attn
+from .attention import (
+    DEFAULT_BLOCK_COLD,
+    DEFAULT_BLOCK_DECODE,
+    eager_decode_attn,
+    eager_past_attn,
+    eager_tril_attn,
+)
 from .attention_bwd import (
     StrictTrilAttnFn,
     StrictTrilSelfAttnFn,
@@ -25,6 +31,7 @@ from .attention_dispatch import (
     backend_info,
     bdh_attn,
     bdh_attn_decode,
+    bdh_attn_past,
     bdh_attn_rope,
     resolve_attn_impl,
     resolve_cold_impl,
@@ -37,6 +44,7 @@ from .hip_attn import (
     tril_decode,
     tril_rope_score_v,
     tril_score_v,
+    tril_score_v_past,
 )
 from .rope import get_freqs, rope_cos_sin
 from .rope_dispatch import backend_info as rope_backend_info
@@ -46,6 +54,7 @@ __all__ = [
     "bdh_attn",
     "bdh_attn_rope",
     "bdh_attn_decode",
+    "bdh_attn_past",
     "resolve_attn_impl",
     "resolve_cold_impl",
     "resolve_decode_impl",
@@ -64,7 +73,9 @@ __all__ = [
     "analytic_tril_attn_backward_blocked",
     "eager_tril_attn",
     "eager_decode_attn",
+    "eager_past_attn",
     "tril_score_v",
+    "tril_score_v_past",
     "tril_rope_score_v",
     "tril_decode",
     "has_hip_ext",

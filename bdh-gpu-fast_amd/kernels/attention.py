@@ -28,6 +28,19 @@ def eager_tril_attn(Q: torch.Tensor, K: torch.Tensor, V: torch.Tensor) -> torch.
     return scores @ V
 
 
+def eager_past_attn(Q: torch.Tensor, K: torch.Tensor, V: torch.Tensor, past: int) -> torch.Tensor:
+    """Queries at offset ``past`` the way the reference's multi-token cached step
+    gets them: strict-tril attention over the whole past||new sequence, last T rows
+    kept (bdh.py:446-461).  Q: (B, H, T, N) are rows past.. of K: (B, H, past+T, N).
+    The rows before ``past`` are zero queries here, so they add nothing.
+    """
+    if past == 0:
+        return eager_tril_attn(Q, K, V)
+    B, H, _, N = Q.shape
+    q_all = torch.cat([Q.new_zeros(B, H, past, N), Q], dim=2)
+    return eager_tril_attn(q_all, K, V)[..., past:, :]
+
+
 def _two_gemm_decode(Q: torch.Tensor, K: torch.Tensor, V: torch.Tensor) -> torch.Tensor:
     """``(Q @ K.mT) @ V`` for decode against the packed past (kernels/attention.py:193-219)."""
     B, H, Tq, N = Q.shape
@@ -51,5 +64,6 @@ __all__ = [
     "DEFAULT_BLOCK_DECODE",
     "eager_tril_attn",
     "eager_decode_attn",
+    "eager_past_attn",
     "_two_gemm_decode",
 ]

@@ -31,7 +31,7 @@ from typing import Literal, Optional
 import torch
 
 from . import hip_attn
-from .attention import DEFAULT_BLOCK_DECODE, eager_decode_attn, eager_tril_attn
+from .attention import DEFAULT_BLOCK_DECODE, eager_decode_attn, eager_past_attn, eager_tril_attn
 from .attention_bwd import TrilRopeSelfAttnFn, _env_autograd_enabled, strict_tril_attn
 from .rope import eager_rope_rotate, rope_cos_sin
 
@@ -196,6 +196,30 @@ def bdh_attn_rope(
     return bdh_attn(qr, qr, V, impl="eager")
 
 
+def bdh_attn_past(
+    Q: torch.Tensor,
+    K: torch.Tensor,
+    V: torch.Tensor,
+    past: int,
+    *,
+    impl: str | None = None,
+) -> torch.Tensor:
+    """T new queries after ``past`` cached rows: ``bdh_attn(K, K, V)[..., past:, :]``
+    when ``Q`` is ``K[..., past:, :]`` (the reference's multi-token cached step,
+    bdh.py:446-461, recomputes that whole attention and slices it).
+
+    New surface entry of this build.  ``hip`` computes only the score tiles that
+    reach a new row; ``eager`` recomputes past||new with torch ops as the
+    reference does.  Inference only under ``hip`` (no autograd).
+    """
+    name = resolve_cold_impl(int(K.size(2)), requested=impl)
+    if name == "eager":
+        return eager_past_attn(Q, K, V, int(past))
+    if _needs_grad(Q, K, V):
+        raise ValueError("bdh_attn_past with impl='hip' is an inference entry; it has no backward")
+    return hip_attn.tril_score_v_past(Q, K, V, int(past))
+
+
 def bdh_attn_decode(
     Q: torch.Tensor,
     K_past: torch.Tensor,
@@ -240,6 +264,7 @@ __all__ = [
     "attn_auto_cold_threshold",
     "bdh_attn",
     "bdh_attn_rope",
+    "bdh_attn_past",
     "bdh_attn_decode",
     "backend_info",
 ]

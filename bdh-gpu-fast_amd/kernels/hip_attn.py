@@ -105,6 +105,29 @@ def tril_score_v(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Ten
     return ext.tril_score_v(q, k, _last_dim_unit(v))
 
 
+def _check_past_shapes(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, past: int) -> None:
+    if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
+        raise ValueError("q, k, v must be 4D (B, H, T, D)")
+    if past < 0:
+        raise ValueError(f"past must be >= 0, got {past}")
+    B, H, T, N = q.shape
+    if tuple(k.shape) != (B, H, past + T, N):
+        raise ValueError(f"k must be (B, H, past+T, N) = {(B, H, past + T, N)}, got {tuple(k.shape)}")
+    if v.size(0) != B or v.size(2) != past + T or v.size(1) not in (1, H):
+        raise ValueError(f"v must be (B, 1|H, past+T, D), got {tuple(v.shape)}")
+
+
+def tril_score_v_past(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, past: int) -> torch.Tensor:
+    """Queries at an offset (chunked prefill): rows ``past..past+T-1`` of the
+    strict-tril attention over k, v of length ``past+T``; out (B, H, T, D)."""
+    past = int(past)
+    _check_past_shapes(q, k, v, past)
+    ext = _require(q, k, v)
+    if q.dtype != k.dtype:
+        raise TypeError(f"q and k dtypes differ: {q.dtype} vs {k.dtype}")
+    return ext.tril_score_v_past(_last_dim_unit(q), _last_dim_unit(k), _last_dim_unit(v), past)
+
+
 def tril_rope_score_v(
     x: torch.Tensor,
     v: torch.Tensor,
@@ -199,6 +222,7 @@ __all__ = [
     "has_hip_kernel",
     "hip_available",
     "tril_score_v",
+    "tril_score_v_past",
     "tril_rope_score_v",
     "tril_decode",
     "tril_score_v_bwd",

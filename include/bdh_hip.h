@@ -86,6 +86,25 @@ int bdh_tril_rope_score_v(const bdh_tensor4* x, const bdh_tensor4* v,
                           bdh_stream stream);
 
 /*
+ * Queries at an offset (chunked prefill): T new rows after `past` cached rows.
+ * out[b,h,i,:] = sum_{j < past+i} <q[b,h,i,:], k[b,h,j,:]> v[b,hv,j,:].
+ * Replaces the reference's multi-token step with a cache, which recomputes
+ * the whole strict-tril attention over past||new and keeps the last T rows
+ * (bdh.py:446-461: bdh_attn(QR_all, QR_all, V_all)[..., S:, :]); here only
+ * the score tiles that reach a new row are computed.
+ * q: (B,H,T,Dk); k: (B,H,past+T,Dk) (rows past.. are the new keys); v:
+ * (B,1|H,past+T,Dv); out: (B,H,T,Dv).  q and k share a dtype.  past == 0 is
+ * bdh_tril_score_v.
+ */
+size_t bdh_tril_score_v_past_workspace(int64_t B, int64_t H, int64_t T,
+                                       int64_t past, int64_t Dk, int64_t Dv,
+                                       int32_t qk_dtype);
+int bdh_tril_score_v_past(const bdh_tensor4* q, const bdh_tensor4* k,
+                          const bdh_tensor4* v, const bdh_tensor4* out,
+                          int64_t past, void* workspace, size_t workspace_bytes,
+                          bdh_stream stream);
+
+/*
  * Decode against the packed past: out = (q K_past^T) V_past (all past keys
  * valid; the new token never attends to itself).
  * Replaces tril_decode (reference csrc/tril_attn_bind.cpp:14-23 ->

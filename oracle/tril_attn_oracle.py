@@ -45,6 +45,7 @@ __all__ = [
     "self_attn_backward",
     "tril_rope_score_v",
     "tril_rope_score_v_backward",
+    "tril_score_v_past",
     "tril_score_v_bruteforce",
     "tril_decode_bruteforce",
     "PINNING",
@@ -483,6 +484,31 @@ def tril_rope_score_v_backward(x, v, dO, freqs, rope_start: int = 0):
 
 
 # ---------------------------------------------------------------------------
+# Queries at an offset (chunked prefill)
+# ---------------------------------------------------------------------------
+def tril_score_v_past(q, k, v, past: int) -> np.ndarray:
+    """``out[b,h,i] = sum_{j < past + i} <q_i, k_j> v_j`` for q ``(B,H,T,Dk)``
+    over k ``(B,H,past+T,Dk)``, v ``(B,1|H,past+T,Dv)``.
+
+    The op the reference computes for a multi-token step with a cache by
+    running the full strict-tril attention over past||new and keeping the
+    last T rows (bdh.py:446-461: ``bdh_attn(QR_all, QR_all, V_all)``, then
+    ``[..., S:, :]``).
+    """
+    q = np.asarray(q, np.float32)
+    k = np.asarray(k, np.float32)
+    v = np.asarray(v, np.float32)
+    B, H, T, Dk = q.shape
+    Tk = k.shape[2]
+    if k.shape != (B, H, past + T, Dk) or v.shape[2] != Tk or v.shape[1] not in (1, H):
+        raise ValueError("tril_score_v_past: q (B,H,T,Dk), k (B,H,past+T,Dk), v (B,1|H,past+T,Dv)")
+    s = np.matmul(q, np.swapaxes(k, -1, -2))  # (B,H,T,Tk)
+    keep = np.arange(Tk)[None, :] < (past + np.arange(T))[:, None]
+    s = np.where(keep, s, np.float32(0))
+    return np.matmul(s, v).astype(np.float32)
+
+
+# ---------------------------------------------------------------------------
 # Brute force (tiny shapes only; pins the BLAS-based paths)
 # ---------------------------------------------------------------------------
 def tril_score_v_bruteforce(q, k, v):
@@ -543,4 +569,5 @@ PINNING = {
     "self_attn_backward": "known answers merged dQ/dV (test_attn_bwd_v4_contract.py:247-253); torch autograd with Q passed twice",
     "tril_rope_score_v": "composition of pinned parts; T=1 -> zeros; rope_start continuity",
     "tril_rope_score_v_backward": "torch autograd (float64) through RoPE + eager tril attention; finite differences",
+    "tril_score_v_past": "the reference's own path: tril_score_v_cpu over past||new, last T rows (bdh.py:446-461); brute force on a zero-padded query; past = 0 is the cold op; T = 1 is decode over the past",
 }

@@ -137,3 +137,41 @@ def test_bf16_fused_rope_full_c1_properties():
     assert not o1[:, :, 0].any().item()
     want, _ = O.tril_rope_score_v(np_of(x[:1]), np_of(v[:1]), O.get_freqs(N), 0, bf16=True)
     assert rel_fro(np_of(o1[:1]), want) <= TOL[BF]
+
+
+def _ran_score_tiles(fn):
+    ext.profile_enable(True)
+    try:
+        out = fn()
+        names = {n for n, _ in ext.profile_collect()}
+    finally:
+        ext.profile_enable(False)
+    assert "k_sy_scores" in names, names
+    return out
+
+
+@pytest.mark.parametrize("mode", ["self", "distinct", "rope"])
+def test_bf16_long_sequences_stay_on_score_tile_path(mode):
+    """Sequences with more than 256 work items per slab (23-24 row tiles):
+    the kernel derives each item from its workgroup index, so the 256x256
+    tile path covers them; results against the oracle."""
+    T = 5800 if mode == "distinct" else 6000
+    B, H, N, D = 1, 1, 64, 16
+    print(f"long {mode} T={T}", flush=True)
+    x = _bf(latent((B, H, T, N), 8))
+    v = _bf(normal((B, 1, T, D), 9))
+    if mode == "self":
+        got = _ran_score_tiles(lambda: ext.tril_score_v(to_dev(x, BF), to_dev(x, BF), to_dev(v, BF)))
+        want = O.tril_score_v_cpu(x, x, v)
+    elif mode == "distinct":
+        k = _bf(latent((B, H, T, N), 10))
+        got = _ran_score_tiles(lambda: ext.tril_score_v(to_dev(x, BF), to_dev(k, BF), to_dev(v, BF)))
+        want = O.tril_score_v_cpu(x, k, v)
+    else:
+        freqs = O.get_freqs(N)
+        f = torch.from_numpy(freqs).to(DEV)
+        got = _ran_score_tiles(lambda: ext.tril_rope_score_v(to_dev(x, BF), to_dev(v, BF), f, 3))
+        want, _ = O.tril_rope_score_v(x, v, freqs, 3, bf16=True)
+    g = np_of(got)
+    assert rel_fro(g, want) <= TOL[BF]
+    assert not g[:, :, 0].any()

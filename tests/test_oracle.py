@@ -352,3 +352,36 @@ def test_rope_attention_against_torch_autograd():
     np.testing.assert_allclose(dx, xt.grad.numpy(), rtol=1e-4, atol=1e-4)
     np.testing.assert_allclose(dv, vt.grad.numpy(), rtol=1e-4, atol=1e-4)
     assert not out[:, :, 0].any()
+
+
+# ----------------------------------------------------------- queries at an offset
+@pytest.mark.parametrize("past,T", [(0, 5), (3, 4), (7, 1), (130, 9)])
+def test_past_equals_full_tril_last_rows(past, T):
+    """bdh.py:446-461: the reference recomputes past||new and keeps rows past.."""
+    rng = np.random.default_rng(past * 31 + T)
+    k = rng.standard_normal((2, 2, past + T, 6)).astype(np.float32)
+    v = rng.standard_normal((2, 1, past + T, 3)).astype(np.float32)
+    got = O.tril_score_v_past(k[:, :, past:], k, v, past)
+    want = O.tril_score_v_cpu(k, k, v)[:, :, past:]
+    np.testing.assert_allclose(got, want, rtol=1e-4, atol=1e-4)
+
+
+def test_past_bruteforce_and_special_cases():
+    rng = np.random.default_rng(5)
+    past, T = 4, 3
+    q = rng.standard_normal((1, 2, T, 5)).astype(np.float32)
+    k = rng.standard_normal((1, 2, past + T, 5)).astype(np.float32)
+    v = rng.standard_normal((1, 2, past + T, 4)).astype(np.float32)
+    # zero-padded query rows in front: row past + i of the full problem is query i
+    qf = np.concatenate([np.zeros((1, 2, past, 5), np.float32), q], axis=2)
+    want = O.tril_score_v_bruteforce(qf, k, v)[:, :, past:]
+    np.testing.assert_allclose(O.tril_score_v_past(q, k, v, past), want, rtol=1e-5, atol=1e-5)
+    # past = 0 is the cold op; T = 1 is decode over the past
+    np.testing.assert_allclose(O.tril_score_v_past(k, k, v, 0), O.tril_score_v_cpu(k, k, v), rtol=1e-5, atol=1e-5)
+    q1 = q[:, :, :1]
+    k1 = k[:, :, : past + 1]
+    v1 = v[:, :, : past + 1]
+    np.testing.assert_allclose(O.tril_score_v_past(q1, k1, v1, past),
+                               O.tril_decode_cpu(q1, k1[:, :, :past], v1[:, :, :past]), rtol=1e-5, atol=1e-5)
+    with pytest.raises(ValueError):
+        O.tril_score_v_past(q, k[:, :, :-1], v, past)
