@@ -1,0 +1,241 @@
+"""BDH model harness around the attention hot path (prefill, cached decode, train step).
+
+A from-scratch model of the same computation as the reference's BDH
+(bdh_baseline.py:109-151 semantics; the layer layout and cache flow of
+bdh.py:947-1193), so the hot path can be measured where the model calls it:
+
+* prefill tok/s (configs C2 and C5): one forward over (B, T) tokens;
+* decode tok/s (config C3): ``generate`` with a packed KR/V cache, the new
+  token's RoPE(x) written straight into its cache slot and attention read
+  from capacity-strided cache views (no cast copies of the past);
+* a training step (C4 at model level): forward, cross entropy, backward.
+
+Per layer (x: (B, T, D), LayerNorm without affine, eps 1e-5):
+
+    x_bthn  = relu(einsum("btd,hdn->bthn", x, encoder))        # (B, T, nh, N), as 2-D GEMMs
+    yKV     = tril(RoPE(x_sparse) RoPE(x_sparse)^T, -1) x      # x_sparse = x_bthn as (B, nh, T, N)
+    y_bthn  = relu(einsum("bhtd,hdn->bthn", LN(yKV), encoder_v))
+    x       = LN(x + LN((x_bthn * y_bthn).view(B, T, nh*N) @ decoder))
+
+then ``logits = x @ lm_head``.  The dense products run on torch (hipBLASLt);
+RoPE and attention go through the ``kernels`` surface, ``impl="hip"`` for the
+gfx950 kernels or ``"eager"`` for the reference's torch semantics.  Under
+``torch.autocast(dtype=bfloat16)`` the GEMMs run in bf16 and LayerNorm in
+fp32, as in the reference's AMP runs.
+"""
+
+from __future__ import annotations
+
+import dataclasses
+from typing import Optional
+
+import torch
+import torch.nn.functional as F
+from torch import nn
+
+import kernels
+
+
+@dataclasses.dataclass
+class BDHConfig:
+    """Model shape (bdh_baseline.py:11-18); N = mlp_internal_dim_multiplier * n_embd // n_head."""
+
+    n_layer: int = 6
+    n_embd: int = 256
+    n_head: int = 4
+    mlp_internal_dim_multiplier: int = 128
+    vocab_size: int = 256
+
+    @property
+    def n_latent(self) -> int:
+        return self.mlp_internal_dim_multiplier * self.n_embd // self.n_head
+
+
+class KVCache:
+    """Packed per-layer cache of RoPE(x) rows and V rows (the roles of bdh_cache.py:226-324).
+
+    ``kr``: (L, B, nh, capacity, N) and ``v``: (L, B, 1, capacity, D) in the
+    storage dtype.  A forward over T new tokens writes rows
+    ``[seq_len, seq_len + T)`` of every layer, reads the past through
+    capacity-strided views of rows ``[0, seq_len)``, and ``commit`` then
+    advances ``seq_len``.
+    """
+
+    def __init__(self, cfg: BDHConfig, batch: int, capacity: int, dtype: torch.dtype, device):
+        L, nh, N, D = cfg.n_layer, cfg.n_head, cfg.n_latent, cfg.n_embd
+        self.capacity = int(capacity)
+        self.kr = torch.empty(L, batch, nh, self.capacity, N, dtype=dtype, device=device)
+        self.v = torch.empty(L, batch, 1, self.capacity, D, dtype=dtype, device=device)
+        self.seq_len = 0
+
+    @property
+    def dtype(self) -> torch.dtype:
+        return self.kr.dtype
+
+    def slot(self, level: int, T: int):
+        """Views of the rows the next T tokens occupy."""
+        if self.seq_len + T > self.capacity:
+            raise ValueError(f"KVCache: {self.seq_len} + {T} rows exceed capacity {self.capacity}")
+        return self.kr[level].narrow(2, self.seq_len, T), self.v[level].narrow(2, self.seq_len, T)
+
+    def past(self, level: int):
+        return self.kr[level].narrow(2, 0, self.seq_len), self.v[level].narrow(2, 0, self.seq_len)
+
+    def span(self, level: int, T: int):
+        """Past and the next T rows together (rows ``[0, seq_len + T)``)."""
+        n = self.seq_len + T
+        return self.kr[level].narrow(2, 0, n), self.v[level].narrow(2, 0, n)
+
+    def commit(self, T: int) -> None:
+        self.seq_len += int(T)
+
+
+def _ln(x: torch.Tensor) -> torch.Tensor:
+    return F.layer_norm(x, (x.size(-1),), eps=1e-5)
+
+
+# The dense products are 2-D matrix products (hipBLASLt GEMMs) on contiguous
+# operands: no einsum and no batched product, whose bf16 forms with
+# transposed-view operands (einsum transposes inside; autograd's backward of
+# a batched product does too) have faulted ROCm GPUs.
+def _encode(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+    """relu(einsum("btd,hdn->bthn", x, w)) as one GEMM: (B*T, D) @ (D, nh*N) -> (B, T, nh, N)."""
+    nh, D, N = w.shape
+    wc = w.permute(1, 0, 2).reshape(D, nh * N)
+    return F.relu(x.reshape(-1, D) @ wc).view(*x.shape[:-1], nh, N)
+
+
+def _encode_heads(y: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+    """relu(einsum("bhtd,hdn->bthn", y, w)): one GEMM per head, (B*T, D) @ (D, N), stacked to (B, T, nh, N)."""
+    B, nh, T, D = y.shape
+    outs = [y[:, h].reshape(B * T, D) @ w[h] for h in range(nh)]
+    return F.relu(torch.stack(outs, dim=1)).view(B, T, nh, w.size(2))
+
+
+class BDH(nn.Module):
+    """BDH language model; parameter names and shapes follow bdh_baseline.py:80-102."""
+
+    def __init__(self, cfg: BDHConfig):
+        super().__init__()
+        self.config = cfg
+        nh, D, N, V = cfg.n_head, cfg.n_embd, cfg.n_latent, cfg.vocab_size
+        self.decoder = nn.Parameter(torch.empty(nh * N, D).normal_(std=0.02))
+        self.encoder = nn.Parameter(torch.empty(nh, D, N).normal_(std=0.02))
+        self.encoder_v = nn.Parameter(torch.empty(nh, D, N).normal_(std=0.02))
+        self.embed = nn.Embedding(V, D)
+        nn.init.normal_(self.embed.weight, mean=0.0, std=0.02)
+        self.lm_head = nn.Parameter(torch.empty(D, V).normal_(std=0.02))
+        self.register_buffer("freqs", kernels.get_freqs(N), persistent=False)
+
+    # ----------------------------------------------------------- attention
+    def _attention(self, level, x_sparse, v_tok, rope_start, cache, impl, cos_sin):
+        """RoPE + strict-tril attention of one layer (bdh.py:348-483 flow)."""
+        T = x_sparse.size(2)
+        if cache is None:
+            if impl == "hip":
+                return kernels.bdh_attn_rope(x_sparse, v_tok, self.freqs, rope_start, impl="hip")
+            qr = kernels.bdh_rope_rotate(x_sparse, *cos_sin, impl="eager")
+            return kernels.bdh_attn(qr, qr, v_tok, impl="eager")
+        S = cache.seq_len
+        slot_kr, slot_v = cache.slot(level, T)
+        slot_v.copy_(v_tok)
+        if impl == "hip" and S == 0 and T > 1:
+            # cold prefill into an empty cache: RoPE(x) lands in the KR slot from the fused kernel
+            return kernels.bdh_attn_rope(x_sparse, slot_v, self.freqs, 0, out_kr=slot_kr, impl="hip")
+        qr = kernels.bdh_rope_rotate(x_sparse, *cos_sin, out=slot_kr, impl=impl)
+        if T == 1:
+            if S == 0:  # position 0 attends to nothing
+                return x_sparse.new_zeros(x_sparse.size(0), x_sparse.size(1), 1, v_tok.size(-1))
+            past_kr, past_v = cache.past(level)
+            return kernels.bdh_attn_decode(qr, past_kr, past_v, impl=impl)
+        kr_all, v_all = cache.span(level, T)
+        return kernels.bdh_attn_past(kr_all[:, :, S:], kr_all, v_all, S, impl=impl)
+
+    # ------------------------------------------------------------- forward
+    def forward(
+        self,
+        idx: torch.Tensor,
+        targets: Optional[torch.Tensor] = None,
+        *,
+        cache: Optional[KVCache] = None,
+        impl: Optional[str] = None,
+        last_only: bool = False,
+    ):
+        """Logits (B, T, V) (or (B, 1, V) with ``last_only``) and the loss when ``targets`` is given.
+
+        With ``cache`` the tokens continue the cached sequence: RoPE positions
+        start at ``cache.seq_len`` and every layer's RoPE(x) and V rows are
+        stored in the cache, which is committed at the end.
+        """
+        impl = kernels.resolve_attn_impl(impl)
+        cfg = self.config
+        B, T = idx.shape
+        nh, N = cfg.n_head, cfg.n_latent
+        rope_start = cache.seq_len if cache is not None else 0
+        need_table = impl != "hip" or (cache is not None and (cache.seq_len > 0 or T == 1))
+        cos_sin = kernels.rope_cos_sin(T, rope_start, self.freqs) if need_table else None
+
+        x = _ln(self.embed(idx))  # (B, T, D)
+        for level in range(cfg.n_layer):
+            x_bthn = _encode(x, self.encoder)
+            x_sparse = x_bthn.permute(0, 2, 1, 3)  # (B, nh, T, N) view
+            y_kv = self._attention(level, x_sparse, x.unsqueeze(1), rope_start, cache, impl, cos_sin)
+            y_bthn = _encode_heads(_ln(y_kv), self.encoder_v)
+            y_mlp = (x_bthn * y_bthn).view(B, T, nh * N) @ self.decoder
+            x = _ln(x + _ln(y_mlp))
+        if cache is not None:
+            cache.commit(T)
+        if last_only:
+            x = x[:, -1:]
+        logits = x @ self.lm_head
+        loss = None
+        if targets is not None:
+            loss = F.cross_entropy(logits.reshape(-1, logits.size(-1)).float(), targets.reshape(-1))
+        return logits, loss
+
+    # ------------------------------------------------------------ generate
+    @staticmethod
+    def sample(logits: torch.Tensor, temperature: float = 1.0, top_k: Optional[int] = None,
+               generator: Optional[torch.Generator] = None) -> torch.Tensor:
+        """One token per row from (B, V) fp32 logits (bdh.py:679-729): scale by
+        1/temperature; with top_k, softmax over the k largest and draw among them."""
+        if temperature != 1.0:
+            logits = logits / temperature
+        if top_k is not None and top_k < logits.size(-1):
+            values, indices = torch.topk(logits, top_k, dim=-1)
+            pick = torch.multinomial(torch.softmax(values, dim=-1), 1, generator=generator)
+            return indices.gather(1, pick)
+        return torch.multinomial(torch.softmax(logits, dim=-1), 1, generator=generator)
+
+    @torch.no_grad()
+    def generate(
+        self,
+        idx: torch.Tensor,
+        max_new_tokens: int,
+        temperature: float = 1.0,
+        top_k: Optional[int] = None,
+        *,
+        cache_dtype: Optional[torch.dtype] = None,
+        amp_dtype: Optional[torch.dtype] = None,
+        impl: Optional[str] = None,
+        generator: Optional[torch.Generator] = None,
+    ) -> torch.Tensor:
+        """Prompt prefill into a packed cache, then one cached forward per new
+        token (bdh.py:1074-1193).  Returns (B, prompt + max_new_tokens) tokens."""
+        B, P = idx.shape
+        dtype = cache_dtype or amp_dtype or torch.float32
+        cache = KVCache(self.config, B, P + max_new_tokens, dtype, idx.device)
+        out = torch.empty(B, P + max_new_tokens, dtype=idx.dtype, device=idx.device)
+        out[:, :P] = idx
+        ctx = (torch.autocast(idx.device.type, dtype=amp_dtype) if amp_dtype is not None
+               else torch.autocast(idx.device.type, enabled=False))
+        with ctx:
+            logits, _ = self(idx, cache=cache, impl=impl, last_only=True)
+            for t in range(max_new_tokens):
+                nxt = self.sample(logits[:, -1].float(), temperature, top_k, generator)
+                out[:, P + t] = nxt[:, 0]
+                logits, _ = self(nxt, cache=cache, impl=impl, last_only=True)
+        return out
+
+
+__all__ = ["BDHConfig", "BDH", "KVCache"]

@@ -22,8 +22,10 @@ def eager_tril_attn(Q: torch.Tensor, K: torch.Tensor, V: torch.Tensor) -> torch.
     """Materialise full T x T scores, ``tril_(-1)``, then ``@ V`` (kernels/attention.py:27-40).
 
     Q, K: (B, H, T, N); V: (B, 1, T, D) or (B, H, T, D) -> (B, H, T, D).
+    Kᵀ is materialised before the batched product: bf16 batched products with
+    a transposed-view operand have faulted ROCm GPUs.  Same values.
     """
-    scores = Q @ K.transpose(-2, -1)
+    scores = Q @ K.transpose(-2, -1).contiguous()
     scores.tril_(diagonal=-1)
     return scores @ V
 
@@ -49,9 +51,9 @@ def _two_gemm_decode(Q: torch.Tensor, K: torch.Tensor, V: torch.Tensor) -> torch
     if S == 0:
         return Q.new_zeros(B, H, Tq, D)
     if Tq == 1 and V.size(1) == H:
-        scores = torch.bmm(Q.reshape(B * H, 1, N), K.reshape(B * H, S, N).transpose(1, 2))
+        scores = torch.bmm(Q.reshape(B * H, 1, N), K.reshape(B * H, S, N).transpose(1, 2).contiguous())
         return torch.bmm(scores, V.reshape(B * H, S, D)).view(B, H, 1, D)
-    return (Q @ K.transpose(-2, -1)) @ V
+    return (Q @ K.transpose(-2, -1).contiguous()) @ V
 
 
 def eager_decode_attn(Q: torch.Tensor, K: torch.Tensor, V: torch.Tensor) -> torch.Tensor:

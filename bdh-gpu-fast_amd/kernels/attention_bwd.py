@@ -32,11 +32,16 @@ def analytic_tril_attn_backward(Q, K, V, dO):
     D = V.shape[-1]
     bcast = V.size(1) == 1 and H != 1
     Vh = V.expand(B, H, T, D) if bcast else V
-    M = (Q @ K.transpose(-2, -1)).tril(diagonal=-1)
-    dS = (dO @ Vh.transpose(-2, -1)).tril(diagonal=-1)
+    # transposed operands are materialised (bf16 batched products on transposed
+    # views have faulted ROCm GPUs); the values are the same
+    def t(x):
+        return x.transpose(-2, -1).contiguous()
+
+    M = (Q @ t(K)).tril(diagonal=-1)
+    dS = (dO @ t(Vh)).tril(diagonal=-1)
     dQ = dS @ K
-    dK = dS.transpose(-2, -1) @ Q
-    dVh = M.transpose(-2, -1) @ dO
+    dK = t(dS) @ Q
+    dVh = t(M) @ dO
     dV = dVh.sum(dim=1, keepdim=True) if bcast else dVh
     return dQ, dK, dV
 

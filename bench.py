@@ -20,8 +20,12 @@ The JSON line also carries:
     workload, in the same unit.
   * ``extra``: other hot-path legs (decode step GB/s at C3, training op
     fwd+bwd TFLOP/s at C4, the unfused path and torch eager on the GPU).
+  * ``models``: the model harness (``bdh_harness.BDH``, random N(0, 0.02^2)
+    weights, uniform byte tokens) at C2 and C5 (prefill tok/s, bf16 autocast)
+    and C3 (``generate`` tok/s with a bf16 packed cache), HIP attention beside
+    the same model with eager attention.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extra]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extra] [--no-models]
 """
 
 from __future__ import annotations
@@ -46,6 +50,9 @@ PEAK_HBM_GBS = 8000.0
 C1 = dict(B=8, nh=4, T=512, N=8192, D=256)
 C3 = dict(B=64, nh=4, N=8192, D=256, S=(256, 384, 511))
 C4 = dict(B=16, nh=4, T=1024, N=8192, D=256)
+C2 = dict(n_layer=6, D=256, nh=4, mult=128, B=32, T=512)
+C5 = dict(n_layer=8, D=512, nh=8, mult=128, B=4, T=2048)
+C3_GEN = dict(n_layer=6, D=256, nh=4, mult=128, B=64, prompt=256, new=256, top_k=3, seed=5)
 CALIB_BYTES = 1 << 29  # reference elementwise pass that scales the HBM byte counters
 
 
@@ -147,6 +154,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--no-extra", action="store_true", help="skip the decode / backward / comparison legs")
+    ap.add_argument("--no-models", action="store_true", help="skip the model-harness legs (C2, C3, C5)")
     ap.add_argument(
         "--calibrate",
         action="store_true",
@@ -226,6 +234,10 @@ def main() -> int:
     if not args.no_extra:
         extra = run_extra(torch, ext, kernels, dev, max(3, args.steps // 5), max(2, args.warmup // 5), x, v)
 
+    models: dict = {}
+    if not args.no_models:
+        models = run_models(torch, ext, dev)
+
     cpu = None
     if not args.no_cpu:
         log("[bench] cpu baseline (oracle on host cores)...")
@@ -258,6 +270,7 @@ def main() -> int:
         "roofline": roofline,
         "cpu_baseline": cpu,
         "extra": extra,
+        "models": models,
     }
     print(json.dumps(line), flush=True)
     return 0
@@ -325,6 +338,83 @@ def run_extra(torch, ext, kernels, dev, steps, warmup, x, v) -> dict:
         ms_t = time_steps(fn, max(2, steps // 2), 1)
         out[key] = {"us": ms_t * 1e3, "tflops": F4 / ms_t / 1e9, "frac_bf16_peak": F4 / ms_t / 1e9 / PEAK_BF16_TFLOPS}
         log(f"[bench] {key}: {ms_t * 1e3:.1f} us, {F4 / ms_t / 1e9:.1f} TFLOP/s")
+    return out
+
+
+def run_models(torch, ext, dev) -> dict:
+    """Model harness legs: prefill tok/s (C2, C5) and generate tok/s (C3)."""
+    import bdh_harness as H
+
+    out: dict = {}
+
+    def build(c):
+        torch.manual_seed(0)
+        cfg = H.BDHConfig(n_layer=c["n_layer"], n_embd=c["D"], n_head=c["nh"], mlp_internal_dim_multiplier=c["mult"])
+        return H.BDH(cfg).to(dev)
+
+    for name, c in (("c2_prefill", C2), ("c5_long_prefill", C5)):
+        m = build(c)
+        g = torch.Generator(device=dev).manual_seed(1)
+        idx = torch.randint(0, 256, (c["B"], c["T"]), generator=g, device=dev)
+        leg = {"B": c["B"], "T": c["T"], "n_layer": c["n_layer"], "D": c["D"], "nh": c["nh"]}
+        for impl in ("hip", "eager"):
+            log(f"[bench] {name} {impl} ...")
+
+            def fwd():
+                with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+                    return m(idx, impl=impl)[0]
+            ms = time_steps(fwd, 3, 1)
+            leg[impl] = {"ms": ms, "tok_s": c["B"] * c["T"] / (ms * 1e-3)}
+        ext.profile_enable(True)
+        fwd_hip = lambda: m(idx, impl="hip")  # noqa: E731
+        with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+            fwd_hip()
+        rec = ext.profile_collect()
+        ext.profile_enable(False)
+        leg["hip"]["attention_kernels_ms"] = sum(t for _, t in rec)
+        out[name] = leg
+        log(f"[bench] {name}: hip {leg['hip']['tok_s']:.0f} tok/s ({leg['hip']['ms']:.2f} ms, attention kernels "
+            f"{leg['hip']['attention_kernels_ms']:.2f} ms), eager {leg['eager']['tok_s']:.0f} tok/s")
+        del m, idx
+        torch.cuda.empty_cache()
+
+    c = C3_GEN
+    m = build(c)
+    g = torch.Generator(device=dev).manual_seed(2)
+    prompt = torch.randint(0, 256, (c["B"], c["prompt"]), generator=g, device=dev)
+    leg = {"B": c["B"], "prompt": c["prompt"], "new_tokens": c["new"], "top_k": c["top_k"], "cache": "bf16"}
+    for impl in ("hip", "eager"):
+        log(f"[bench] c3_generate {impl} ...")
+
+        def gen():
+            return m.generate(prompt, c["new"], top_k=c["top_k"], cache_dtype=torch.bfloat16,
+                              amp_dtype=torch.bfloat16, impl=impl,
+                              generator=torch.Generator(device=dev).manual_seed(c["seed"]))
+        gen()  # warm-up (allocator, library)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        gen()
+        torch.cuda.synchronize()
+        s = time.perf_counter() - t0
+        leg[impl] = {"s": s, "tok_s": c["B"] * c["new"] / s}
+        if impl == "hip":
+            ext.profile_enable(True)
+            gen()
+            rec = ext.profile_collect()
+            ext.profile_enable(False)
+            dec = [t for n, t in rec if n.startswith("k_decode")]
+            Nl = c["mult"] * c["D"] // c["nh"]
+            by = sum(2 * (c["B"] * c["nh"] * S * Nl + c["B"] * S * c["D"] + c["B"] * c["nh"] * Nl + c["B"] * c["nh"] * c["D"])
+                     for S in range(c["prompt"], c["prompt"] + c["new"])) * c["n_layer"]
+            leg[impl]["decode_attention_ms"] = sum(dec)
+            leg[impl]["decode_attention_gbs"] = by / (sum(dec) * 1e-3) / 1e9 if dec else None
+            leg[impl]["library_kernels_ms"] = sum(t for _, t in rec)
+    out["c3_generate"] = leg
+    log(f"[bench] c3_generate: hip {leg['hip']['tok_s']:.0f} tok/s ({leg['hip']['s']:.3f} s; decode attention "
+        f"{leg['hip']['decode_attention_ms']:.1f} ms, {leg['hip']['decode_attention_gbs']:.0f} GB/s), "
+        f"eager {leg['eager']['tok_s']:.0f} tok/s")
+    del m
+    torch.cuda.empty_cache()
     return out
 
 
