@@ -1370,8 +1370,8 @@ bool sy_cold_check(const bdh_tensor4* q, const bdh_tensor4* k, const bdh_tensor4
          q->stride[2] == k->stride[2];
   if (rope && !self) return false;
   if (T < 1 || N < 64 || N % 64 != 0 || !rows16(q) || !rows16(k)) return false;
-  // score x V: 8-element (16 / 32-byte) V row chunks, at most 256 columns
-  if (v->size[3] > 256 || v->size[3] % 8 != 0 || !rows16(v)) return false;
+  // score x V: 8-element (16 / 32-byte) V row chunks, 256 columns per launch
+  if (v->size[3] % 8 != 0 || !rows16(v)) return false;
   if (((T - 1) * std::max(q->stride[2], k->stride[2]) + N) * 2 >= (int64_t(1) << 31)) return false;
   if (rope && std::max<int64_t>(T, 128 * ((T + kSyTile - 1) / kSyTile)) * N * 2 >= (int64_t(1) << 31)) return false;
   if (T > 65535) return false;
@@ -1388,7 +1388,8 @@ bool sy_cold_check(const bdh_tensor4* q, const bdh_tensor4* k, const bdh_tensor4
 bool sy_keeps_scores(const bdh_tensor4* q, const bdh_tensor4* v, size_t* scores_bytes) {
   SyPlan p;
   bool self = false;
-  if (v->size[3] < 1 || !sy_cold_check(q, q, v, false, nullptr, p, self) || !self) return false;
+  // the backward from saved tiles (sy_bwd_dv) takes at most 256 columns of V
+  if (v->size[3] < 1 || v->size[3] > 256 || !sy_cold_check(q, q, v, false, nullptr, p, self) || !self) return false;
   if (scores_bytes) *scores_bytes = p.part_bytes;
   return true;
 }
@@ -1485,8 +1486,17 @@ int sy_run(const bdh_tensor4* q, const bdh_tensor4* k, const bdh_tensor4* v, con
   sa.past = int(past);
   const dim3 gsv(unsigned((T + 63) / 64 - sa.rb0), unsigned(nslab));
   const bool o16 = out->dtype == BDH_BF16, v16 = v->dtype == BDH_BF16;
-  if (o16) return v16 ? launch_sy_sv<bf16_t, bf16_t>(sa, gsv, s) : launch_sy_sv<bf16_t, float>(sa, gsv, s);
-  return v16 ? launch_sy_sv<float, bf16_t>(sa, gsv, s) : launch_sy_sv<float, float>(sa, gsv, s);
+  // one launch per 256 columns of V (the score tiles are read again by each)
+  for (int64_t d0 = 0; d0 < Dv; d0 += 256) {
+    SvArgs sc = sa;
+    sc.v.p = static_cast<const char*>(v->data) + d0 * esize(v->dtype);
+    sc.o.p = static_cast<const char*>(out->data) + d0 * esize(out->dtype);
+    sc.D = int(std::min<int64_t>(256, Dv - d0));
+    const int rc = o16 ? (v16 ? launch_sy_sv<bf16_t, bf16_t>(sc, gsv, s) : launch_sy_sv<bf16_t, float>(sc, gsv, s))
+                       : (v16 ? launch_sy_sv<float, bf16_t>(sc, gsv, s) : launch_sy_sv<float, float>(sc, gsv, s));
+    if (rc != BDH_OK) return rc;
+  }
+  return BDH_OK;
 }
 
 }  // namespace

@@ -175,3 +175,30 @@ def test_bf16_long_sequences_stay_on_score_tile_path(mode):
     g = np_of(got)
     assert rel_fro(g, want) <= TOL[BF]
     assert not g[:, :, 0].any()
+
+
+@pytest.mark.parametrize("mode", ["self", "rope", "past"])
+@pytest.mark.parametrize("D", [392, 512])
+def test_bf16_wide_v_runs_score_tiles_per_256_columns(mode, D):
+    """V wider than 256 columns (C5: D = 512): the score tiles are computed
+    once and score x V runs once per 256 columns (the last slice ragged at
+    D = 392); results against the oracle, fp32 V for the fused-RoPE case."""
+    B, H, T, N = 2, 2, 300, 256
+    print(f"wide V {mode} D={D}", flush=True)
+    x = _bf(latent((B, H, T, N), 23))
+    v = _bf(normal((B, 1, T, D), 24))
+    if mode == "self":
+        fn = lambda: ext.tril_score_v(to_dev(x, BF), to_dev(x, BF), to_dev(v, BF))  # noqa: E731
+        want = O.tril_score_v_cpu(x, x, v)
+    elif mode == "rope":
+        freqs = O.get_freqs(N)
+        f = torch.from_numpy(freqs).to(DEV)
+        fn = lambda: ext.tril_rope_score_v(to_dev(x, BF), to_dev(v, torch.float32), f, 0)  # noqa: E731
+        want, _ = O.tril_rope_score_v(x, v, freqs, 0, bf16=True)
+    else:
+        past = 100
+        xd = to_dev(x, BF)
+        fn = lambda: ext.tril_score_v_past(xd[:, :, past:], xd, to_dev(v, BF), past)  # noqa: E731
+        want = O.tril_score_v_past(x[:, :, past:], x, v, past)
+    got = np_of(_ran_score_tiles(fn))
+    assert rel_fro(got, want) <= TOL[BF]
