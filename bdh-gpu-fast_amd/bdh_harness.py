@@ -112,6 +112,32 @@ def _encode_heads(y: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
     return F.relu(torch.stack(outs, dim=1)).view(B, T, nh, w.size(2))
 
 
+# Inference forms on the HIP path (no autograd, so no backward products):
+def _compute_dtype(t: torch.Tensor) -> torch.dtype:
+    return torch.get_autocast_dtype(t.device.type) if torch.is_autocast_enabled(t.device.type) else t.dtype
+
+
+def _encode_relu_epilogue(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+    """The encoder GEMM with the ReLU applied in its epilogue (hipBLASLt), (B, T, nh, N)."""
+    nh, D, N = w.shape
+    dt = _compute_dtype(x)
+    wc = w.permute(1, 0, 2).reshape(D, nh * N).to(dt)
+    zero = torch.zeros(nh * N, dtype=dt, device=x.device)
+    return torch._addmm_activation(zero, x.reshape(-1, D).to(dt), wc).view(*x.shape[:-1], nh, N)
+
+
+def _gated_product(x_bthn: torch.Tensor, y_ln: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+    """x_bthn * relu(encoder_v GEMM): one batched GEMM (nh, B*T, D) @ (nh, D, N) on
+    contiguous operands into head-major rows, then one HIP pass that applies
+    the ReLU, multiplies by x and writes token-major (B, T, nh, N)."""
+    B, T, nh, N = x_bthn.shape
+    D = y_ln.size(-1)
+    dt = _compute_dtype(x_bthn)
+    a = y_ln.permute(1, 0, 2, 3).reshape(nh, B * T, D).to(dt)
+    y = torch.bmm(a, w.to(dt))  # (nh, B*T, N)
+    return kernels.relu_mul(x_bthn, y.view(nh, B, T, N).permute(1, 2, 0, 3))
+
+
 class BDH(nn.Module):
     """BDH language model; parameter names and shapes follow bdh_baseline.py:80-102."""
 
@@ -175,13 +201,17 @@ class BDH(nn.Module):
         need_table = impl != "hip" or (cache is not None and (cache.seq_len > 0 or T == 1))
         cos_sin = kernels.rope_cos_sin(T, rope_start, self.freqs) if need_table else None
 
+        fast = impl == "hip" and not torch.is_grad_enabled()
         x = _ln(self.embed(idx))  # (B, T, D)
         for level in range(cfg.n_layer):
-            x_bthn = _encode(x, self.encoder)
+            x_bthn = _encode_relu_epilogue(x, self.encoder) if fast else _encode(x, self.encoder)
             x_sparse = x_bthn.permute(0, 2, 1, 3)  # (B, nh, T, N) view
             y_kv = self._attention(level, x_sparse, x.unsqueeze(1), rope_start, cache, impl, cos_sin)
-            y_bthn = _encode_heads(_ln(y_kv), self.encoder_v)
-            y_mlp = (x_bthn * y_bthn).view(B, T, nh * N) @ self.decoder
+            if fast:
+                xy = _gated_product(x_bthn, _ln(y_kv), self.encoder_v)
+            else:
+                xy = x_bthn * _encode_heads(_ln(y_kv), self.encoder_v)
+            y_mlp = xy.view(B, T, nh * N) @ self.decoder
             x = _ln(x + _ln(y_mlp))
         if cache is not None:
             cache.commit(T)

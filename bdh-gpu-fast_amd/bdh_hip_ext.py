@@ -41,6 +41,7 @@ __all__ = [
     "tril_score_v_bwd_saved",
     "tril_rope_score_v_bwd",
     "rope_rotate",
+    "relu_mul",
     "profile_enable",
     "profile_collect",
     "launch_count",
@@ -68,6 +69,7 @@ EXPORTED_SYMBOLS = (
     "bdh_tril_score_v_bwd_saved",
     "bdh_tril_rope_score_v_bwd_workspace",
     "bdh_tril_rope_score_v_bwd",
+    "bdh_relu_mul",
     "bdh_profile_enable",
     "bdh_profile_collect",
 )
@@ -122,6 +124,7 @@ def _load():
         "bdh_tril_score_v_bwd_saved": (ctypes.c_int, [P, P, P, P, P, vp, sz, vp, sz, vp]),
         "bdh_tril_rope_score_v_bwd_workspace": (sz, [i64, i64, i64, i64, i64, i64, i32]),
         "bdh_tril_rope_score_v_bwd": (ctypes.c_int, [P, P, P, fp, i64, P, P, vp, sz, vp]),
+        "bdh_relu_mul": (ctypes.c_int, [P, P, P, vp]),
         "bdh_profile_enable": (None, [i32]),
         "bdh_profile_collect": (ctypes.c_int, [ctypes.c_char_p, i32, fp, i32]),
     }
@@ -460,6 +463,20 @@ def rope_rotate(
 
 
 # ---------------------------------------------------------------- profiling
+def relu_mul(x: torch.Tensor, y: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """``x * relu(y)`` elementwise for 4-D views of one shape; ``out`` defaults to a
+    contiguous tensor in x's dtype."""
+    dev = _require_device(x, y, out)
+    if x.dim() != 4 or y.shape != x.shape:
+        raise ValueError(f"relu_mul: x and y must be 4-D of one shape, got {tuple(x.shape)} and {tuple(y.shape)}")
+    if out is None:
+        out = torch.empty(x.shape, dtype=x.dtype, device=dev)
+    with torch.cuda.device(dev):
+        rc = _lib.bdh_relu_mul(ctypes.byref(_t4(x)), ctypes.byref(_t4(y)), ctypes.byref(_t4(out)), _stream(dev))
+    _check(rc, "relu_mul")
+    return out
+
+
 def profile_enable(on: bool = True) -> None:
     """Bracket every library kernel launch with HIP events (on its stream)."""
     _lib.bdh_profile_enable(1 if on else 0)

@@ -41,6 +41,7 @@ from .hip_attn import (
     ext_status,
     has_hip_ext,
     has_hip_kernel,
+    relu_mul,
     tril_decode,
     tril_rope_score_v,
     tril_score_v,
@@ -76,6 +77,7 @@ __all__ = [
     "eager_past_attn",
     "tril_score_v",
     "tril_score_v_past",
+    "relu_mul",
     "tril_rope_score_v",
     "tril_decode",
     "has_hip_ext",

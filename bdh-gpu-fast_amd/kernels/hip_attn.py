@@ -128,6 +128,12 @@ def tril_score_v_past(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, past: i
     return ext.tril_score_v_past(_last_dim_unit(q), _last_dim_unit(k), _last_dim_unit(v), past)
 
 
+def relu_mul(x: torch.Tensor, y: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """``x * relu(y)`` on the GPU (the BDH layer's gated product, bdh.py:914-945)."""
+    ext = _require(x, y, out)
+    return ext.relu_mul(_last_dim_unit(x), _last_dim_unit(y), out)
+
+
 def tril_rope_score_v(
     x: torch.Tensor,
     v: torch.Tensor,
@@ -223,6 +229,7 @@ __all__ = [
     "hip_available",
     "tril_score_v",
     "tril_score_v_past",
+    "relu_mul",
     "tril_rope_score_v",
     "tril_decode",
     "tril_score_v_bwd",

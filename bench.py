@@ -371,10 +371,12 @@ def run_models(torch, ext, dev) -> dict:
             fwd_hip()
         rec = ext.profile_collect()
         ext.profile_enable(False)
-        leg["hip"]["attention_kernels_ms"] = sum(t for _, t in rec)
+        leg["hip"]["attention_kernels_ms"] = sum(t for n, t in rec if n != "k_relu_mul")
+        leg["hip"]["relu_mul_ms"] = sum(t for n, t in rec if n == "k_relu_mul")
         out[name] = leg
         log(f"[bench] {name}: hip {leg['hip']['tok_s']:.0f} tok/s ({leg['hip']['ms']:.2f} ms, attention kernels "
-            f"{leg['hip']['attention_kernels_ms']:.2f} ms), eager {leg['eager']['tok_s']:.0f} tok/s")
+            f"{leg['hip']['attention_kernels_ms']:.2f} ms, relu_mul {leg['hip']['relu_mul_ms']:.2f} ms), "
+            f"eager {leg['eager']['tok_s']:.0f} tok/s")
         del m, idx
         torch.cuda.empty_cache()
 

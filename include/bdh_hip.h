@@ -194,6 +194,18 @@ int bdh_tril_rope_score_v_bwd(const bdh_tensor4* x, const bdh_tensor4* v,
                               size_t workspace_bytes, bdh_stream stream);
 
 /*
+ * Consumer of the attention in the BDH layer: out = x * max(y, 0), elementwise.
+ * Replaces the ReLU of encoder_v's output (bdh.py:914-925, `_bias_relu_`) and
+ * the sparse product of _mlp_merge (bdh.py:927-945, `x_bthn * y_bthn`) in one
+ * pass.  x, y, out: 4-D views of equal sizes, each in its own dtype, so y can
+ * be the head-major (nh, B, T, N) output of a batched GEMM viewed as
+ * (B, T, nh, N).  The product is formed in fp32 and rounded once to out's
+ * dtype; NaN in y propagates as in torch's relu.
+ */
+int bdh_relu_mul(const bdh_tensor4* x, const bdh_tensor4* y, const bdh_tensor4* out,
+                 bdh_stream stream);
+
+/*
  * Per-kernel timing (measurement support; no counterpart in the reference).
  * While enabled, every kernel the library launches is bracketed by HIP events
  * on its stream.  bdh_profile_collect() waits for the recorded events and

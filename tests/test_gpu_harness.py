@@ -130,3 +130,26 @@ def test_generate_end_to_end_bf16():
                      generator=torch.Generator(device=DEV).manual_seed(5))
     assert out.shape == (4, 80) and torch.equal(out[:, :64], idx)
     assert int(out.min()) >= 0 and int(out.max()) < 256
+
+
+@pytest.mark.parametrize("dx,dy", [(torch.bfloat16, torch.bfloat16), (torch.float32, torch.float32),
+                                   (torch.bfloat16, torch.float32)])
+@pytest.mark.parametrize("N", [2048, 200, 37])
+def test_relu_mul_equals_torch(dx, dy, N):
+    """out = x * relu(y) with y the head-major (nh, B, T, N) tensor viewed as
+    (B, T, nh, N): equal to torch's product in x's dtype (8-wide and ragged
+    rows), NaN in y propagates like torch's relu."""
+    print(f"relu_mul {dx} {dy} N={N}", flush=True)
+    B, T, nh = 2, 33, 3
+    g = torch.Generator(device=DEV).manual_seed(N)
+    x = torch.randn(B, T, nh, N, generator=g, device=DEV).to(dx)
+    y_hm = torch.randn(nh, B, T, N, generator=g, device=DEV).to(dy)
+    y_hm[0, 0, 0, 0] = float("nan")
+    y = y_hm.permute(1, 2, 0, 3)
+    got = ext.relu_mul(x, y)
+    want = (x.float() * torch.relu(y.float())).to(dx)
+    assert got.shape == x.shape and got.dtype == dx and got.is_contiguous()
+    assert torch.isnan(got[0, 0, 0, 0])
+    assert torch.equal(got.nan_to_num(7.0), want.nan_to_num(7.0))
+    with pytest.raises(RuntimeError):
+        ext.relu_mul(x, x, out=x)  # out overlaps an input
