@@ -117,22 +117,28 @@ def _compute_dtype(t: torch.Tensor) -> torch.dtype:
     return torch.get_autocast_dtype(t.device.type) if torch.is_autocast_enabled(t.device.type) else t.dtype
 
 
-def _encode_relu_epilogue(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
-    """The encoder GEMM with the ReLU applied in its epilogue (hipBLASLt), (B, T, nh, N)."""
-    nh, D, N = w.shape
-    dt = _compute_dtype(x)
-    wc = w.permute(1, 0, 2).reshape(D, nh * N).to(dt)
-    zero = torch.zeros(nh * N, dtype=dt, device=x.device)
-    return torch._addmm_activation(zero, x.reshape(-1, D).to(dt), wc).view(*x.shape[:-1], nh, N)
+def _encode_relu_epilogue(x: torch.Tensor, wc: torch.Tensor, zero: torch.Tensor, nh: int) -> torch.Tensor:
+    """The encoder GEMM with the ReLU applied in its epilogue (hipBLASLt): x (B, T, D) @
+    wc (D, nh*N) with a zero bias -> (B, T, nh, N)."""
+    D = x.size(-1)
+    out = torch._addmm_activation(zero, x.reshape(-1, D).to(wc.dtype), wc)
+    return out.view(*x.shape[:-1], nh, wc.size(1) // nh)
 
 
-def _gated_product(x_bthn: torch.Tensor, y_ln: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
-    """x_bthn * relu(encoder_v GEMM): one batched GEMM (nh, B*T, D) @ (nh, D, N) on
-    contiguous operands into head-major rows, then one HIP pass that applies
-    the ReLU, multiplies by x and writes token-major (B, T, nh, N)."""
+def _gated_product(x_bthn: torch.Tensor, y_ln: torch.Tensor, w: torch.Tensor, wt=None) -> torch.Tensor:
+    """x_bthn * relu(encoder_v GEMM), token-major (B, T, nh, N).
+
+    bf16 (K a multiple of 32, N of 8): one HIP kernel, the GEMM with the gated
+    product as its epilogue (its output never reaches HBM).  Otherwise one
+    batched GEMM (nh, B*T, D) @ (nh, D, N) on contiguous operands into
+    head-major rows, then one HIP pass for the ReLU and the product."""
     B, T, nh, N = x_bthn.shape
     D = y_ln.size(-1)
     dt = _compute_dtype(x_bthn)
+    if dt == torch.bfloat16 and x_bthn.dtype == torch.bfloat16 and D % 32 == 0 and N % 8 == 0:
+        if wt is None:
+            wt = w.transpose(1, 2).to(dt).contiguous()  # (nh, N, D)
+        return kernels.gated_gemm(y_ln.to(dt).contiguous(), wt, x_bthn)
     a = y_ln.permute(1, 0, 2, 3).reshape(nh, B * T, D).to(dt)
     y = torch.bmm(a, w.to(dt))  # (nh, B*T, N)
     return kernels.relu_mul(x_bthn, y.view(nh, B, T, N).permute(1, 2, 0, 3))
@@ -152,6 +158,26 @@ class BDH(nn.Module):
         nn.init.normal_(self.embed.weight, mean=0.0, std=0.02)
         self.lm_head = nn.Parameter(torch.empty(D, V).normal_(std=0.02))
         self.register_buffer("freqs", kernels.get_freqs(N), persistent=False)
+        self._wcache: dict = {}
+
+    def _prepared(self, dt: torch.dtype):
+        """Inference layouts of the weights in the compute dtype, rebuilt when a weight changes:
+        encoder as (D, nh*N) with a zero bias (ReLU-epilogue GEMM), encoder_v transposed to
+        (nh, N, D) (gated GEMM), decoder (nh*N, D)."""
+        key = tuple((p.data_ptr(), p._version) for p in (self.encoder, self.encoder_v, self.decoder))
+        hit = self._wcache.get(dt)
+        if hit is not None and hit[0] == key:
+            return hit[1]
+        nh, D, N = self.encoder.shape
+        with torch.no_grad():
+            prep = {
+                "enc": self.encoder.permute(1, 0, 2).reshape(D, nh * N).to(dt).contiguous(),
+                "zero": torch.zeros(nh * N, dtype=dt, device=self.encoder.device),
+                "encv_t": self.encoder_v.transpose(1, 2).to(dt).contiguous(),
+                "dec": self.decoder.to(dt).contiguous(),
+            }
+        self._wcache = {dt: (key, prep)}
+        return prep
 
     # ----------------------------------------------------------- attention
     def _attention(self, level, x_sparse, v_tok, rope_start, cache, impl, cos_sin):
@@ -203,15 +229,24 @@ class BDH(nn.Module):
 
         fast = impl == "hip" and not torch.is_grad_enabled()
         x = _ln(self.embed(idx))  # (B, T, D)
+        prep = self._prepared(_compute_dtype(x)) if fast else None
         for level in range(cfg.n_layer):
-            x_bthn = _encode_relu_epilogue(x, self.encoder) if fast else _encode(x, self.encoder)
+            if fast:
+                x_bthn = _encode_relu_epilogue(x, prep["enc"], prep["zero"], nh)
+            else:
+                x_bthn = _encode(x, self.encoder)
             x_sparse = x_bthn.permute(0, 2, 1, 3)  # (B, nh, T, N) view
             y_kv = self._attention(level, x_sparse, x.unsqueeze(1), rope_start, cache, impl, cos_sin)
             if fast:
-                xy = _gated_product(x_bthn, _ln(y_kv), self.encoder_v)
+                xy = _gated_product(x_bthn, _ln(y_kv), self.encoder_v, prep["encv_t"])
+                if B * T <= 256 and xy.dtype == torch.bfloat16:
+                    # few rows (decode): split-K GEMM instead of a few tiles down K = nh*N
+                    y_mlp = kernels.small_gemm(xy.view(B * T, nh * N), prep["dec"]).view(B, T, -1)
+                else:
+                    y_mlp = xy.view(B, T, nh * N) @ prep["dec"]
             else:
                 xy = x_bthn * _encode_heads(_ln(y_kv), self.encoder_v)
-            y_mlp = xy.view(B, T, nh * N) @ self.decoder
+                y_mlp = xy.view(B, T, nh * N) @ self.decoder
             x = _ln(x + _ln(y_mlp))
         if cache is not None:
             cache.commit(T)

@@ -42,6 +42,8 @@ __all__ = [
     "tril_rope_score_v_bwd",
     "rope_rotate",
     "relu_mul",
+    "gated_gemm",
+    "small_gemm",
     "profile_enable",
     "profile_collect",
     "launch_count",
@@ -70,6 +72,9 @@ EXPORTED_SYMBOLS = (
     "bdh_tril_rope_score_v_bwd_workspace",
     "bdh_tril_rope_score_v_bwd",
     "bdh_relu_mul",
+    "bdh_gated_gemm",
+    "bdh_small_gemm_workspace",
+    "bdh_small_gemm",
     "bdh_profile_enable",
     "bdh_profile_collect",
 )
@@ -125,6 +130,9 @@ def _load():
         "bdh_tril_rope_score_v_bwd_workspace": (sz, [i64, i64, i64, i64, i64, i64, i32]),
         "bdh_tril_rope_score_v_bwd": (ctypes.c_int, [P, P, P, fp, i64, P, P, vp, sz, vp]),
         "bdh_relu_mul": (ctypes.c_int, [P, P, P, vp]),
+        "bdh_gated_gemm": (ctypes.c_int, [P, P, P, P, vp]),
+        "bdh_small_gemm_workspace": (sz, [i64, i64, i64]),
+        "bdh_small_gemm": (ctypes.c_int, [P, P, P, vp, sz, vp]),
         "bdh_profile_enable": (None, [i32]),
         "bdh_profile_collect": (ctypes.c_int, [ctypes.c_char_p, i32, fp, i32]),
     }
@@ -474,6 +482,37 @@ def relu_mul(x: torch.Tensor, y: torch.Tensor, out: Optional[torch.Tensor] = Non
     with torch.cuda.device(dev):
         rc = _lib.bdh_relu_mul(ctypes.byref(_t4(x)), ctypes.byref(_t4(y)), ctypes.byref(_t4(out)), _stream(dev))
     _check(rc, "relu_mul")
+    return out
+
+
+def gated_gemm(y: torch.Tensor, wt: torch.Tensor, x: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """``x * relu(y @ wt^T)`` per head, bf16: y (B, nh, T, K), wt (nh, N, K), x (B, T, nh, N)."""
+    dev = _require_device(y, wt, x, out)
+    if wt.dim() != 3:
+        raise ValueError(f"gated_gemm: wt must be (nh, N, K), got {tuple(wt.shape)}")
+    if out is None:
+        out = torch.empty(x.shape, dtype=x.dtype, device=dev)
+    with torch.cuda.device(dev):
+        rc = _lib.bdh_gated_gemm(ctypes.byref(_t4(y)), ctypes.byref(_t4(wt.unsqueeze(0))), ctypes.byref(_t4(x)),
+                                 ctypes.byref(_t4(out)), _stream(dev))
+    _check(rc, "gated_gemm")
+    return out
+
+
+def small_gemm(a: torch.Tensor, b: torch.Tensor, out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
+    """``a @ b`` for few rows of a: a (M, K), b (K, D) bf16 -> (M, D) in ``out_dtype`` (default a's)."""
+    dev = _require_device(a, b)
+    if a.dim() != 2 or b.dim() != 2 or a.size(1) != b.size(0):
+        raise ValueError(f"small_gemm: a (M, K) and b (K, D), got {tuple(a.shape)} and {tuple(b.shape)}")
+    M, K = a.shape
+    D = b.size(1)
+    out = torch.empty(M, D, dtype=out_dtype or a.dtype, device=dev)
+    with torch.cuda.device(dev):
+        ws, nb = _workspace(_lib.bdh_small_gemm_workspace(M, K, D), dev)
+        rc = _lib.bdh_small_gemm(ctypes.byref(_t4(a.view(1, 1, M, K))), ctypes.byref(_t4(b.view(1, 1, K, D))),
+                                 ctypes.byref(_t4(out.view(1, 1, M, D))),
+                                 ws.data_ptr() if ws is not None else None, nb, _stream(dev))
+    _check(rc, "small_gemm")
     return out
 
 

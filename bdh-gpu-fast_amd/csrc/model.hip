@@ -11,6 +11,7 @@
 // product is formed in fp32 and rounded once to the output dtype, the same
 // value torch's bf16 / fp32 elementwise product gives.
 #include "common.h"
+#include "tile_gemm.h"
 
 namespace bdh {
 
@@ -79,6 +80,257 @@ __global__ __launch_bounds__(256) void k_relu_mul(ReluMulArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// encoder_v GEMM with the gated product as its epilogue:
+//   out[b,t,h,n] = x[b,t,h,n] * relu(sum_k y[b,h,t,k] * wt[h,n,k])       (bf16)
+// y is the LayerNorm of the attention output (B, nh, T, K), wt encoder_v
+// transposed to (nh, N, K), so both operands are K-contiguous rows.  y never
+// goes to HBM: the kernel reads x once and writes out once.
+//
+// Tiles of 256 rows (tokens) x 128 columns of one head, 8 waves of 64 x 64
+// (2 x 2 MFMA 32x32x16 blocks), K in stages of 32 double-buffered in LDS
+// (16-byte chunk c of row r at c ^ ((r >> 2) & 3), conflict-free fragment
+// reads).  Two workgroups per CU, so one tile's epilogue overlaps another's
+// main loop.  Tiles are taken in groups of 8 row blocks per column block
+// (A and B blocks of a group stay in L2), each XCD a contiguous range.
+// Epilogue: relu(acc) rounded to bf16 (the value the unfused GEMM would
+// store) goes to LDS, then 16-byte coalesced reads of x and stores of out.
+constexpr int kGM = 256, kGN = 128, kGK = 32;
+constexpr int kGStageA = kGM * 64, kGStageB = kGN * 64, kGStage = kGStageA + kGStageB;  // 24 KB
+constexpr int kGOutRow = kGN * 2 + 16;  // padded LDS row of the output tile (bytes)
+constexpr int kGLds = kGM * kGOutRow > 2 * kGStage ? kGM * kGOutRow : 2 * kGStage;
+constexpr int kGGroup = 8;
+
+struct GatedArgs {
+  const bf16_t* y;
+  int64_t y0, y1, y2;  // (B, nh, T, K)
+  const bf16_t* w;
+  int64_t w1, w2;      // (1, nh, N, K)
+  const bf16_t* x;
+  int64_t x0, x1, x2;  // (B, T, nh, N)
+  bf16_t* o;
+  int64_t o0, o1, o2;
+  int T, M, N, K, nmb, nnb;
+  int64_t total, per_xcd;
+};
+
+__device__ __forceinline__ f32x16 mma_bf16(bf16x8 a, bf16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ int g_sw(int row, int c) { return row * 64 + ((c ^ ((row >> 2) & 3)) * 16); }
+
+__global__ __launch_bounds__(512, 2) void k_gated_gemm(const GatedArgs a) {
+  __shared__ __attribute__((aligned(16))) uint8_t g_lds[kGLds];
+  const int bid = blockIdx.x, xcd = bid & 7, kk = bid >> 3;
+  if (kk >= a.per_xcd) return;
+  const int64_t t = int64_t(xcd) * a.per_xcd + kk;
+  if (t >= a.total) return;
+  // tile -> (head, row block, column block): groups of kGGroup row blocks, rows fastest
+  const int64_t per_head = int64_t(a.nmb) * a.nnb;
+  const int h = int(t / per_head);
+  const int g = int(t - int64_t(h) * per_head);
+  const int gm = g / (kGGroup * a.nnb);
+  const int gsz = min(kGGroup, a.nmb - gm * kGGroup);
+  const int q = g - gm * kGGroup * a.nnb;
+  const int mbi = gm * kGGroup + q % gsz, nbi = q / gsz;
+  const int m0 = mbi * kGM, n0 = nbi * kGN;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+
+  // loader: A rows lr and lr + 128, B row lr; 16-byte chunk lc of the 64-byte stage row
+  const int lr = tid >> 2, lc = tid & 3;
+  const bf16_t* ap[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int m = min(m0 + lr + 128 * i, a.M - 1);
+    const int b = m / a.T, tt = m - b * a.T;
+    ap[i] = a.y + b * a.y0 + h * a.y1 + tt * a.y2 + lc * 8;
+  }
+  const bf16_t* bp = a.w + h * a.w1 + int64_t(min(n0 + lr, a.N - 1)) * a.w2 + lc * 8;
+  const int aoff0 = g_sw(lr, lc), aoff1 = g_sw(lr + 128, lc), boff = kGStageA + g_sw(lr, lc);
+  uint4 ra0, ra1, rb;
+  auto gload = [&](int s) {
+    const int k = s * kGK;
+    ra0 = *reinterpret_cast<const uint4*>(ap[0] + k);
+    ra1 = *reinterpret_cast<const uint4*>(ap[1] + k);
+    rb = *reinterpret_cast<const uint4*>(bp + k);
+  };
+  auto lstore = [&](int buf) {
+    uint8_t* base = g_lds + buf * kGStage;
+    *reinterpret_cast<uint4*>(base + aoff0) = ra0;
+    *reinterpret_cast<uint4*>(base + aoff1) = ra1;
+    *reinterpret_cast<uint4*>(base + boff) = rb;
+  };
+
+  // fragments: wave (wm, wn) owns rows 64 wm.., columns 64 wn..; lane row / column fr, k half fh
+  const int wm = w >> 1, wn = w & 1, fr = lane & 31, fh = lane >> 5;
+  int fa[2][2], fb[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      fa[i][j] = g_sw(64 * wm + 32 * i + fr, 2 * j + fh);
+      fb[i][j] = kGStageA + g_sw(64 * wn + 32 * i + fr, 2 * j + fh);
+    }
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][c][r] = 0.f;
+
+  const int nst = a.K / kGK;
+  gload(0);
+  lstore(0);
+  __syncthreads();
+  for (int s = 0; s < nst; ++s) {
+    if (s + 1 < nst) gload(s + 1);
+    const uint8_t* base = g_lds + (s & 1) * kGStage;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      bf16x8 va[2], vb[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        va[i] = *reinterpret_cast<const bf16x8*>(base + fa[i][j]);
+        vb[i] = *reinterpret_cast<const bf16x8*>(base + fb[i][j]);
+      }
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int c = 0; c < 2; ++c) acc[i][c] = mma_bf16(va[i], vb[c], acc[i][c]);
+    }
+    // the other buffer was last read in stage s - 1, which every wave finished
+    // before the barrier that ended it
+    if (s + 1 < nst) lstore((s + 1) & 1);
+    __syncthreads();
+  }
+
+  // epilogue: relu(acc) as bf16 into the LDS output tile, then the gated product
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = 64 * wm + 32 * i + 8 * (r >> 2) + 4 * fh + (r & 3);
+        const int col = 64 * wn + 32 * c + fr;
+        *reinterpret_cast<bf16_t*>(g_lds + row * kGOutRow + col * 2) = f2bf(relu_f(acc[i][c][r]));
+      }
+  __syncthreads();
+#pragma unroll
+  for (int e = 0; e < (kGM * kGN / 8) / 512; ++e) {
+    const int ch = tid + 512 * e;
+    const int row = ch >> 4, cc = ch & 15;
+    const int m = m0 + row, n = n0 + cc * 8;
+    if (m >= a.M || n >= a.N) continue;
+    const int b = m / a.T, tt = m - b * a.T;
+    float fy[8], fx[8], fo[8];
+    load8(reinterpret_cast<const bf16_t*>(g_lds + row * kGOutRow + cc * 16), fy);
+    load8(a.x + b * a.x0 + tt * a.x1 + h * a.x2 + n, fx);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) fo[i] = fx[i] * fy[i];
+    store8(a.o + b * a.o0 + tt * a.o1 + h * a.o2 + n, fo);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Few-row GEMM with split K: out (M, D) = a (M, K) @ b (K, D), bf16 operands,
+// fp32 accumulation, for the decoder product of a decode step (M = batch,
+// K = nh*N = 32768, D = 256), where a library GEMM runs a handful of tiles
+// down the whole K.  Each workgroup takes one 128 x 128 output tile over one
+// K range (the 128-tile MFMA engine), writing fp32 partials [split][M][D];
+// k_small_gemm_reduce sums the splits and casts to out's dtype.
+struct SmallGemmArgs {
+  const bf16_t* a;
+  int64_t as;  // row stride of a
+  const bf16_t* b;
+  int64_t bs;  // row stride of b
+  float* part;
+  int M, K, D, kc;
+  bool avec, bvec;
+};
+
+__global__ __launch_bounds__(kNT) void k_small_gemm(SmallGemmArgs a) {
+  __shared__ Smem<true> sm;
+  const int n0 = blockIdx.x * kTile, split = blockIdx.y, m0 = blockIdx.z * kTile;
+  KRows<bf16_t, true, false, 0> la;
+  la.base = a.a;
+  la.rs = a.as;
+  la.r0 = m0;
+  la.nrows = a.M;
+  la.K = a.K;
+  la.vec = a.avec;
+  NRows<bf16_t, true, false> lb;
+  lb.base = a.b;
+  lb.rs = a.bs;
+  lb.n0 = n0;
+  lb.ncols = a.D;
+  lb.krows = a.K;
+  lb.vec4 = a.bvec;
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+  const int kb = split * a.kc, ke = min(a.K, kb + a.kc);
+  mainloop<true, false>(sm, la, lb, false, kb, ke, acc, true);
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int wm = wave >> 1, wn = wave & 1;
+  float* dst = a.part + int64_t(split) * a.M * a.D;
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        int row, col;
+        acc_coord<false>(wm, wn, lane, i, j, r, row, col);
+        const int gm = m0 + row, gn = n0 + col;
+        if (gm < a.M && gn < a.D) dst[int64_t(gm) * a.D + gn] = acc[i][j][r];
+      }
+}
+
+// 64 outputs per workgroup; four groups of 64 threads each sum every fourth
+// split (coalesced 256-byte rows), then combine through LDS.
+template <typename TO>
+__global__ __launch_bounds__(256) void k_small_gemm_reduce(const float* part, int nsplit, int M, int D,
+                                                           TO* out, int64_t os) {
+  __shared__ float red[4][64];
+  const int l = threadIdx.x & 63, g = threadIdx.x >> 6;
+  const int64_t MD = int64_t(M) * D;
+  const int64_t idx = int64_t(blockIdx.x) * 64 + l;
+  float s = 0.f;
+  if (idx < MD)
+    for (int sp = g; sp < nsplit; sp += 4) s += part[int64_t(sp) * MD + idx];
+  red[g][l] = s;
+  __syncthreads();
+  if (g == 0 && idx < MD) {
+    const int64_t m = idx / D, d = idx - m * D;
+    out[m * os + d] = from_f<TO>(red[0][l] + red[1][l] + red[2][l] + red[3][l]);
+  }
+}
+
+struct SmallGemmPlan {
+  int nsplit, kc;
+  size_t ws_bytes;
+};
+
+inline SmallGemmPlan small_gemm_plan(int64_t M, int64_t K, int64_t D) {
+  SmallGemmPlan p;
+  const int64_t tiles = ((M + kTile - 1) / kTile) * ((D + kTile - 1) / kTile);
+  const int64_t BK = Mode<true>::BK;
+  int64_t S = tiles > 0 ? (256 + tiles - 1) / tiles : 1;
+  S = std::max<int64_t>(1, std::min<int64_t>(S, (K + BK - 1) / BK));
+  int64_t kc = (K + S - 1) / S;
+  kc = std::max<int64_t>(BK, (kc + BK - 1) / BK * BK);
+  p.kc = int(kc);
+  p.nsplit = int((K + kc - 1) / kc);
+  p.ws_bytes = size_t(p.nsplit) * size_t(M) * size_t(D) * sizeof(float);
+  return p;
+}
+
 namespace {
 
 template <typename TX, typename TY>
@@ -137,4 +389,109 @@ extern "C" int bdh_relu_mul(const bdh_tensor4* x, const bdh_tensor4* y, const bd
                     : launch_relu_mul<bf16_t, float>(a, out->dtype, grid, s);
   return yb ? launch_relu_mul<float, bf16_t>(a, out->dtype, grid, s)
             : launch_relu_mul<float, float>(a, out->dtype, grid, s);
+}
+
+// out = x * relu(y @ wt^T) per head; see k_gated_gemm.
+extern "C" int bdh_gated_gemm(const bdh_tensor4* y, const bdh_tensor4* wt, const bdh_tensor4* x,
+                              const bdh_tensor4* out, bdh_stream stream) {
+  BDH_TRY(check_view(y));
+  BDH_TRY(check_view(wt));
+  BDH_TRY(check_view(x));
+  BDH_TRY(check_view(out));
+  const int64_t B = x->size[0], T = x->size[1], H = x->size[2], N = x->size[3], K = y->size[3];
+  if (y->dtype != BDH_BF16 || wt->dtype != BDH_BF16 || x->dtype != BDH_BF16 || out->dtype != BDH_BF16)
+    return BDH_ERR_DTYPE;
+  if (y->size[0] != B || y->size[1] != H || y->size[2] != T) return BDH_ERR_SHAPE;
+  if (wt->size[0] != 1 || wt->size[1] != H || wt->size[2] != N || wt->size[3] != K) return BDH_ERR_SHAPE;
+  for (int i = 0; i < 4; ++i)
+    if (out->size[i] != x->size[i]) return BDH_ERR_SHAPE;
+  if (views_overlap(out, x) || views_overlap(out, y) || views_overlap(out, wt)) return BDH_ERR_ALIAS;
+  if (numel4(out) == 0) return BDH_OK;
+  if (K < kGK || K % kGK != 0 || N % 8 != 0) return BDH_ERR_SHAPE;
+  // 16-byte rows: aligned bases, outer strides multiples of 8 elements
+  auto rows16 = [](const bdh_tensor4* t) {
+    if ((reinterpret_cast<uintptr_t>(t->data) & 15) != 0) return false;
+    for (int i = 0; i < 3; ++i)
+      if (t->size[i] > 1 && t->stride[i] % 8 != 0) return false;
+    return true;
+  };
+  if (!rows16(y) || !rows16(wt) || !rows16(x) || !rows16(out)) return BDH_ERR_STRIDE;
+  const int64_t M = B * T;
+  if (M >= (int64_t(1) << 31) || T >= (int64_t(1) << 31)) return BDH_ERR_SHAPE;
+  GatedArgs a;
+  a.y = static_cast<const bf16_t*>(y->data);
+  a.y0 = y->stride[0];
+  a.y1 = y->stride[1];
+  a.y2 = y->stride[2];
+  a.w = static_cast<const bf16_t*>(wt->data);
+  a.w1 = wt->stride[1];
+  a.w2 = wt->stride[2];
+  a.x = static_cast<const bf16_t*>(x->data);
+  a.x0 = x->stride[0];
+  a.x1 = x->stride[1];
+  a.x2 = x->stride[2];
+  a.o = static_cast<bf16_t*>(out->data);
+  a.o0 = out->stride[0];
+  a.o1 = out->stride[1];
+  a.o2 = out->stride[2];
+  a.T = int(T);
+  a.M = int(M);
+  a.N = int(N);
+  a.K = int(K);
+  a.nmb = int((M + kGM - 1) / kGM);
+  a.nnb = int((N + kGN - 1) / kGN);
+  a.total = int64_t(a.nmb) * a.nnb * H;
+  a.per_xcd = (a.total + 7) / 8;
+  const int64_t grid = 8 * a.per_xcd;
+  if (grid >= (int64_t(1) << 31)) return BDH_ERR_SHAPE;
+  BDH_LAUNCH("k_gated_gemm", k_gated_gemm, dim3(unsigned(grid)), dim3(512), 0, static_cast<hipStream_t>(stream), a);
+  return BDH_OK;
+}
+
+extern "C" size_t bdh_small_gemm_workspace(int64_t M, int64_t K, int64_t D) {
+  if (M <= 0 || K <= 0 || D <= 0) return 0;
+  return small_gemm_plan(M, K, D).ws_bytes;
+}
+
+// out (1, 1, M, D) = a (1, 1, M, K) @ b (1, 1, K, D); see k_small_gemm.
+extern "C" int bdh_small_gemm(const bdh_tensor4* a, const bdh_tensor4* b, const bdh_tensor4* out, void* workspace,
+                              size_t workspace_bytes, bdh_stream stream) {
+  BDH_TRY(check_view(a));
+  BDH_TRY(check_view(b));
+  BDH_TRY(check_view(out));
+  if (a->dtype != BDH_BF16 || b->dtype != BDH_BF16) return BDH_ERR_DTYPE;
+  for (const bdh_tensor4* t : {a, b, out})
+    if (t->size[0] != 1 || t->size[1] != 1) return BDH_ERR_SHAPE;
+  const int64_t M = a->size[2], K = a->size[3], D = b->size[3];
+  if (b->size[2] != K || out->size[2] != M || out->size[3] != D) return BDH_ERR_SHAPE;
+  if (views_overlap(out, a) || views_overlap(out, b)) return BDH_ERR_ALIAS;
+  if (numel4(out) == 0) return BDH_OK;
+  if (M >= (int64_t(1) << 24) || K >= (int64_t(1) << 30) || D >= (int64_t(1) << 24)) return BDH_ERR_SHAPE;
+  if ((M * D + 63) / 64 >= (int64_t(1) << 31)) return BDH_ERR_SHAPE;
+  const SmallGemmPlan p = small_gemm_plan(M, K, D);
+  if (workspace == nullptr || workspace_bytes < p.ws_bytes) return BDH_ERR_WORKSPACE;
+  if ((M + kTile - 1) / kTile > 65535 || p.nsplit > 65535) return BDH_ERR_SHAPE;
+  SmallGemmArgs g;
+  g.a = static_cast<const bf16_t*>(a->data);
+  g.as = a->stride[2];
+  g.b = static_cast<const bf16_t*>(b->data);
+  g.bs = b->stride[2];
+  g.part = static_cast<float*>(workspace);
+  g.M = int(M);
+  g.K = int(K);
+  g.D = int(D);
+  g.kc = p.kc;
+  g.avec = (reinterpret_cast<uintptr_t>(a->data) & 15) == 0 && a->stride[2] % 8 == 0 && K % 8 == 0;
+  g.bvec = (reinterpret_cast<uintptr_t>(b->data) & 7) == 0 && b->stride[2] % 4 == 0 && D % 4 == 0;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const dim3 grid{unsigned((D + kTile - 1) / kTile), unsigned(p.nsplit), unsigned((M + kTile - 1) / kTile)};
+  BDH_LAUNCH("k_small_gemm", k_small_gemm, grid, dim3(kNT), 0, s, g);
+  const unsigned rg = unsigned((M * D + 63) / 64);
+  if (out->dtype == BDH_BF16)
+    BDH_LAUNCH("k_small_gemm_reduce", k_small_gemm_reduce<bf16_t>, dim3(rg), dim3(256), 0, s, g.part, p.nsplit,
+               int(M), int(D), static_cast<bf16_t*>(out->data), out->stride[2]);
+  else
+    BDH_LAUNCH("k_small_gemm_reduce", k_small_gemm_reduce<float>, dim3(rg), dim3(256), 0, s, g.part, p.nsplit,
+               int(M), int(D), static_cast<float*>(out->data), out->stride[2]);
+  return BDH_OK;
 }

@@ -210,7 +210,11 @@ static bool vec8_ok(const bdh_tensor4* t) {
 
 template <typename TV, typename TC, typename TO>
 static int launch_rope(const RopeArgs& a, hipStream_t s) {
-  if (a.vec8 && a.bcast) {
+  // The broadcast kernel has (N / 2048) x T workgroups: at short T (a decode
+  // step: 4 at N = 8192) that leaves the chip idle, so few time steps take the
+  // per-row kernel, whose grid also spans B * H.
+  const int64_t bc_wgs = (a.N + 2047) / 2048 * a.T;
+  if (a.vec8 && a.bcast && bc_wgs >= 512) {
     dim3 grid((unsigned)((a.N + 2047) / 2048), (unsigned)a.T);
     BDH_LAUNCH("k_rope", (k_rope8_bc<TV, TC, TO>), grid, dim3(256), 0, s, a);
     return BDH_OK;

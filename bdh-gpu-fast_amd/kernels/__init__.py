@@ -40,8 +40,10 @@ from .attention_dispatch import (
 from .hip_attn import (
     ext_status,
     has_hip_ext,
+    gated_gemm,
     has_hip_kernel,
     relu_mul,
+    small_gemm,
     tril_decode,
     tril_rope_score_v,
     tril_score_v,
@@ -78,6 +80,8 @@ __all__ = [
     "tril_score_v",
     "tril_score_v_past",
     "relu_mul",
+    "gated_gemm",
+    "small_gemm",
     "tril_rope_score_v",
     "tril_decode",
     "has_hip_ext",

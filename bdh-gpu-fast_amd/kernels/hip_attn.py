@@ -134,6 +134,18 @@ def relu_mul(x: torch.Tensor, y: torch.Tensor, out: Optional[torch.Tensor] = Non
     return ext.relu_mul(_last_dim_unit(x), _last_dim_unit(y), out)
 
 
+def gated_gemm(y: torch.Tensor, wt: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
+    """``x * relu(y @ wt^T)`` per head on the GPU (encoder_v GEMM + gated product, bdh.py:914-945)."""
+    ext = _require(y, wt, x)
+    return ext.gated_gemm(y, wt, x)
+
+
+def small_gemm(a: torch.Tensor, b: torch.Tensor, out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
+    """``a @ b`` for few rows of a on the GPU, split over K (the decoder product of a decode step)."""
+    ext = _require(a, b)
+    return ext.small_gemm(a, b, out_dtype)
+
+
 def tril_rope_score_v(
     x: torch.Tensor,
     v: torch.Tensor,
@@ -230,6 +242,8 @@ __all__ = [
     "tril_score_v",
     "tril_score_v_past",
     "relu_mul",
+    "gated_gemm",
+    "small_gemm",
     "tril_rope_score_v",
     "tril_decode",
     "tril_score_v_bwd",

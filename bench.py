@@ -26,6 +26,7 @@ The JSON line also carries:
     the same model with eager attention.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extra] [--no-models]
+       python bench.py --model c2|c5|c3     (one model leg, HIP path only)
 """
 
 from __future__ import annotations
@@ -136,6 +137,21 @@ def cpu_baseline(reps: int = 3) -> dict:
         times.append(time.perf_counter() - t)
     med = statistics.median(times)
     F = attn_flops(Bs, nh, T, N, D)
+
+    # Model harness counterpart (C2 shape, fp32): the numpy model oracle on one sequence.
+    from oracle import bdh_model_oracle as M
+
+    c = C2
+    Nl = c["mult"] * c["D"] // c["nh"]
+    p = M.init_params(c["n_layer"], c["D"], c["nh"], Nl, 256, seed=0)
+    idx = rng.integers(0, 256, (1, c["T"]))
+    M.bdh_forward(p, idx)  # warmup
+    mt = []
+    for _ in range(reps):
+        t = time.perf_counter()
+        M.bdh_forward(p, idx)
+        mt.append(time.perf_counter() - t)
+    mmed = statistics.median(mt)
     return {
         "value": F / med / 1e12,
         "unit": "TFLOP/s",
@@ -144,6 +160,13 @@ def cpu_baseline(reps: int = 3) -> dict:
         "sample": f"C1 fp32 with B={Bs} of 8 (nh=4 T=512 N=8192 D=256): numpy RoPE + tiled strict-tril "
         f"score x V (oracle/tril_attn_oracle.py), median of {reps} after 1 warmup, {med * 1e3:.0f} ms per call",
         "ms_per_call": med * 1e3,
+        "models": {
+            "c2_prefill": {
+                "tok_s": c["T"] / mmed,
+                "sample": f"C2 model (L=6 D=256 nh=4 N=8192) fp32 forward of B=1 of 32 sequences, T=512 "
+                f"(oracle/bdh_model_oracle.py), median of {reps} after 1 warmup, {mmed * 1e3:.0f} ms per sequence",
+            }
+        },
     }
 
 
@@ -155,6 +178,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--no-extra", action="store_true", help="skip the decode / backward / comparison legs")
     ap.add_argument("--no-models", action="store_true", help="skip the model-harness legs (C2, C3, C5)")
+    ap.add_argument("--model", choices=("c2", "c5", "c3"), default=None,
+                    help="run only this model-harness leg on the HIP path (for profiling) and print its JSON")
     ap.add_argument(
         "--calibrate",
         action="store_true",
@@ -179,6 +204,10 @@ def main() -> int:
     assert torch.cuda.is_available(), "bench.py needs a ROCm GPU"
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+
+    if args.model is not None:
+        print(json.dumps(run_models(torch, ext, dev, only=args.model)), flush=True)
+        return 0
 
     B, nh, T, N, D = (C1[k] for k in ("B", "nh", "T", "N", "D"))
     gq = torch.Generator(device=dev).manual_seed(0)
@@ -242,7 +271,8 @@ def main() -> int:
     if not args.no_cpu:
         log("[bench] cpu baseline (oracle on host cores)...")
         cpu = cpu_baseline()
-        log(f"[bench] cpu baseline: {cpu['value']:.4f} TFLOP/s on {cpu['cores']} threads")
+        log(f"[bench] cpu baseline: {cpu['value']:.4f} TFLOP/s on {cpu['cores']} threads; "
+            f"C2 model {cpu['models']['c2_prefill']['tok_s']:.0f} tok/s")
 
     line = {
         "metric": METRIC,
@@ -341,8 +371,9 @@ def run_extra(torch, ext, kernels, dev, steps, warmup, x, v) -> dict:
     return out
 
 
-def run_models(torch, ext, dev) -> dict:
-    """Model harness legs: prefill tok/s (C2, C5) and generate tok/s (C3)."""
+def run_models(torch, ext, dev, only=None) -> dict:
+    """Model harness legs: prefill tok/s (C2, C5) and generate tok/s (C3).
+    ``only`` ("c2", "c5" or "c3") runs that leg alone, HIP path only."""
     import bdh_harness as H
 
     out: dict = {}
@@ -352,12 +383,15 @@ def run_models(torch, ext, dev) -> dict:
         cfg = H.BDHConfig(n_layer=c["n_layer"], n_embd=c["D"], n_head=c["nh"], mlp_internal_dim_multiplier=c["mult"])
         return H.BDH(cfg).to(dev)
 
+    impls = ("hip",) if only else ("hip", "eager")
     for name, c in (("c2_prefill", C2), ("c5_long_prefill", C5)):
+        if only is not None and not name.startswith(only):
+            continue
         m = build(c)
         g = torch.Generator(device=dev).manual_seed(1)
         idx = torch.randint(0, 256, (c["B"], c["T"]), generator=g, device=dev)
         leg = {"B": c["B"], "T": c["T"], "n_layer": c["n_layer"], "D": c["D"], "nh": c["nh"]}
-        for impl in ("hip", "eager"):
+        for impl in impls:
             log(f"[bench] {name} {impl} ...")
 
             def fwd():
@@ -371,21 +405,24 @@ def run_models(torch, ext, dev) -> dict:
             fwd_hip()
         rec = ext.profile_collect()
         ext.profile_enable(False)
-        leg["hip"]["attention_kernels_ms"] = sum(t for n, t in rec if n != "k_relu_mul")
-        leg["hip"]["relu_mul_ms"] = sum(t for n, t in rec if n == "k_relu_mul")
+        mlp = ("k_gated_gemm", "k_relu_mul")
+        leg["hip"]["attention_kernels_ms"] = sum(t for n, t in rec if n not in mlp)
+        leg["hip"]["gated_product_kernels_ms"] = sum(t for n, t in rec if n in mlp)
         out[name] = leg
         log(f"[bench] {name}: hip {leg['hip']['tok_s']:.0f} tok/s ({leg['hip']['ms']:.2f} ms, attention kernels "
-            f"{leg['hip']['attention_kernels_ms']:.2f} ms, relu_mul {leg['hip']['relu_mul_ms']:.2f} ms), "
-            f"eager {leg['eager']['tok_s']:.0f} tok/s")
+            f"{leg['hip']['attention_kernels_ms']:.2f} ms, gated product {leg['hip']['gated_product_kernels_ms']:.2f} ms)"
+            + (f", eager {leg['eager']['tok_s']:.0f} tok/s" if "eager" in leg else ""))
         del m, idx
         torch.cuda.empty_cache()
 
+    if only is not None and only != "c3":
+        return out
     c = C3_GEN
     m = build(c)
     g = torch.Generator(device=dev).manual_seed(2)
     prompt = torch.randint(0, 256, (c["B"], c["prompt"]), generator=g, device=dev)
     leg = {"B": c["B"], "prompt": c["prompt"], "new_tokens": c["new"], "top_k": c["top_k"], "cache": "bf16"}
-    for impl in ("hip", "eager"):
+    for impl in impls:
         log(f"[bench] c3_generate {impl} ...")
 
         def gen():
@@ -413,8 +450,8 @@ def run_models(torch, ext, dev) -> dict:
             leg[impl]["library_kernels_ms"] = sum(t for _, t in rec)
     out["c3_generate"] = leg
     log(f"[bench] c3_generate: hip {leg['hip']['tok_s']:.0f} tok/s ({leg['hip']['s']:.3f} s; decode attention "
-        f"{leg['hip']['decode_attention_ms']:.1f} ms, {leg['hip']['decode_attention_gbs']:.0f} GB/s), "
-        f"eager {leg['eager']['tok_s']:.0f} tok/s")
+        f"{leg['hip']['decode_attention_ms']:.1f} ms, {leg['hip']['decode_attention_gbs']:.0f} GB/s)"
+        + (f", eager {leg['eager']['tok_s']:.0f} tok/s" if "eager" in leg else ""))
     del m
     torch.cuda.empty_cache()
     return out

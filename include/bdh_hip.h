@@ -206,6 +206,31 @@ int bdh_relu_mul(const bdh_tensor4* x, const bdh_tensor4* y, const bdh_tensor4* 
                  bdh_stream stream);
 
 /*
+ * encoder_v GEMM with the gated product fused into its epilogue, bf16:
+ *   out[b,t,h,n] = x[b,t,h,n] * max(sum_k y[b,h,t,k] * wt[0,h,n,k], 0)
+ * Replaces `_encoder_v_relu` (bdh.py:914-925, einsum("bhtd,hdn->bthn") +
+ * ReLU) followed by the `x_bthn * y_bthn` of _mlp_merge (bdh.py:927-945); the
+ * GEMM's output never reaches HBM.  y: (B, nh, T, K), the LayerNorm of the
+ * attention output; wt: (1, nh, N, K), encoder_v transposed; x, out:
+ * (B, T, nh, N).  K a multiple of 32, N of 8, rows 16-byte aligned.  The
+ * GEMM result is rounded to bf16 after the ReLU, then multiplied by x.
+ */
+int bdh_gated_gemm(const bdh_tensor4* y, const bdh_tensor4* wt, const bdh_tensor4* x,
+                   const bdh_tensor4* out, bdh_stream stream);
+
+/*
+ * Few-row GEMM with split K, bf16 operands, fp32 accumulation:
+ *   out (1, 1, M, D) = a (1, 1, M, K) @ b (1, 1, K, D)
+ * For the decoder product of a decode step (bdh.py:927-945, `_mlp_merge`'s
+ * F.linear with M = batch rows, K = nh*N, D = n_embd), where a library GEMM
+ * walks the whole K with a few tiles.  out is bf16 or fp32.  The workspace
+ * holds the fp32 partial sums of the K splits.
+ */
+size_t bdh_small_gemm_workspace(int64_t M, int64_t K, int64_t D);
+int bdh_small_gemm(const bdh_tensor4* a, const bdh_tensor4* b, const bdh_tensor4* out,
+                   void* workspace, size_t workspace_bytes, bdh_stream stream);
+
+/*
  * Per-kernel timing (measurement support; no counterpart in the reference).
  * While enabled, every kernel the library launches is bracketed by HIP events
  * on its stream.  bdh_profile_collect() waits for the recorded events and

@@ -153,3 +153,38 @@ def test_relu_mul_equals_torch(dx, dy, N):
     assert torch.equal(got.nan_to_num(7.0), want.nan_to_num(7.0))
     with pytest.raises(RuntimeError):
         ext.relu_mul(x, x, out=x)  # out overlaps an input
+
+
+@pytest.mark.parametrize("shape", [(2, 300, 2, 1000, 96), (1, 512, 4, 8192, 256), (3, 257, 3, 136, 64),
+                                   (1, 1, 1, 8, 32)])
+def test_gated_gemm_matches_reference(shape):
+    """x * relu(y @ wt^T) per head against a CPU fp32 reference (the GEMM
+    rounded to bf16 after the ReLU, as the kernel and the unfused GEMM do):
+    ragged row and column tiles, C2 width, one token."""
+    B, T, nh, N, K = shape
+    print(f"gated_gemm {shape}", flush=True)
+    g = torch.Generator().manual_seed(K + N)
+    y = torch.randn(B, nh, T, K, generator=g).to(torch.bfloat16)
+    wt = (0.1 * torch.randn(nh, N, K, generator=g)).to(torch.bfloat16)
+    x = torch.relu(torch.randn(B, T, nh, N, generator=g)).to(torch.bfloat16)
+    got = ext.gated_gemm(y.to(DEV), wt.to(DEV), x.to(DEV))
+    lin = torch.matmul(y.float(), wt.float().transpose(1, 2).contiguous())  # (B, nh, T, N) on the CPU
+    want = (x.float() * torch.relu(lin).to(torch.bfloat16).float().permute(0, 2, 1, 3)).to(torch.bfloat16)
+    assert got.shape == x.shape and got.dtype == torch.bfloat16
+    assert rel_fro(got.float().cpu().numpy(), want.float().numpy()) <= 1e-2
+
+
+@pytest.mark.parametrize("shape,odt", [((64, 32768, 256), torch.bfloat16), ((3, 1000, 200), torch.float32),
+                                       ((300, 640, 130), torch.bfloat16), ((1, 64, 8), torch.float32)])
+def test_small_gemm_matches_reference(shape, odt):
+    """Split-K few-row GEMM against a CPU fp32 product: the decode-step decoder
+    shape, ragged K / D / row tiles, fp32 and bf16 outputs."""
+    M, K, D = shape
+    print(f"small_gemm {shape} {odt}", flush=True)
+    g = torch.Generator().manual_seed(M + K)
+    a = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    b = (0.05 * torch.randn(K, D, generator=g)).to(torch.bfloat16)
+    got = ext.small_gemm(a.to(DEV), b.to(DEV), odt)
+    want = a.float() @ b.float()
+    assert got.shape == (M, D) and got.dtype == odt
+    assert rel_fro(got.float().cpu().numpy(), want.numpy()) <= (1e-5 if odt == torch.float32 else 1e-2)
