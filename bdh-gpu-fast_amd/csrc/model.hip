@@ -88,18 +88,19 @@ __global__ __launch_bounds__(256) void k_relu_mul(ReluMulArgs a) {
 // goes to HBM: the kernel reads x once and writes out once.
 //
 // Tiles of 256 rows (tokens) x 128 columns of one head, 8 waves of 64 x 64
-// (2 x 2 MFMA 32x32x16 blocks), K in stages of 32 double-buffered in LDS
-// (16-byte chunk c of row r at c ^ ((r >> 2) & 3), conflict-free fragment
-// reads).  Two workgroups per CU, so one tile's epilogue overlaps another's
-// main loop.  Tiles are taken in groups of 8 row blocks per column block
-// (A and B blocks of a group stay in L2), each XCD a contiguous range.
+// (2 x 2 MFMA 32x32x16 blocks), K in stages of 32 through a ring of three LDS
+// buffers, the global loads issued two stages ahead (16-byte chunk c of row r
+// at c ^ ((r >> 2) & 3), conflict-free fragment reads).  Two workgroups per
+// CU, so one tile's epilogue overlaps another's main loop.  Tiles run column
+// blocks fastest (the tiles in flight on an XCD share their A block and cover
+// whole rows of one head), each XCD a contiguous range.
 // Epilogue: relu(acc) rounded to bf16 (the value the unfused GEMM would
 // store) goes to LDS, then 16-byte coalesced reads of x and stores of out.
 constexpr int kGM = 256, kGN = 128, kGK = 32;
 constexpr int kGStageA = kGM * 64, kGStageB = kGN * 64, kGStage = kGStageA + kGStageB;  // 24 KB
 constexpr int kGOutRow = kGN * 2 + 16;  // padded LDS row of the output tile (bytes)
-constexpr int kGLds = kGM * kGOutRow > 2 * kGStage ? kGM * kGOutRow : 2 * kGStage;
-constexpr int kGGroup = 8;
+constexpr int kGRing = 3;
+constexpr int kGLds = kGM * kGOutRow > kGRing * kGStage ? kGM * kGOutRow : kGRing * kGStage;
 
 struct GatedArgs {
   const bf16_t* y;
@@ -125,14 +126,11 @@ __global__ __launch_bounds__(512, 2) void k_gated_gemm(const GatedArgs a) {
   if (kk >= a.per_xcd) return;
   const int64_t t = int64_t(xcd) * a.per_xcd + kk;
   if (t >= a.total) return;
-  // tile -> (head, row block, column block): groups of kGGroup row blocks, rows fastest
+  // tile -> (head, row block, column block), column blocks fastest
   const int64_t per_head = int64_t(a.nmb) * a.nnb;
   const int h = int(t / per_head);
   const int g = int(t - int64_t(h) * per_head);
-  const int gm = g / (kGGroup * a.nnb);
-  const int gsz = min(kGGroup, a.nmb - gm * kGGroup);
-  const int q = g - gm * kGGroup * a.nnb;
-  const int mbi = gm * kGGroup + q % gsz, nbi = q / gsz;
+  const int mbi = g / a.nnb, nbi = g - mbi * a.nnb;
   const int m0 = mbi * kGM, n0 = nbi * kGN;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
 
@@ -147,19 +145,29 @@ __global__ __launch_bounds__(512, 2) void k_gated_gemm(const GatedArgs a) {
   }
   const bf16_t* bp = a.w + h * a.w1 + int64_t(min(n0 + lr, a.N - 1)) * a.w2 + lc * 8;
   const int aoff0 = g_sw(lr, lc), aoff1 = g_sw(lr + 128, lc), boff = kGStageA + g_sw(lr, lc);
-  uint4 ra0, ra1, rb;
-  auto gload = [&](int s) {
+  // two stages in flight in named registers (slot 0: q0*, slot 1: q1*), so none
+  // of them is addressed through memory
+  uint4 q0a, q0b, q0c, q1a, q1b, q1c;
+  auto gload = [&](int s, auto slotc) __attribute__((always_inline)) {
     const int k = s * kGK;
-    ra0 = *reinterpret_cast<const uint4*>(ap[0] + k);
-    ra1 = *reinterpret_cast<const uint4*>(ap[1] + k);
-    rb = *reinterpret_cast<const uint4*>(bp + k);
+    const uint4 va = *reinterpret_cast<const uint4*>(ap[0] + k);
+    const uint4 vb = *reinterpret_cast<const uint4*>(ap[1] + k);
+    const uint4 vc = *reinterpret_cast<const uint4*>(bp + k);
+    if constexpr (decltype(slotc)::value == 0) {
+      q0a = va; q0b = vb; q0c = vc;
+    } else {
+      q1a = va; q1b = vb; q1c = vc;
+    }
   };
-  auto lstore = [&](int buf) {
+  auto lstore = [&](int buf, auto slotc) __attribute__((always_inline)) {
     uint8_t* base = g_lds + buf * kGStage;
-    *reinterpret_cast<uint4*>(base + aoff0) = ra0;
-    *reinterpret_cast<uint4*>(base + aoff1) = ra1;
-    *reinterpret_cast<uint4*>(base + boff) = rb;
+    constexpr bool z = decltype(slotc)::value == 0;
+    *reinterpret_cast<uint4*>(base + aoff0) = z ? q0a : q1a;
+    *reinterpret_cast<uint4*>(base + aoff1) = z ? q0b : q1b;
+    *reinterpret_cast<uint4*>(base + boff) = z ? q0c : q1c;
   };
+  using S0 = std::integral_constant<int, 0>;
+  using S1 = std::integral_constant<int, 1>;
 
   // fragments: wave (wm, wn) owns rows 64 wm.., columns 64 wn..; lane row / column fr, k half fh
   const int wm = w >> 1, wn = w & 1, fr = lane & 31, fh = lane >> 5;
@@ -180,12 +188,17 @@ __global__ __launch_bounds__(512, 2) void k_gated_gemm(const GatedArgs a) {
       for (int r = 0; r < 16; ++r) acc[i][c][r] = 0.f;
 
   const int nst = a.K / kGK;
-  gload(0);
-  lstore(0);
+  gload(0, S0());
+  if (nst > 1) gload(1, S1());
+  lstore(0, S0());
   __syncthreads();
-  for (int s = 0; s < nst; ++s) {
-    if (s + 1 < nst) gload(s + 1);
-    const uint8_t* base = g_lds + (s & 1) * kGStage;
+  int buf = 0;
+  // stage s keeps its registers in slot s & 1; the loop is unrolled by two so
+  // the slots are compile-time register indices
+  auto stage = [&](int s, auto slotc) __attribute__((always_inline)) {
+    constexpr int SL = decltype(slotc)::value;
+    if (s + 2 < nst) gload(s + 2, slotc);
+    const uint8_t* base = g_lds + buf * kGStage;
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       bf16x8 va[2], vb[2];
@@ -199,10 +212,16 @@ __global__ __launch_bounds__(512, 2) void k_gated_gemm(const GatedArgs a) {
 #pragma unroll
         for (int c = 0; c < 2; ++c) acc[i][c] = mma_bf16(va[i], vb[c], acc[i][c]);
     }
-    // the other buffer was last read in stage s - 1, which every wave finished
-    // before the barrier that ended it
-    if (s + 1 < nst) lstore((s + 1) & 1);
+    // the next ring buffer was last read in stage s - 2, which every wave
+    // finished before the barrier that ended it
+    const int nbuf = buf == kGRing - 1 ? 0 : buf + 1;
+    if (s + 1 < nst) lstore(nbuf, std::integral_constant<int, SL ^ 1>());
     __syncthreads();
+    buf = nbuf;
+  };
+  for (int s = 0; s < nst; s += 2) {
+    stage(s, S0());
+    if (s + 1 < nst) stage(s + 1, S1());
   }
 
   // epilogue: relu(acc) as bf16 into the LDS output tile, then the gated product
