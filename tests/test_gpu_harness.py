@@ -67,6 +67,19 @@ def test_forward_bf16_c2_width_matches_oracle():
     assert rel_fro(got.float().cpu().numpy(), M.bdh_forward(p, idx)) <= 2e-2
 
 
+def test_forward_full_c2_config_matches_oracle():
+    """The C2 model configuration in full (6 layers, D=256, nh=4, N=8192, T=512)
+    on two sequences, bf16 autocast, against the numpy model oracle (fp32):
+    logits within 2e-2."""
+    print("harness C2 config forward", flush=True)
+    p = M.init_params(6, 256, 4, 8192, 256, seed=31)
+    m = _model(p, mult=128)
+    idx = np.random.default_rng(32).integers(0, 256, (2, 512))
+    with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+        got, _ = m(torch.from_numpy(idx).to(DEV), impl="hip")
+    assert rel_fro(got.float().cpu().numpy(), M.bdh_forward(p, idx)) <= 2e-2
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_cached_paths_match_uncached_forward(dtype):
     print(f"harness cached paths {dtype}", flush=True)

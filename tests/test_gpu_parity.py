@@ -152,6 +152,26 @@ def test_decode_matches_oracle_on_capacity_strided_cache(S, Tq, N, D, Hv, qdt, c
         assert not got.any()
 
 
+def test_decode_full_c3_size_properties():
+    """C3 at full size (B=64 nh=4 N=8192 D=256, bf16 cache of capacity 512, S=511):
+    the decode of the query at position S over the cache equals row S of the cold
+    op over the same S+1 rows (the definition of a decode step), within bf16
+    tolerance; doubling V doubles the output exactly; batch element 0 against
+    the oracle."""
+    B, H, N, D, S, cap = 64, 4, 8192, 256, 511, 512
+    g = torch.Generator(device=DEV).manual_seed(3)
+    kc = torch.relu(0.32 * torch.randn(B, H, cap, N, generator=g, device=DEV)).to(torch.bfloat16)
+    vc = torch.randn(B, 1, cap, D, generator=g, device=DEV).to(torch.bfloat16)
+    q = kc[:, :, S:S + 1]
+    got = ext.tril_decode(q, kc.narrow(2, 0, S), vc.narrow(2, 0, S))
+    cold_row = ext.tril_score_v_past(q, kc, vc, S)  # queries at offset S over the S+1 rows
+    assert rel_fro(np_of(got), np_of(cold_row)) <= TOL[torch.bfloat16]
+    got2 = ext.tril_decode(q, kc.narrow(2, 0, S), (vc * 2).narrow(2, 0, S))
+    assert torch.equal(got2, got * 2)
+    want = O.tril_decode_cpu(np_of(q[:1]), np_of(kc[:1, :, :S]), np_of(vc[:1, :, :S]))
+    assert rel_fro(np_of(got[:1]), want) <= TOL[torch.bfloat16]
+
+
 # -------------------------------------------------------------------- RoPE
 @pytest.mark.parametrize("vdt,odt", [(torch.float32, torch.float32), (torch.bfloat16, torch.bfloat16),
                                      (torch.bfloat16, torch.float32), (torch.float32, torch.bfloat16)])
