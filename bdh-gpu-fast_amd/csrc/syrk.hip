@@ -1398,9 +1398,12 @@ namespace {
 
 // past > 0 (no RoPE): out holds rows past.. only, and the score tiles of the
 // row tiles below past / 256 are neither computed nor stored.
+// ext_table (relative RoPE only): a table built by sy_build_rel_table with
+// ext_rows >= 128 * (tiles of T) rows, used instead of building one in ws
+// (ws then needs only the partial tiles).
 int sy_run(const bdh_tensor4* q, const bdh_tensor4* k, const bdh_tensor4* v, const bdh_tensor4* out,
            const float* freqs, int64_t rope_start, const bdh_tensor4* qr, int64_t past, void* ws,
-           size_t ws_bytes, hipStream_t s) {
+           size_t ws_bytes, hipStream_t s, const void* ext_table = nullptr, int64_t ext_rows = 0) {
   const int64_t B = q->size[0], H = q->size[1], T = q->size[2], N = q->size[3];
   const bool rope = freqs != nullptr;
   SyPlan p;
@@ -1410,17 +1413,22 @@ int sy_run(const bdh_tensor4* q, const bdh_tensor4* k, const bdh_tensor4* v, con
   const int64_t nslab = B * H;
   const int64_t Dv = v->size[3];
   const int64_t grid_scores = 8 * ((nslab + 7) / 8) * p.ips;
-  if (ws == nullptr || ws_bytes < p.ws_bytes) return BDH_ERR_WORKSPACE;
-
-  uint8_t* wsb = static_cast<uint8_t*>(ws);
-  uint32_t* table = rope ? reinterpret_cast<uint32_t*>(wsb) : nullptr;
-  bf16_t* part = reinterpret_cast<bf16_t*>(wsb + p.table_bytes);
   // Without the RoPE(x) copy the scores use the relative table (rows rotated
   // about their tile's centre); the copy needs absolute positions.
   const bool want_qr = qr != nullptr && numel4(qr) > 0;
   const bool rel = rope && !want_qr;
-  const int tq = rel ? 128 * p.nt : int(T);
-  if (rope) {
+  if (rel && ext_table != nullptr && ext_rows < int64_t(128) * p.nt) return BDH_ERR_ARG;
+  // (a table whose byte offsets pass 2^31 is not used: the kernel's offsets
+  // are 32-bit; the one built in ws for this T fits)
+  const bool given = rel && ext_table != nullptr && ext_rows * N * 2 < (int64_t(1) << 31);
+  if (ws == nullptr || ws_bytes < (given ? p.part_bytes : p.ws_bytes)) return BDH_ERR_WORKSPACE;
+
+  uint8_t* wsb = static_cast<uint8_t*>(ws);
+  uint32_t* table = given ? static_cast<uint32_t*>(const_cast<void*>(ext_table))
+                          : (rope ? reinterpret_cast<uint32_t*>(wsb) : nullptr);
+  bf16_t* part = reinterpret_cast<bf16_t*>(given ? wsb : wsb + p.table_bytes);
+  const int tq = given ? int(ext_rows) : (rel ? 128 * p.nt : int(T));
+  if (rope && !given) {
     BDH_LAUNCH("k_rope_table", k_rope_table, dim3(unsigned((N / 2 + 255) / 256), unsigned(tq)), dim3(256), 0, s,
                freqs, rope_start, int(N / 2), tq, rel, table);
   }
@@ -1505,6 +1513,27 @@ int sy_cold(const bdh_tensor4* q, const bdh_tensor4* k, const bdh_tensor4* v, co
             const float* freqs, int64_t rope_start, const bdh_tensor4* qr, void* ws, size_t ws_bytes,
             hipStream_t s) {
   return sy_run(q, k, v, out, freqs, rope_start, qr, 0, ws, ws_bytes, s);
+}
+
+size_t sy_rel_table_bytes(int64_t T, int64_t N) {
+  if (T <= 0 || N <= 0 || N % 64 != 0) return 0;
+  return align_up(size_t(128 * ((T + kSyTile - 1) / kSyTile)) * size_t(N / 2) * 4, 256);
+}
+
+int sy_build_rel_table(const float* freqs, int64_t N, int64_t T, void* table, size_t bytes, hipStream_t s) {
+  const size_t need = sy_rel_table_bytes(T, N);
+  if (need == 0) return BDH_ERR_SHAPE;
+  if (freqs == nullptr || table == nullptr || bytes < need) return BDH_ERR_ARG;
+  const int rows = int(128 * ((T + kSyTile - 1) / kSyTile));
+  if (rows > 65535) return BDH_ERR_SHAPE;
+  BDH_LAUNCH("k_rope_table", k_rope_table, dim3(unsigned((N / 2 + 255) / 256), unsigned(rows)), dim3(256), 0, s,
+             freqs, int64_t(0), int(N / 2), rows, true, static_cast<uint32_t*>(table));
+  return BDH_OK;
+}
+
+int sy_cold_tab(const bdh_tensor4* x, const bdh_tensor4* v, const bdh_tensor4* out, const float* freqs,
+                int64_t rope_start, const void* table, int64_t rows, void* ws, size_t ws_bytes, hipStream_t s) {
+  return sy_run(x, x, v, out, freqs, rope_start, nullptr, 0, ws, ws_bytes, s, table, rows);
 }
 
 size_t sy_past_workspace(int64_t B, int64_t H, int64_t Tk, int64_t past, int64_t N, int64_t Dv) {

@@ -65,10 +65,27 @@ def attn_flops(B, nh, T, N, D) -> float:
     return float(B * nh * (N + D) * T * (T - 1))
 
 
-def time_steps(fn, steps: int, warmup: int) -> float:
-    """ms per step over exactly ``steps`` calls, synchronised on both sides."""
+def settle(fn, seconds: float = 0.2) -> None:
+    """Run the step untimed for ``seconds``: the first ~100 steps of a cold
+    process run up to 10% slower (clocks and queues settling), which a short
+    warmup would leave in the timed region."""
+    import time
     import torch
 
+    t_end = time.perf_counter() + seconds
+    while time.perf_counter() < t_end:
+        for _ in range(4):
+            fn()
+        torch.cuda.synchronize()
+
+
+def time_steps(fn, steps: int, warmup: int, settle_s: float = 0.2) -> float:
+    """ms per step over exactly ``steps`` calls, synchronised on both sides,
+    after ``settle`` for ``settle_s`` seconds and ``warmup`` untimed calls."""
+    import torch
+
+    if settle_s > 0:
+        settle(fn, settle_s)
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
@@ -173,8 +190,8 @@ def cpu_baseline(reps: int = 3) -> dict:
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--no-extra", action="store_true", help="skip the decode / backward / comparison legs")
     ap.add_argument("--no-models", action="store_true", help="skip the model-harness legs (C2, C3, C5)")
@@ -231,8 +248,9 @@ def main() -> int:
         log(f"[bench] calibration multiply: {CALIB_BYTES} bytes read, {CALIB_BYTES} bytes written")
         del src, dst
 
+    settle(step)
     launches0 = ext.launch_count()
-    ms = time_steps(step, args.steps, args.warmup)
+    ms = time_steps(step, args.steps, args.warmup, settle_s=0)
     assert ext.launch_count() - launches0 == args.steps + args.warmup, "HIP library calls missing"
     F = attn_flops(B, nh, T, N, D)
     value = F / (ms * 1e-3) / 1e12
