@@ -1113,7 +1113,13 @@ __global__ __launch_bounds__(512, 1) void k_sy_sv(const SvArgs a) {
   uint8_t* const vblk = sv_lds + 64 * 128;   // 64 x 512 bytes
   float* const red = reinterpret_cast<float*>(sv_lds);
   constexpr int VL = sizeof(TV) == 2 ? 1 : 2;  // 16-byte loads per 8 V elements
-  const int rb = int(blockIdx.x) + a.rb0, slab = blockIdx.y;
+  // Row blocks have 1..nrb key chunks and workgroups go to the XCDs round
+  // robin by linear id, so the block index is rotated by the slab: with the
+  // plain order an XCD would get one block length only (C1: one XCD every
+  // 8-chunk block, another every 1-chunk block), and the longest ones would
+  // share one XCD's bandwidth.
+  const int slab = blockIdx.y;
+  const int rb = int((blockIdx.x + blockIdx.y) % gridDim.x) + a.rb0;
   const int b = slab / a.H, h = slab - b * a.H, hv = a.Hv == 1 ? 0 : h;
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   const int r0 = rb * 64;
@@ -1135,10 +1141,12 @@ __global__ __launch_bounds__(512, 1) void k_sy_sv(const SvArgs a) {
   // columns are not stored).
   const int vcc = min(vc, a.D / 8 - 1);
 
-  constexpr int PF = 2;
+  // chunks in flight: three while a chunk's loads take at most 8 registers
+  // of 16 bytes per thread, else two
+  constexpr int PF = NS + 4 * VL <= 8 ? 3 : 2;
   uint4 pr[PF][NS];    // partial rows of the chunks in flight
   uint4 vr[PF][4][VL];  // V rows of the chunks in flight
-  auto load_chunk = [&](int ck, auto slotc) {
+  auto load_chunk = [&](int ck, auto slotc) __attribute__((always_inline)) {
     constexpr int k = decltype(slotc)::value;
     const int j0 = ck * 64;
     const int tile = ti * (ti + 1) / 2 + (j0 >> 8) - a.t0;
@@ -1154,7 +1162,7 @@ __global__ __launch_bounds__(512, 1) void k_sy_sv(const SvArgs a) {
     }
   };
   // split sum, mask (j < i, j < T), one rounding; then the V block as bf16
-  auto store_chunk = [&](int ck, auto slotc) {
+  auto store_chunk = [&](int ck, auto slotc) __attribute__((always_inline)) {
     constexpr int k = decltype(slotc)::value;
     const int j0 = ck * 64 + lk;
     float sacc[8];
@@ -1220,15 +1228,21 @@ __global__ __launch_bounds__(512, 1) void k_sy_sv(const SvArgs a) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][c][r] = 0.f;
 
+  // Every processed chunk issues the same loads (chunks past the last re-read
+  // the last one, an L2 hit), and the first PF chunks issue in slot order (no
+  // scheduling across the barriers), so the compiler's wait before a chunk's
+  // store leaves the PF - 1 chunks behind it in flight; a conditional load, or
+  // slots interleaved at the start, make it wait for all of them.
   sy_static_for<PF>([&](auto kc) {
-    if (int(decltype(kc)::value) < nch) load_chunk(int(decltype(kc)::value), kc);
+    load_chunk(min(int(decltype(kc)::value), nch - 1), kc);
+    __builtin_amdgcn_sched_barrier(0);
   });
-  for (int c0 = 0; c0 < nch; c0 += PF) sy_static_for<PF>([&](auto kc) {
-    const int ck = c0 + int(decltype(kc)::value);
-    if (ck >= nch) return;
+  // chunk ck from slot kc: staged into the blocks, then the slot refilled with
+  // chunk ck + PF, then the MFMAs
+  auto do_chunk = [&](int ck, auto kc) __attribute__((always_inline)) {
     __syncthreads();  // the previous chunk's fragment reads are done
     store_chunk(ck, kc);
-    if (ck + PF < nch) load_chunk(ck + PF, kc);
+    load_chunk(min(ck + PF, nch - 1), kc);
     __syncthreads();
 #pragma unroll
     for (int k2 = 0; k2 < 2; ++k2) {
@@ -1250,6 +1264,15 @@ __global__ __launch_bounds__(512, 1) void k_sy_sv(const SvArgs a) {
 #pragma unroll
         for (int c = 0; c < 2; ++c) acc[i][c] = mma(fa[i], fb[c], acc[i][c]);
     }
+  };
+  // Full groups of PF chunks in the loop, the rest after it: a chunk skipped
+  // inside the loop would reach the back edge with fewer loads issued, and
+  // the compiler's waits would then drain every slot.
+  int c0 = 0;
+  for (; c0 + PF <= nch; c0 += PF)
+    sy_static_for<PF>([&](auto kc) { do_chunk(c0 + int(decltype(kc)::value), kc); });
+  sy_static_for<PF>([&](auto kc) {
+    if (c0 + int(decltype(kc)::value) < nch) do_chunk(c0 + int(decltype(kc)::value), kc);
   });
   // add the second key half's sums (waves 4-7) into the first's (waves 0-3)
   __syncthreads();  // the blocks' last fragment reads are done
