@@ -61,9 +61,6 @@ EXPORTED_SYMBOLS = (
     "bdh_tril_score_v_past_workspace",
     "bdh_tril_score_v_past",
     "bdh_tril_rope_score_v",
-    "bdh_rope_rel_table_bytes",
-    "bdh_rope_rel_table",
-    "bdh_tril_rope_score_v_tab",
     "bdh_tril_decode_workspace",
     "bdh_tril_decode",
     "bdh_rope_rotate",
@@ -122,9 +119,6 @@ def _load():
         "bdh_tril_score_v_past_workspace": (sz, [i64, i64, i64, i64, i64, i64, i32]),
         "bdh_tril_score_v_past": (ctypes.c_int, [P, P, P, P, i64, vp, sz, vp]),
         "bdh_tril_rope_score_v": (ctypes.c_int, [P, P, P, fp, i64, P, vp, sz, vp]),
-        "bdh_rope_rel_table_bytes": (sz, [i64, i64]),
-        "bdh_rope_rel_table": (ctypes.c_int, [fp, i64, i64, vp, sz, vp]),
-        "bdh_tril_rope_score_v_tab": (ctypes.c_int, [P, P, P, fp, i64, vp, sz, i64, vp, sz, vp]),
         "bdh_tril_decode_workspace": (sz, [i64, i64, i64, i64, i64, i64]),
         "bdh_tril_decode": (ctypes.c_int, [P, P, P, P, vp, sz, vp]),
         "bdh_rope_rotate": (ctypes.c_int, [P, P, P, P, i32, vp]),
@@ -209,12 +203,11 @@ def _stream(dev: torch.device) -> ctypes.c_void_p:
     return ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
 
 
-def _check(rc: int, what: str, count: bool = True) -> None:
+def _check(rc: int, what: str) -> None:
     global _launches
     if rc != 0:
         raise RuntimeError(f"bdh_hip_ext.{what} failed: {_lib.bdh_error_string(rc).decode()} (code {rc})")
-    if count:
-        _launches += 1
+    _launches += 1
 
 
 def _workspace(nbytes: int, dev: torch.device) -> Tuple[Optional[torch.Tensor], int]:
@@ -301,43 +294,6 @@ def tril_score_v_save(x: torch.Tensor, v: torch.Tensor) -> Tuple[torch.Tensor, O
     return out, (ws if keeps_scores(x, v) else None)
 
 
-# Relative RoPE tables of the fused forward, one per (device, freqs buffer,
-# N): (freqs view held alive, its version, rows T covered, table, stream it
-# was built on, event after the build).  The table depends only on the
-# frequencies and the sequence's tile count, so it is built once, like the
-# reference's cos/sin cache (rope_dispatch.py), and rebuilt when the freqs
-# buffer is written in place (its version changes) or a longer sequence comes.
-_rel_tables: "dict[tuple, tuple]" = {}
-_REL_TABLES_MAX = 8
-
-
-def _rel_table(f: torch.Tensor, fptr, N: int, T: int, dev: torch.device):
-    """(table tensor, rows T it covers) for contiguous fp32 freqs ``f``; builds
-    on the current stream, and orders another stream's use after the build."""
-    key = (dev.index, f.data_ptr(), N)
-    cur = torch.cuda.current_stream(dev)
-    hit = _rel_tables.get(key)
-    if hit is not None and hit[1] == f._version and hit[2] >= T:
-        _, _, cap, table, stream, ev = hit
-        if stream != cur:
-            cur.wait_event(ev)
-            table.record_stream(cur)
-        return table, cap
-    cap = max(256, -(-T // 256) * 256, hit[2] if hit is not None else 0)
-    nbytes = int(_lib.bdh_rope_rel_table_bytes(cap, N))
-    if nbytes == 0:
-        return None, 0
-    table = torch.empty(nbytes, dtype=torch.uint8, device=dev)
-    _check(_lib.bdh_rope_rel_table(fptr, N, cap, table.data_ptr(), nbytes, _stream(dev)), "rope_rel_table",
-           count=False)
-    ev = torch.cuda.Event()
-    ev.record(cur)
-    if hit is None and len(_rel_tables) >= _REL_TABLES_MAX:
-        _rel_tables.pop(next(iter(_rel_tables)))
-    _rel_tables[key] = (f, f._version, cap, table, cur, ev)
-    return table, cap
-
-
 def tril_rope_score_v(
     x: torch.Tensor,
     v: torch.Tensor,
@@ -345,15 +301,12 @@ def tril_rope_score_v(
     rope_start: int = 0,
     qr_out: Optional[torch.Tensor] = None,
     out: Optional[torch.Tensor] = None,
-    rel_table_cache: bool = True,
 ) -> torch.Tensor:
     """Cold BDH attention with RoPE fused into the loads: ``tril(R(x) R(x)^T, -1) v``.
 
     ``freqs`` is the (N,) or (1,1,1,N) fp32 frequency buffer (pairs share a
     value); positions are ``rope_start + t``.  ``qr_out`` optionally receives
-    ``R(x)`` (e.g. the KR cache slot).  Without ``qr_out``, a bf16 call with
-    contiguous ``freqs`` uses the cached relative table (built on first use;
-    ``rel_table_cache=False`` builds it in the workspace on every call).
+    ``R(x)`` (e.g. the KR cache slot).
     """
     dev = _require_device(x, v, qr_out, out)
     B, H, T, N = x.shape
@@ -363,21 +316,11 @@ def tril_rope_score_v(
     with torch.cuda.device(dev):
         need = _lib.bdh_tril_score_v_workspace(B, H, T, N, v.size(-1), _dtype_code(x))
         ws, nb = _workspace(need, dev)
-        table = None
-        if rel_table_cache and qr_out is None and x.dtype == torch.bfloat16 and freqs.is_contiguous() and T > 0:
-            table, cap = _rel_table(f, fptr, N, T, dev)
-        if table is not None:
-            rc = _lib.bdh_tril_rope_score_v_tab(
-                ctypes.byref(_t4(x)), ctypes.byref(_t4(v)), ctypes.byref(_t4(out)), fptr, int(rope_start),
-                table.data_ptr(), table.numel(), cap,
-                ws.data_ptr() if ws is not None else None, nb, _stream(dev),
-            )
-        else:
-            rc = _lib.bdh_tril_rope_score_v(
-                ctypes.byref(_t4(x)), ctypes.byref(_t4(v)), ctypes.byref(_t4(out)), fptr, int(rope_start),
-                ctypes.byref(_t4(qr_out)) if qr_out is not None else None,
-                ws.data_ptr() if ws is not None else None, nb, _stream(dev),
-            )
+        rc = _lib.bdh_tril_rope_score_v(
+            ctypes.byref(_t4(x)), ctypes.byref(_t4(v)), ctypes.byref(_t4(out)), fptr, int(rope_start),
+            ctypes.byref(_t4(qr_out)) if qr_out is not None else None,
+            ws.data_ptr() if ws is not None else None, nb, _stream(dev),
+        )
     _check(rc, "tril_rope_score_v")
     return out
 

@@ -58,13 +58,6 @@ size_t sy_workspace(int64_t B, int64_t H, int64_t T, int64_t N, int64_t Dv, bool
 int sy_cold(const bdh_tensor4* q, const bdh_tensor4* k, const bdh_tensor4* v, const bdh_tensor4* out,
             const float* freqs, int64_t rope_start, const bdh_tensor4* qr, void* ws, size_t ws_bytes,
             hipStream_t s);
-// Relative RoPE table of the fused forward, built once for sequences of up to
-// T rows (it depends only on freqs and the tile count), then passed to
-// sy_cold_tab instead of being rebuilt in the workspace.
-size_t sy_rel_table_bytes(int64_t T, int64_t N);
-int sy_build_rel_table(const float* freqs, int64_t N, int64_t T, void* table, size_t bytes, hipStream_t s);
-int sy_cold_tab(const bdh_tensor4* x, const bdh_tensor4* v, const bdh_tensor4* out, const float* freqs,
-                int64_t rope_start, const void* table, int64_t rows, void* ws, size_t ws_bytes, hipStream_t s);
 // Queries at an offset on the same path, when q is rows past.. of k (same
 // storage and strides, bf16): only the row tiles that hold new rows.
 size_t sy_past_workspace(int64_t B, int64_t H, int64_t Tk, int64_t past, int64_t N, int64_t Dv);

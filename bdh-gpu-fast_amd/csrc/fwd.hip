@@ -403,33 +403,6 @@ extern "C" int bdh_tril_score_v(const bdh_tensor4* q, const bdh_tensor4* k, cons
                   static_cast<hipStream_t>(stream));
 }
 
-extern "C" size_t bdh_rope_rel_table_bytes(int64_t T, int64_t N) { return sy_rel_table_bytes(T, N); }
-
-extern "C" int bdh_rope_rel_table(const float* freqs, int64_t N, int64_t T, void* table, size_t table_bytes,
-                                  bdh_stream stream) {
-  return sy_build_rel_table(freqs, N, T, table, table_bytes, static_cast<hipStream_t>(stream));
-}
-
-extern "C" int bdh_tril_rope_score_v_tab(const bdh_tensor4* x, const bdh_tensor4* v, const bdh_tensor4* out,
-                                         const float* freqs, int64_t rope_start, const void* table,
-                                         size_t table_bytes, int64_t table_T, void* workspace,
-                                         size_t workspace_bytes, bdh_stream stream) {
-  BDH_TRY(check_cold(x, x, v, out));
-  if (freqs == nullptr && x->size[3] > 0) return BDH_ERR_ARG;
-  if (x->size[3] % 2 != 0) return BDH_ERR_SHAPE;
-  if (rope_start < 0 || rope_start + x->size[2] > (int64_t(1) << 24)) return BDH_ERR_ARG;
-  if (table == nullptr || table_T < x->size[2] || table_bytes < sy_rel_table_bytes(table_T, x->size[3]))
-    return BDH_ERR_ARG;
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  if (numel4(out) == 0) return BDH_OK;
-  if (x->dtype == BDH_BF16 && x->size[2] > 0) {
-    const int64_t rows = 128 * ((table_T + 255) / 256);
-    const int rc = sy_cold_tab(x, v, out, freqs, rope_start, table, rows, workspace, workspace_bytes, s);
-    if (rc != kNotEligible) return rc;
-  }
-  return run_cold(x, x, v, out, freqs, rope_start, nullptr, workspace, workspace_bytes, s);
-}
-
 extern "C" int bdh_tril_rope_score_v(const bdh_tensor4* x, const bdh_tensor4* v,
                                      const bdh_tensor4* out, const float* freqs,
                                      int64_t rope_start, const bdh_tensor4* qr_out,

@@ -2,9 +2,12 @@
 //
 //   out[b,h,i,:] = sum_{j<i} <R_i, R_j> V_j,   R = RoPE(x) (or R = q, k given)
 //
-// Forward, three kernels per call:
-//  1. k_rope_table  (RoPE only): (cos, sin) of every (row, pair) as two bf16
-//     halves of one dword, stage-major.  The same table serves every (b,h).
+// Forward, two kernels per call (three with an absolute-position table):
+//  1. k_rope_table (RoPE with the RoPE(x) copy): (cos, sin) of every (row,
+//     pair) as two bf16 halves of one dword, stage-major.  The same table
+//     serves every (b,h).  Without the copy the score kernel rotates rows
+//     about their tile's centre and makes the same dwords itself from the
+//     frequencies, which it keeps in LDS.
 //  2. k_sy_scores: partial score tiles S = R R^T.
 //     * 256x256 output tiles over the lower triangle of each (b,h) slab; with
 //       Q = K the diagonal tiles go in pairs, each computing its 36 lower
@@ -14,8 +17,8 @@
 //       (workgroup id % 8 selects the XCD), so the tiles that load the same
 //       row blocks walk k in step and the second load is an L2 hit.
 //     * x streams HBM -> LDS through global_load_lds_dwordx4 into a ring of
-//       32-wide k stages (5 slots issued four stages ahead; with RoPE 4 slots
-//       and one slot for the next stage's table entries).  The 16-byte chunk
+//       32-wide k stages (5 slots issued four stages ahead; with RoPE 4 slots,
+//       and a fifth for the next stage's table entries or the frequencies).  The 16-byte chunk
 //       c of row r sits at position c ^ ((r >> 2) & 3) of its 64-byte LDS
 //       row, which makes the MFMA fragment reads bank-conflict free.
 //     * RoPE is applied in place in the stage before its MFMAs: each lane
@@ -44,7 +47,7 @@ constexpr int kSyThreads = 512;
 constexpr int kSyTile = 256;
 constexpr int kSyBlk = kSyTile * 64;   // bytes of one row block per stage (256 rows x 32 bf16)
 constexpr int kSySlot = 2 * kSyBlk;    // A and B row blocks
-constexpr int kSyLdsSlots = 5;    // 160 KB: x ring of 5 (plain) or 4 x + 1 RoPE table (fused)
+constexpr int kSyLdsSlots = 5;    // 160 KB: x ring of 5 (plain), or 4 x + table or frequencies (fused)
 constexpr int kSyTileElems = kSyTile * kSyTile;
 
 typedef __attribute__((address_space(3))) uint8_t lds_u8;
@@ -66,6 +69,7 @@ struct SyArgs {
   int per_split;       // work items per split of a slab
   int nfull;           // of which full tiles (the rest: diagonal pairs)
   const uint32_t* cs;  // RoPE table, stage-major [N/32][T][16] (cos, sin) dwords, or null
+  const float* freqs = nullptr;  // relative RoPE: the N frequencies (cos, sin made in the kernel)
   bf16_t* part;        // [nslab][ntl][nsplit][256*256] partial score tiles (bf16)
   bf16_t* qr;          // optional RoPE(x) copy
   int64_t r0, r1, r2;
@@ -220,17 +224,22 @@ __device__ __forceinline__ f32x16 mma(bf16x8 a, bf16x8 b, f32x16 c) {
 // score kernel needs for a 256-row block are one contiguous 16 KB run.  Row t
 // is position rope_start + t (absolute table), or the half-integer distance
 // t + 0.5 (relative table: rows rotated about the centre of their tile).
+// phase = fp32(pos) * freq, then cos/sin of 2 pi frac(phase); v_cos/v_sin
+// take the angle in revolutions, so frac(phase) goes in directly.  The values
+// are rounded to bf16, far above the hardware functions' error.  One dword
+// (cos | sin << 16); the table kernel and the score kernel's relative mode
+// both make their entries here, so they are the same bits.
+__device__ __forceinline__ uint32_t rope_cs(float pos, float freq) {
+  const float ph = __fmul_rn(pos, freq);
+  const float fr = ph - floorf(ph);
+  return pack_bf2(__builtin_amdgcn_cosf(fr), __builtin_amdgcn_sinf(fr));
+}
+
 __global__ __launch_bounds__(256) void k_rope_table(const float* __restrict__ freqs, int64_t rope_start,
-                                                    int N2, int T, bool half, uint32_t* __restrict__ cs) {
+                                                    int N2, int T, uint32_t* __restrict__ cs) {
   const int t = blockIdx.y, m = blockIdx.x * 256 + threadIdx.x;
   if (m >= N2) return;
-  // phase = fp32(pos) * freq, then cos/sin of 2 pi frac(phase); v_cos/v_sin
-  // take the angle in revolutions, so frac(phase) goes in directly.  The
-  // values are rounded to bf16, far above the hardware functions' error.
-  const float pos = half ? float(t) + 0.5f : float(rope_start + t);
-  const float ph = __fmul_rn(pos, freqs[2 * m]);
-  const float fr = ph - floorf(ph);
-  cs[(int64_t(m >> 4) * T + t) * 16 + (m & 15)] = pack_bf2(__builtin_amdgcn_cosf(fr), __builtin_amdgcn_sinf(fr));
+  cs[(int64_t(m >> 4) * T + t) * 16 + (m & 15)] = rope_cs(float(rope_start + t), freqs[2 * m]);
 }
 
 // Diagonal tiles (Q = K) in pairs: the 36 lower 32x32 blocks of one diagonal
@@ -347,17 +356,20 @@ __global__ __launch_bounds__(kSyThreads, 1) void k_sy_scores(const SyArgs a) {
     xoff[u] = uint32_t((int64_t(rc) * (blk == 0 ? a.q2 : (SELF ? a.q2 : a.k2)) + 8 * c) * 2);
     toff[u] = uint32_t(rc * 64 + 16 * c);
   }
-  // Relative table rows of this lane's chunks (rho: LDS row of chunk 0):
+  // Relative positions of this lane's chunks (rho: LDS row of chunk 0):
   // diagonal items q = 127 - rho for all four chunks; full tiles
-  // q = 128 (ta - tb - 1) + rho (chunks 0 and 3) and + 255 - rho (1 and 2).
-  uint32_t trel[2] = {0u, 0u};
+  // q = 128 (ta - tb - 1) + rho (chunks 0 and 3) and + 255 - rho (1 and 2);
+  // the angle is that of q + 0.5.  The lane's chunk holds pairs 4 cq .. +3
+  // of each stage.
+  float qpos[2] = {0.f, 0.f};
+  int rcq = 0;
   if constexpr (REL) {
     const int rho = 16 * w + (lane >> 2);
-    const int cq = (lane & 3) ^ ((lane >> 4) & 3);
+    rcq = (lane & 3) ^ ((lane >> 4) & 3);
     const int q0 = diag ? 127 - rho : 128 * (ta - tb - 1) + rho;
     const int q1 = diag ? q0 : 128 * (ta - tb - 1) + 255 - rho;
-    trel[0] = uint32_t(q0 * 64 + 16 * cq);
-    trel[1] = uint32_t(q1 * 64 + 16 * cq);
+    qpos[0] = float(q0) + 0.5f;
+    qpos[1] = float(q1) + 0.5f;
   }
   // MFMA fragment offsets within a row block for the two k16 halves of a
   // stage; lrev reads a 32-row group stored in reverse (REL upper half), so
@@ -378,14 +390,24 @@ __global__ __launch_bounds__(kSyThreads, 1) void k_sy_scores(const SyArgs a) {
 
   auto kofs = [&](int s) { return (split + S * (s >> 1)) * 64 + (s & 1) * 32; };
   // LDS: an x ring of NX slots, issued lead = NX - 1 stages ahead; with RoPE
-  // four x slots and one slot for the table entries of the next stage
-  // (relative tables: two 16 KB slots, stage s in slot s & 1).
+  // four x slots and a fifth slot: absolute positions, the table entries of
+  // the next stage; relative, the frequencies of this workgroup's stages
+  // (16 pairs a stage, at most 512 stages), from which each lane makes its
+  // cos/sin entries.
   constexpr int NX = ROPE ? 4 : 5;
   constexpr int lead = NX - 1;
   auto xslot_ofs = [&](int s) { return (s % NX) * kSySlot; };
   auto slot = [&](int s) { return sy_lds + xslot_ofs(s); };
-  auto tslot_ofs = [&](int s) { return NX * kSySlot + (REL ? (s & 1) * 16384 : 0); };
+  auto tslot_ofs = [&](int s) { return NX * kSySlot; };
   auto tslot = [&](int s) { return sy_lds + tslot_ofs(s); };
+  const float* const pfl = reinterpret_cast<const float*>(sy_lds + NX * kSySlot);
+  // (cos, sin) dwords of this lane's four pairs of stage st at position p:
+  // the relative table's entries, made from the same arithmetic
+  auto rel_entry = [&](int st, float p) {
+    const float* f = pfl + st * 16 + 4 * rcq;
+    const float f0 = f[0], f1 = f[1], f2 = f[2], f3 = f[3];
+    return u32x4{rope_cs(p, f0), rope_cs(p, f1), rope_cs(p, f2), rope_cs(p, f3)};
+  };
   // The DMA instructions of one stage: per-stage scalar bases, per-instruction
   // immediates (instruction u of wave w fills LDS bytes [(8u + w) KB, +1 KB)
   // of its slot).
@@ -411,10 +433,7 @@ __global__ __launch_bounds__(kSyThreads, 1) void k_sy_scores(const SyArgs a) {
   };
   auto dma_t = [&](const StageDma& d, auto ic) {
     constexpr int i = decltype(ic)::value;
-    if constexpr (REL)
-      dma16<i * 8192>(d.tm0, tbase, trel[i] + d.kt);
-    else
-      dma16<i * 8192>(d.tm0, tbase, toff[i] + d.kt);
+    dma16<i * 8192>(d.tm0, tbase, toff[i] + d.kt);
   };
   // RoPE in place of chunk u of stage s (this lane's own DMA chunk)
   // (the row and chunk of instruction u follow from the lane: row
@@ -443,7 +462,10 @@ __global__ __launch_bounds__(kSyThreads, 1) void k_sy_scores(const SyArgs a) {
   auto rot_load = [&](int s, auto wtc, auto uc, u32x4& x, u32x4& t) {
     constexpr int u = decltype(uc)::value;
     x = *reinterpret_cast<const u32x4*>(slot(s) + vrot + u * 8192);
-    t = *reinterpret_cast<const u32x4*>(tslot(s) + vrot + sy_rot_tidx<REL>(decltype(wtc)::value, u) * 8192);
+    if constexpr (REL)
+      t = rel_entry(s, qpos[sy_rot_tidx<REL>(decltype(wtc)::value, u)]);
+    else
+      t = *reinterpret_cast<const u32x4*>(tslot(s) + vrot + sy_rot_tidx<REL>(decltype(wtc)::value, u) * 8192);
   };
 
   // The wave program selects one of five instantiations of the whole pipeline
@@ -523,19 +545,14 @@ __global__ __launch_bounds__(kSyThreads, 1) void k_sy_scores(const SyArgs a) {
     if constexpr (REL) {
       for (int st = 0; st < lead - 1; ++st) {
         const StageDma d = stage_dma(st);
-        dma_x(d, I0());
-        dma_x(d, I1());
-        sy_static_for<NT>([&](auto ic) { dma_t(d, ic); });
-        dma_x(d, I2());
-        dma_x(d, I3());
+        sy_static_for<4>([&](auto uc) { dma_x(d, uc); });
       }
       const StageDma d = stage_dma(lead - 1);
       dma_x(d, I0());
       dma_x(d, I1());
-      sy_wait<(lead - 2) * (4 + NT) + 2>();  // stage 0 and its table landed
+      sy_wait<(lead - 2) * 4 + 2>();  // stage 0 landed
       rotate_all(0);
       sy_barrier();
-      sy_static_for<NT>([&](auto ic) { dma_t(d, ic); });
       dma_x(d, I2());
       dma_x(d, I3());
     } else {
@@ -576,19 +593,16 @@ __global__ __launch_bounds__(kSyThreads, 1) void k_sy_scores(const SyArgs a) {
     // slot (s-1) % NX, last read before the previous barrier; the table slot
     // is rewritten after the barrier that follows its rotation.
     constexpr int KW = NM / 2 - 1;  // wait for stage s+1 after first-half MFMA KW
-    // operations issued after the awaited ones at that wait: RoPE, after the
-    // table of s+1: x chunks 2-3 of s + lead - 1 and 0-1 of s + lead; else,
-    // after x of s+1: x of s+2 .. s+lead-1 and chunks 0-1 of s + lead
-    // (REL: after x chunks 2-3 of s+1, stage s+2 with its table and chunks
-    // 0-1 of s + lead)
-    constexpr int NWAIT = REL ? (lead - 2) * (4 + NT) + 2 : ROPE ? 4 : (lead - 2) * 4 + 2;
+    // (without RoPE) operations issued after the awaited ones at that wait:
+    // after x of s+1, x of s+2 .. s+lead-1 and chunks 0-1 of s + lead
+    constexpr int NWAIT = (lead - 2) * 4 + 2;
     // RoPE: the wait for stage s+1 comes first, all four chunks and their
     // table entries are read at once, and half a chunk is rotated after each
     // of the first eight MFMAs (scheduling barriers keep that order, so the
     // rotation's VALU work runs under the MFMAs).  Operations issued after
     // the awaited ones: REL, stages s+2 .. s+lead-1 with their tables;
     // absolute, x chunks 2-3 of s+2 after the table of s+1.
-    constexpr int NWAITR = REL ? (lead - 2) * (4 + NT) : 2;
+    constexpr int NWAITR = REL ? (lead - 2) * 4 : 2;
     constexpr int NTD = REL ? NT : 4;  // distinct table entries per lane and stage
     for (int s = 0; s + 1 < nst; ++s) {
       read_frags(f1, s, 1);
@@ -601,7 +615,10 @@ __global__ __launch_bounds__(kSyThreads, 1) void k_sy_scores(const SyArgs a) {
           x[decltype(uc)::value] = *reinterpret_cast<const u32x4*>(slot(s + 1) + vrot + decltype(uc)::value * 8192);
         });
         sy_static_for<NTD>([&](auto ic) {
-          t[decltype(ic)::value] = *reinterpret_cast<const u32x4*>(tslot(s + 1) + vrot + decltype(ic)::value * 8192);
+          if constexpr (REL)
+            t[decltype(ic)::value] = rel_entry(s + 1, qpos[decltype(ic)::value]);
+          else
+            t[decltype(ic)::value] = *reinterpret_cast<const u32x4*>(tslot(s + 1) + vrot + decltype(ic)::value * 8192);
         });
         __builtin_amdgcn_sched_barrier(0);
         sy_static_for<NM>([&](auto mc) {
@@ -644,9 +661,7 @@ __global__ __launch_bounds__(kSyThreads, 1) void k_sy_scores(const SyArgs a) {
       __builtin_amdgcn_sched_barrier(0);
       sy_barrier();
       read_frags(f0, s + 1, 0);
-      if constexpr (REL) {
-        sy_static_for<NT>([&](auto ic) { dma_t(d, ic); });  // table of stage s + lead
-      } else if constexpr (ROPE) {
+      if constexpr (ROPE && !REL) {
         const StageDma dt = stage_dma(s + 2);
         sy_static_for<4>([&](auto ic) { dma_t(dt, ic); });
       }
@@ -737,6 +752,13 @@ __global__ __launch_bounds__(kSyThreads, 1) void k_sy_scores(const SyArgs a) {
       }
     });
   };
+  if constexpr (REL) {
+    // the frequencies of this workgroup's stages into the fifth slot (plain
+    // loads and stores, before any DMA is in flight)
+    float* const pf = reinterpret_cast<float*>(sy_lds + 4 * kSySlot);
+    for (int i = tid; i < nst * 16; i += kSyThreads) pf[i] = a.freqs[kofs(i >> 4) + 2 * (i & 15)];
+    __syncthreads();
+  }
   if (!diag) {
     run(std::integral_constant<int, 0>());
   } else {
@@ -1350,8 +1372,9 @@ SyPlan sy_plan(int64_t nslab, int64_t T, int64_t N, bool self, bool rope, int64_
   p.nsplit = S;
   p.per_split = per_split;
   p.ips = per_split * S;
-  // table rows: T positions (absolute) or 128 nt distances (relative)
-  p.table_bytes = rope ? align_up(size_t(std::max<int64_t>(T, 128 * p.nt)) * size_t(N / 2) * 4, 256) : 0;
+  // table of T absolute positions (used when the RoPE(x) copy is asked for,
+  // or more than 512 stages per workgroup; else cos/sin are made in the kernel)
+  p.table_bytes = rope ? align_up(size_t(T) * size_t(N / 2) * 4, 256) : 0;
   p.part_bytes = size_t(nslab) * size_t(p.ntl) * size_t(S) * kSyTileElems * sizeof(bf16_t);
   (void)Dv;
   p.ws_bytes = p.table_bytes + p.part_bytes;
@@ -1396,7 +1419,7 @@ bool sy_cold_check(const bdh_tensor4* q, const bdh_tensor4* k, const bdh_tensor4
   // score x V: 8-element (16 / 32-byte) V row chunks, 256 columns per launch
   if (v->size[3] % 8 != 0 || !rows16(v)) return false;
   if (((T - 1) * std::max(q->stride[2], k->stride[2]) + N) * 2 >= (int64_t(1) << 31)) return false;
-  if (rope && std::max<int64_t>(T, 128 * ((T + kSyTile - 1) / kSyTile)) * N * 2 >= (int64_t(1) << 31)) return false;
+  if (rope && T * N * 2 >= (int64_t(1) << 31)) return false;  // 32-bit offsets into a table
   if (T > 65535) return false;
   if (qr != nullptr && (qr->dtype != BDH_BF16 || !rows16(qr))) return false;
   const int64_t nslab = B * H;
@@ -1421,12 +1444,9 @@ namespace {
 
 // past > 0 (no RoPE): out holds rows past.. only, and the score tiles of the
 // row tiles below past / 256 are neither computed nor stored.
-// ext_table (relative RoPE only): a table built by sy_build_rel_table with
-// ext_rows >= 128 * (tiles of T) rows, used instead of building one in ws
-// (ws then needs only the partial tiles).
 int sy_run(const bdh_tensor4* q, const bdh_tensor4* k, const bdh_tensor4* v, const bdh_tensor4* out,
            const float* freqs, int64_t rope_start, const bdh_tensor4* qr, int64_t past, void* ws,
-           size_t ws_bytes, hipStream_t s, const void* ext_table = nullptr, int64_t ext_rows = 0) {
+           size_t ws_bytes, hipStream_t s) {
   const int64_t B = q->size[0], H = q->size[1], T = q->size[2], N = q->size[3];
   const bool rope = freqs != nullptr;
   SyPlan p;
@@ -1436,24 +1456,22 @@ int sy_run(const bdh_tensor4* q, const bdh_tensor4* k, const bdh_tensor4* v, con
   const int64_t nslab = B * H;
   const int64_t Dv = v->size[3];
   const int64_t grid_scores = 8 * ((nslab + 7) / 8) * p.ips;
-  // Without the RoPE(x) copy the scores use the relative table (rows rotated
-  // about their tile's centre); the copy needs absolute positions.
+  // Without the RoPE(x) copy the scores rotate rows about their tile's
+  // centre, and each lane makes its cos/sin entries from the frequencies,
+  // which the workgroup keeps in LDS (16 a stage, at most 512 stages); the
+  // copy, or more stages, use a table of absolute positions.
   const bool want_qr = qr != nullptr && numel4(qr) > 0;
-  const bool rel = rope && !want_qr;
-  if (rel && ext_table != nullptr && ext_rows < int64_t(128) * p.nt) return BDH_ERR_ARG;
-  // (a table whose byte offsets pass 2^31 is not used: the kernel's offsets
-  // are 32-bit; the one built in ws for this T fits)
-  const bool given = rel && ext_table != nullptr && ext_rows * N * 2 < (int64_t(1) << 31);
-  if (ws == nullptr || ws_bytes < (given ? p.part_bytes : p.ws_bytes)) return BDH_ERR_WORKSPACE;
+  const int max_stages = 2 * ((p.nchunk + p.nsplit - 1) / p.nsplit);
+  const bool rel = rope && !want_qr && max_stages <= 512;
+  if (ws == nullptr || ws_bytes < p.ws_bytes) return BDH_ERR_WORKSPACE;
 
   uint8_t* wsb = static_cast<uint8_t*>(ws);
-  uint32_t* table = given ? static_cast<uint32_t*>(const_cast<void*>(ext_table))
-                          : (rope ? reinterpret_cast<uint32_t*>(wsb) : nullptr);
-  bf16_t* part = reinterpret_cast<bf16_t*>(given ? wsb : wsb + p.table_bytes);
-  const int tq = given ? int(ext_rows) : (rel ? 128 * p.nt : int(T));
-  if (rope && !given) {
+  uint32_t* table = rope && !rel ? reinterpret_cast<uint32_t*>(wsb) : nullptr;
+  bf16_t* part = reinterpret_cast<bf16_t*>(wsb + p.table_bytes);
+  const int tq = rope && !rel ? int(T) : 0;
+  if (table != nullptr) {
     BDH_LAUNCH("k_rope_table", k_rope_table, dim3(unsigned((N / 2 + 255) / 256), unsigned(tq)), dim3(256), 0, s,
-               freqs, rope_start, int(N / 2), tq, rel, table);
+               freqs, rope_start, int(N / 2), tq, table);
   }
   SyArgs a;
   a.g = nullptr;
@@ -1476,6 +1494,7 @@ int sy_run(const bdh_tensor4* q, const bdh_tensor4* k, const bdh_tensor4* v, con
   a.ntl = p.ntl;
   a.t0 = p.t0;
   a.cs = table;
+  a.freqs = rel ? freqs : nullptr;
   a.tq = tq;
   a.part = part;
   a.qr = nullptr;
@@ -1536,27 +1555,6 @@ int sy_cold(const bdh_tensor4* q, const bdh_tensor4* k, const bdh_tensor4* v, co
             const float* freqs, int64_t rope_start, const bdh_tensor4* qr, void* ws, size_t ws_bytes,
             hipStream_t s) {
   return sy_run(q, k, v, out, freqs, rope_start, qr, 0, ws, ws_bytes, s);
-}
-
-size_t sy_rel_table_bytes(int64_t T, int64_t N) {
-  if (T <= 0 || N <= 0 || N % 64 != 0) return 0;
-  return align_up(size_t(128 * ((T + kSyTile - 1) / kSyTile)) * size_t(N / 2) * 4, 256);
-}
-
-int sy_build_rel_table(const float* freqs, int64_t N, int64_t T, void* table, size_t bytes, hipStream_t s) {
-  const size_t need = sy_rel_table_bytes(T, N);
-  if (need == 0) return BDH_ERR_SHAPE;
-  if (freqs == nullptr || table == nullptr || bytes < need) return BDH_ERR_ARG;
-  const int rows = int(128 * ((T + kSyTile - 1) / kSyTile));
-  if (rows > 65535) return BDH_ERR_SHAPE;
-  BDH_LAUNCH("k_rope_table", k_rope_table, dim3(unsigned((N / 2 + 255) / 256), unsigned(rows)), dim3(256), 0, s,
-             freqs, int64_t(0), int(N / 2), rows, true, static_cast<uint32_t*>(table));
-  return BDH_OK;
-}
-
-int sy_cold_tab(const bdh_tensor4* x, const bdh_tensor4* v, const bdh_tensor4* out, const float* freqs,
-                int64_t rope_start, const void* table, int64_t rows, void* ws, size_t ws_bytes, hipStream_t s) {
-  return sy_run(x, x, v, out, freqs, rope_start, nullptr, 0, ws, ws_bytes, s, table, rows);
 }
 
 size_t sy_past_workspace(int64_t B, int64_t H, int64_t Tk, int64_t past, int64_t N, int64_t Dv) {

@@ -86,29 +86,6 @@ int bdh_tril_rope_score_v(const bdh_tensor4* x, const bdh_tensor4* v,
                           bdh_stream stream);
 
 /*
- * The same forward with its RoPE table built once and kept by the caller, as
- * the reference keeps its cos/sin table across layers and steps
- * (bdh.py:157-200 ensure_rope_table and rope_cos_sin; bdh.py:125-139 reuse of a
- * given cos_sin).  The table holds (cos, sin) of every pair at positions
- * measured from each 256-row tile's centre, so it depends on freqs and the
- * tile count only, not on rope_start.
- * bdh_rope_rel_table_bytes: table size for sequences of up to T rows (0 when
- * N is not a multiple of 64: use bdh_tril_rope_score_v).
- * bdh_rope_rel_table: build it on `stream`.
- * bdh_tril_rope_score_v_tab: as bdh_tril_rope_score_v without qr_out, for
- * T <= table_T; results equal bdh_tril_rope_score_v's bit for bit.
- */
-size_t bdh_rope_rel_table_bytes(int64_t T, int64_t N);
-int bdh_rope_rel_table(const float* freqs, int64_t N, int64_t T, void* table,
-                       size_t table_bytes, bdh_stream stream);
-int bdh_tril_rope_score_v_tab(const bdh_tensor4* x, const bdh_tensor4* v,
-                              const bdh_tensor4* out, const float* freqs,
-                              int64_t rope_start, const void* table,
-                              size_t table_bytes, int64_t table_T,
-                              void* workspace, size_t workspace_bytes,
-                              bdh_stream stream);
-
-/*
  * Queries at an offset (chunked prefill): T new rows after `past` cached rows.
  * out[b,h,i,:] = sum_{j < past+i} <q[b,h,i,:], k[b,h,j,:]> v[b,hv,j,:].
  * Replaces the reference's multi-token step with a cache, which recomputes

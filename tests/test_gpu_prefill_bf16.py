@@ -1,6 +1,6 @@
 """GPU parity of the bf16 prefill path (256x256 split-K score tiles, LDS-DMA
-stream, RoPE from a table built per call or kept per freqs buffer) against
-the CPU oracle.
+stream, RoPE from cos/sin made in the kernel (relative) or a per-call table
+(absolute)) against the CPU oracle.
 
 These shapes all qualify for that path (bf16, N a multiple of 64, 16-byte
 aligned rows): ragged and exact multiples of the 256-row tile, one to five
@@ -205,46 +205,26 @@ def test_bf16_wide_v_runs_score_tiles_per_256_columns(mode, D):
     assert rel_fro(got, want) <= TOL[BF]
 
 
-def test_bf16_cached_rope_table_equals_per_call_table():
-    """The relative RoPE table kept across calls (per freqs buffer) gives the
-    same bits as the table built in the workspace on each call: first use,
-    growth to a longer sequence, reuse of the longer table for a shorter one,
-    other rope_start values, an in-place write to freqs (rebuild), another
-    stream.  The table build is not counted as an entry-point call."""
-    B, H, N, D = 2, 4, 1024, 64
-    f = torch.from_numpy(O.get_freqs(N)).to(DEV)
-    key = (f.device.index, f.data_ptr(), N)
 
-    def both(T, start, seed):
-        x = torch.relu(0.3 * torch.randn(B, H, T, N, generator=torch.Generator(device=DEV).manual_seed(seed),
-                                         device=DEV)).to(BF)
-        v = torch.randn(B, 1, T, D, generator=torch.Generator(device=DEV).manual_seed(seed + 1),
-                        device=DEV).to(BF)
-        n0 = ext.launch_count()
-        got = ext.tril_rope_score_v(x, v, f, start)
-        assert ext.launch_count() == n0 + 1
-        ref = ext.tril_rope_score_v(x, v, f, start, rel_table_cache=False)
-        assert torch.equal(got, ref), (T, start)
-        return ext._rel_tables[key]
-
-    e1 = both(300, 0, 1)
-    assert e1[2] == 512
-    e2 = both(1100, 9, 2)
-    assert e2[2] == 1280
-    e3 = both(300, 4, 3)
-    assert e3[3] is e2[3]  # the longer table serves the shorter sequence
-    f.mul_(1.5)  # new frequencies in place: the version changes, the table is rebuilt
-    e4 = both(300, 0, 4)
-    assert e4[3] is not e2[3] and e4[2] == 1280
-    s = torch.cuda.Stream()
-    s.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(s):
-        both(700, 2, 5)
-    torch.cuda.current_stream().wait_stream(s)
-    torch.cuda.synchronize()
-    # sanity against the oracle for the rebuilt (scaled-frequency) table
-    x = _bf(latent((1, 1, 300, N), 30))
-    v = _bf(normal((1, 1, 300, D), 31))
-    got = np_of(ext.tril_rope_score_v(to_dev(x, BF), to_dev(v, BF), f, 0))
-    want, _ = O.tril_rope_score_v(x, v, f.cpu().numpy(), 0, bf16=True)
+@pytest.mark.parametrize("N,table", [(16384, False), (16448, True)])
+def test_bf16_fused_rope_stage_limit(N, table):
+    """Without the RoPE(x) copy the score kernel makes cos/sin from 16
+    frequencies per stage kept in 32 KB of LDS, so at most 512 stages per
+    workgroup: 256 slabs of T = 2 run one split, so N = 16384 (512 stages)
+    fills it and N = 16448 (514) takes the absolute-position table instead.
+    Both against the oracle; the kernel profile shows which path ran."""
+    B, H, T, D = 8, 32, 2, 16
+    print(f"stage limit N={N}", flush=True)
+    x = _bf(latent((B, H, T, N), 41))
+    v = _bf(normal((B, 1, T, D), 42))
+    freqs = O.get_freqs(N)
+    want, _ = O.tril_rope_score_v(x, v, freqs, 5, bf16=True)
+    ext.profile_enable(True)
+    try:
+        got = np_of(ext.tril_rope_score_v(to_dev(x, BF), to_dev(v, BF), torch.from_numpy(freqs).to(DEV), 5))
+        names = {n for n, _ in ext.profile_collect()}
+    finally:
+        ext.profile_enable(False)
+    assert "k_sy_scores" in names and ("k_rope_table" in names) == table, names
     assert rel_fro(got, want) <= TOL[BF]
+    assert not got[:, :, 0].any()
