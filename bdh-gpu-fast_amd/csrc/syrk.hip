@@ -222,8 +222,8 @@ __device__ __forceinline__ f32x16 mma(bf16x8 a, bf16x8 b, f32x16 c) {
 // RoPE table, stage-major: the (cos, sin) of pair m at row t sits in dword
 // ((m / 16) * T + t) * 16 + m % 16, so the table entries one k32 stage of the
 // score kernel needs for a 256-row block are one contiguous 16 KB run.  Row t
-// is position rope_start + t (absolute table), or the half-integer distance
-// t + 0.5 (relative table: rows rotated about the centre of their tile).
+// is position rope_start + t.  (The score kernel's relative mode makes its
+// entries for half-integer distances itself, with rope_cs below.)
 // phase = fp32(pos) * freq, then cos/sin of 2 pi frac(phase); v_cos/v_sin
 // take the angle in revolutions, so frac(phase) goes in directly.  The values
 // are rounded to bf16, far above the hardware functions' error.  One dword
@@ -308,8 +308,8 @@ constexpr int sy_rot_tidx(int wt, int u) { return !REL ? u : (wt == 0 ? ((u == 1
 // and within a row block the row at LDS position P is block row P (P < 128)
 // or 383 - P (P >= 128), so the two rows a lane loads per block share q: one
 // table entry per lane and stage on diagonal items, two on full tiles (row
-// a of A and row 255 - a of B, rotated by the negated angle).  The table
-// moves at the lead of x through two 16 KB slots.
+// a of A and row 255 - a of B, rotated by the negated angle).  The lane
+// makes those entries from the stage's frequencies in LDS (rel_entry).
 // GOUT (with Q = dO, K = V, one split): instead of partial tiles, write the
 // backward's G = dS + dS^T, dS = tril(dO V^T, -1), into a.g.
 template <int RM, bool SELF, bool GOUT = false>
@@ -586,8 +586,9 @@ __global__ __launch_bounds__(kSyThreads, 1) void k_sy_scores(const SyArgs a) {
     //     chunks 0-1 of stage s + lead issued between them; once this lane's
     //     part of stage s+1 (and its table) landed, the rotation of stage s+1
     //  B. barrier: stage s+1 is complete (loaded and rotated) in LDS
-    //  C. read the first-half fragments of s+1; (RoPE) issue the table of
-    //     stage s+2; second-half MFMAs of s with x chunks 2-3 of stage s + lead.
+    //  C. read the first-half fragments of s+1; (absolute RoPE) issue the
+    //     table of stage s+2; second-half MFMAs of s with x chunks 2-3 of
+    //     stage s + lead.
     // The barrier sits between the halves, so after it the MFMA pipe runs the
     // second half while the next fragments load.  Stage s + lead goes to x
     // slot (s-1) % NX, last read before the previous barrier; the table slot
