@@ -6,7 +6,9 @@ BASELINE shape B=8, nh=4, T=512, N=8192, D=256 in bf16, RoPE fused into the
 HIP kernels (``kernels.bdh_attn_rope(impl="hip")``), inputs resident in HBM.
 One step = one call over the whole batch.  Throughput is the algorithmic
 F = B*nh*(N+D)*T*(T-1) flops per step (strict lower triangle; RoPE's
-elementwise work is not counted) divided by the measured step time.
+elementwise work is not counted) divided by the measured step time.  The step
+runs untimed for 0.2 s, then W warmup steps, then exactly K timed steps
+(defaults K = 200, W = 100), synchronised on both sides.
 
 The JSON line also carries:
   * ``roofline``: the dominant kernel (``k_sy_scores``, the score tiles QR QR^T)
