@@ -311,6 +311,50 @@ __global__ __launch_bounds__(kNT) void k_small_gemm(SmallGemmArgs a) {
       }
 }
 
+// 256 outputs per workgroup (4 consecutive per lane, D % 4 == 0); four
+// groups of 64 threads each sum every fourth split with 16-byte loads, four
+// splits in flight, then combine through LDS.  Each output's sum runs in the
+// order of the scalar kernel below (group g: splits g, g + 4, ...; then the
+// groups in order), so both give the same bits.
+template <typename TO>
+__global__ __launch_bounds__(256) void k_small_gemm_reduce4(const float* part, int nsplit, int M, int D,
+                                                            TO* out, int64_t os) {
+  __shared__ float4 red4[4][64];
+  const int l = threadIdx.x & 63, g = threadIdx.x >> 6;
+  const int64_t MD = int64_t(M) * D;
+  const int64_t idx = (int64_t(blockIdx.x) * 64 + l) * 4;
+  float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (idx < MD) {
+    const float* p = part + idx;
+    int sp = g;
+    for (; sp + 12 < nsplit; sp += 16) {
+      const float4 v0 = *reinterpret_cast<const float4*>(p + int64_t(sp) * MD);
+      const float4 v1 = *reinterpret_cast<const float4*>(p + int64_t(sp + 4) * MD);
+      const float4 v2 = *reinterpret_cast<const float4*>(p + int64_t(sp + 8) * MD);
+      const float4 v3 = *reinterpret_cast<const float4*>(p + int64_t(sp + 12) * MD);
+      s.x += v0.x; s.y += v0.y; s.z += v0.z; s.w += v0.w;
+      s.x += v1.x; s.y += v1.y; s.z += v1.z; s.w += v1.w;
+      s.x += v2.x; s.y += v2.y; s.z += v2.z; s.w += v2.w;
+      s.x += v3.x; s.y += v3.y; s.z += v3.z; s.w += v3.w;
+    }
+    for (; sp < nsplit; sp += 4) {
+      const float4 v = *reinterpret_cast<const float4*>(p + int64_t(sp) * MD);
+      s.x += v.x; s.y += v.y; s.z += v.z; s.w += v.w;
+    }
+  }
+  red4[g][l] = s;
+  __syncthreads();
+  if (g == 0 && idx < MD) {
+    const int64_t m = idx / D, d = idx - m * D;
+    const float4 r0 = red4[0][l], r1 = red4[1][l], r2 = red4[2][l], r3 = red4[3][l];
+    TO* o = out + m * os + d;
+    o[0] = from_f<TO>(r0.x + r1.x + r2.x + r3.x);
+    o[1] = from_f<TO>(r0.y + r1.y + r2.y + r3.y);
+    o[2] = from_f<TO>(r0.z + r1.z + r2.z + r3.z);
+    o[3] = from_f<TO>(r0.w + r1.w + r2.w + r3.w);
+  }
+}
+
 // 64 outputs per workgroup; four groups of 64 threads each sum every fourth
 // split (coalesced 256-byte rows), then combine through LDS.
 template <typename TO>
@@ -505,6 +549,16 @@ extern "C" int bdh_small_gemm(const bdh_tensor4* a, const bdh_tensor4* b, const 
   hipStream_t s = static_cast<hipStream_t>(stream);
   const dim3 grid{unsigned((D + kTile - 1) / kTile), unsigned(p.nsplit), unsigned((M + kTile - 1) / kTile)};
   BDH_LAUNCH("k_small_gemm", k_small_gemm, grid, dim3(kNT), 0, s, g);
+  if (D % 4 == 0) {
+    const unsigned rg4 = unsigned((M * D / 4 + 63) / 64);
+    if (out->dtype == BDH_BF16)
+      BDH_LAUNCH("k_small_gemm_reduce", k_small_gemm_reduce4<bf16_t>, dim3(rg4), dim3(256), 0, s, g.part,
+                 p.nsplit, int(M), int(D), static_cast<bf16_t*>(out->data), out->stride[2]);
+    else
+      BDH_LAUNCH("k_small_gemm_reduce", k_small_gemm_reduce4<float>, dim3(rg4), dim3(256), 0, s, g.part,
+                 p.nsplit, int(M), int(D), static_cast<float*>(out->data), out->stride[2]);
+    return BDH_OK;
+  }
   const unsigned rg = unsigned((M * D + 63) / 64);
   if (out->dtype == BDH_BF16)
     BDH_LAUNCH("k_small_gemm_reduce", k_small_gemm_reduce<bf16_t>, dim3(rg), dim3(256), 0, s, g.part, p.nsplit,
