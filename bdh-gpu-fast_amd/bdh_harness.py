@@ -94,6 +94,24 @@ def _ln(x: torch.Tensor) -> torch.Tensor:
     return F.layer_norm(x, (x.size(-1),), eps=1e-5)
 
 
+def _ln_rows_ok(t: torch.Tensor) -> bool:
+    """Shapes the HIP row LayerNorm takes: D = 64 * 2^k <= 1024, fp32 or bf16."""
+    d = t.size(-1)
+    return t.dtype in (torch.float32, torch.bfloat16) and d % 64 == 0 and d <= 1024 and (d // 64) & (d // 64 - 1) == 0
+
+
+def _ln_fast(y: torch.Tensor, x: Optional[torch.Tensor] = None, dt: Optional[torch.dtype] = None) -> torch.Tensor:
+    """``LN(y)`` (in ``dt``) or ``LN(x + LN(y))`` (in x's dtype) as one HIP pass: the
+    LayerNorm of the reference's _ln / _residual_ln (bdh.py:565-574, 731-750), fp32
+    arithmetic as under autocast."""
+    if _ln_rows_ok(y) and (x is None or _ln_rows_ok(x)):
+        return kernels.layer_norm_rows(y, x, out_dtype=x.dtype if x is not None else dt)
+    if x is None:
+        out = _ln(y.float())
+        return out.to(dt) if dt is not None else out
+    return _ln(x + _ln(y.float()))
+
+
 # The dense products are 2-D matrix products (hipBLASLt GEMMs) on contiguous
 # operands: no einsum and no batched product, whose bf16 forms with
 # transposed-view operands (einsum transposes inside; autograd's backward of
@@ -238,7 +256,7 @@ class BDH(nn.Module):
             x_sparse = x_bthn.permute(0, 2, 1, 3)  # (B, nh, T, N) view
             y_kv = self._attention(level, x_sparse, x.unsqueeze(1), rope_start, cache, impl, cos_sin)
             if fast:
-                xy = _gated_product(x_bthn, _ln(y_kv), self.encoder_v, prep["encv_t"])
+                xy = _gated_product(x_bthn, _ln_fast(y_kv, dt=_compute_dtype(x_bthn)), self.encoder_v, prep["encv_t"])
                 if B * T <= 256 and xy.dtype == torch.bfloat16:
                     # few rows (decode): split-K GEMM instead of a few tiles down K = nh*N
                     y_mlp = kernels.small_gemm(xy.view(B * T, nh * N), prep["dec"]).view(B, T, -1)
@@ -247,7 +265,7 @@ class BDH(nn.Module):
             else:
                 xy = x_bthn * _encode_heads(_ln(y_kv), self.encoder_v)
                 y_mlp = xy.view(B, T, nh * N) @ self.decoder
-            x = _ln(x + _ln(y_mlp))
+            x = _ln_fast(y_mlp, x) if fast else _ln(x + _ln(y_mlp))
         if cache is not None:
             cache.commit(T)
         if last_only:

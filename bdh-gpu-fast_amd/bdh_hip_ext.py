@@ -44,6 +44,7 @@ __all__ = [
     "relu_mul",
     "gated_gemm",
     "small_gemm",
+    "layer_norm_rows",
     "profile_enable",
     "profile_collect",
     "launch_count",
@@ -75,6 +76,7 @@ EXPORTED_SYMBOLS = (
     "bdh_gated_gemm",
     "bdh_small_gemm_workspace",
     "bdh_small_gemm",
+    "bdh_layer_norm_rows",
     "bdh_profile_enable",
     "bdh_profile_collect",
 )
@@ -130,6 +132,7 @@ def _load():
         "bdh_tril_rope_score_v_bwd_workspace": (sz, [i64, i64, i64, i64, i64, i64, i32]),
         "bdh_tril_rope_score_v_bwd": (ctypes.c_int, [P, P, P, fp, i64, P, P, vp, sz, vp]),
         "bdh_relu_mul": (ctypes.c_int, [P, P, P, vp]),
+        "bdh_layer_norm_rows": (ctypes.c_int, [P, P, P, vp]),
         "bdh_gated_gemm": (ctypes.c_int, [P, P, P, P, vp]),
         "bdh_small_gemm_workspace": (sz, [i64, i64, i64]),
         "bdh_small_gemm": (ctypes.c_int, [P, P, P, vp, sz, vp]),
@@ -482,6 +485,27 @@ def relu_mul(x: torch.Tensor, y: torch.Tensor, out: Optional[torch.Tensor] = Non
     with torch.cuda.device(dev):
         rc = _lib.bdh_relu_mul(ctypes.byref(_t4(x)), ctypes.byref(_t4(y)), ctypes.byref(_t4(out)), _stream(dev))
     _check(rc, "relu_mul")
+    return out
+
+
+def layer_norm_rows(y: torch.Tensor, x: Optional[torch.Tensor] = None, out_dtype: Optional[torch.dtype] = None,
+                    out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """LayerNorm over the last dim (no affine, eps 1e-5): ``LN(y)``, or ``LN(x + LN(y))``
+    with ``x``; 1- to 4-D tensors of one shape, fp32 or bf16; ``out`` defaults to a
+    contiguous tensor in ``out_dtype`` (y's dtype)."""
+    dev = _require_device(y, x, out)
+    if x is not None and x.shape != y.shape:
+        raise ValueError(f"layer_norm_rows: x {tuple(x.shape)} and y {tuple(y.shape)} differ")
+    if out is None:
+        out = torch.empty(y.shape, dtype=out_dtype or y.dtype, device=dev)
+
+    def v4(t: torch.Tensor) -> torch.Tensor:
+        return t.reshape((1,) * (4 - t.dim()) + tuple(t.shape)) if t.dim() < 4 else t
+
+    with torch.cuda.device(dev):
+        rc = _lib.bdh_layer_norm_rows(ctypes.byref(_t4(v4(x))) if x is not None else None, ctypes.byref(_t4(v4(y))),
+                                      ctypes.byref(_t4(v4(out))), _stream(dev))
+    _check(rc, "layer_norm_rows")
     return out
 
 

@@ -375,6 +375,64 @@ __global__ __launch_bounds__(256) void k_small_gemm_reduce(const float* part, in
   }
 }
 
+// ---------------------------------------------------------------------------
+// LayerNorm over the last dim of rows (no affine, eps 1e-5, fp32 arithmetic),
+// the model's _ln and _residual_ln (reference bdh.py:565-574, 731-750):
+//   out = LN(y)              (x absent)
+//   out = LN(x + LN(y))      (the layer's residual update)
+// One wave per row, elements lane + 64 e (e < E, D = 64 E): coalesced, and
+// the row stays in registers, so the mean and then the variance about it
+// take two passes over registers and one over memory.  Rows are the first
+// three dims of 4-D strided views.
+struct LnArgs {
+  View x, y, o;
+  int64_t d1, d2, rows;
+  int D;
+};
+
+template <int E>
+__device__ __forceinline__ void ln_row(float (&v)[E], int D) {
+  float s = 0.f;
+#pragma unroll
+  for (int e = 0; e < E; ++e) s += v[e];
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
+  const float mean = s / float(D);
+  float q = 0.f;
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    v[e] -= mean;
+    q += v[e] * v[e];
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) q += __shfl_xor(q, off, 64);
+  const float r = rsqrtf(q / float(D) + 1e-5f);
+#pragma unroll
+  for (int e = 0; e < E; ++e) v[e] *= r;
+}
+
+template <typename TX, typename TY, typename TO, int E>
+__global__ __launch_bounds__(256) void k_ln_rows(const LnArgs a) {
+  const int64_t row = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (row >= a.rows) return;
+  const int lane = threadIdx.x & 63;
+  const int64_t i2 = row % a.d2, t = row / a.d2, i1 = t % a.d1, i0 = t / a.d1;
+  const TY* y = static_cast<const TY*>(a.y.p) + i0 * a.y.s0 + i1 * a.y.s1 + i2 * a.y.s2;
+  float v[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) v[e] = to_f(y[lane + 64 * e]);
+  ln_row<E>(v, a.D);
+  if (a.x.p != nullptr) {
+    const TX* x = static_cast<const TX*>(a.x.p) + i0 * a.x.s0 + i1 * a.x.s1 + i2 * a.x.s2;
+#pragma unroll
+    for (int e = 0; e < E; ++e) v[e] += to_f(x[lane + 64 * e]);
+    ln_row<E>(v, a.D);
+  }
+  TO* o = static_cast<TO*>(const_cast<void*>(a.o.p)) + i0 * a.o.s0 + i1 * a.o.s1 + i2 * a.o.s2;
+#pragma unroll
+  for (int e = 0; e < E; ++e) o[lane + 64 * e] = from_f<TO>(v[e]);
+}
+
 struct SmallGemmPlan {
   int nsplit, kc;
   size_t ws_bytes;
@@ -405,10 +463,67 @@ int launch_relu_mul(const ReluMulArgs& a, int32_t odt, dim3 grid, hipStream_t s)
   return BDH_OK;
 }
 
+template <typename TX, typename TY, typename TO>
+int launch_ln_rows(const LnArgs& a, dim3 grid, hipStream_t s) {
+  switch (a.D / 64) {
+    case 1: BDH_LAUNCH("k_ln_rows", (k_ln_rows<TX, TY, TO, 1>), grid, dim3(256), 0, s, a); break;
+    case 2: BDH_LAUNCH("k_ln_rows", (k_ln_rows<TX, TY, TO, 2>), grid, dim3(256), 0, s, a); break;
+    case 4: BDH_LAUNCH("k_ln_rows", (k_ln_rows<TX, TY, TO, 4>), grid, dim3(256), 0, s, a); break;
+    case 8: BDH_LAUNCH("k_ln_rows", (k_ln_rows<TX, TY, TO, 8>), grid, dim3(256), 0, s, a); break;
+    case 16: BDH_LAUNCH("k_ln_rows", (k_ln_rows<TX, TY, TO, 16>), grid, dim3(256), 0, s, a); break;
+    default: return BDH_ERR_SHAPE;
+  }
+  return BDH_OK;
+}
+
+template <typename TX, typename TY>
+int launch_ln_rows_o(const LnArgs& a, int32_t odt, dim3 grid, hipStream_t s) {
+  return odt == BDH_BF16 ? launch_ln_rows<TX, TY, bf16_t>(a, grid, s) : launch_ln_rows<TX, TY, float>(a, grid, s);
+}
+
 }  // namespace
 }  // namespace bdh
 
 using namespace bdh;
+
+extern "C" int bdh_layer_norm_rows(const bdh_tensor4* x, const bdh_tensor4* y, const bdh_tensor4* out,
+                                   bdh_stream stream) {
+  BDH_TRY(check_view(y));
+  BDH_TRY(check_view(out));
+  if (x != nullptr) BDH_TRY(check_view(x));
+  for (int i = 0; i < 4; ++i)
+    if (out->size[i] != y->size[i] || (x != nullptr && x->size[i] != y->size[i])) return BDH_ERR_SHAPE;
+  if (views_overlap(out, y) || (x != nullptr && views_overlap(out, x))) return BDH_ERR_ALIAS;
+  if (numel4(out) == 0) return BDH_OK;
+  const int64_t D = y->size[3];
+  if (D % 64 != 0 || D > 1024 || ((D / 64) & (D / 64 - 1)) != 0) return BDH_ERR_SHAPE;
+  const int64_t rows = y->size[0] * y->size[1] * y->size[2];
+  if ((rows + 3) / 4 >= (int64_t(1) << 31)) return BDH_ERR_SHAPE;
+  auto view = [](const bdh_tensor4* t) {
+    View v;
+    v.p = t->data;
+    v.s0 = t->stride[0];
+    v.s1 = t->stride[1];
+    v.s2 = t->stride[2];
+    return v;
+  };
+  LnArgs a;
+  a.x = x != nullptr ? view(x) : View{nullptr, 0, 0, 0};
+  a.y = view(y);
+  a.o = view(out);
+  a.d1 = y->size[1];
+  a.d2 = y->size[2];
+  a.rows = rows;
+  a.D = int(D);
+  const dim3 grid{unsigned((rows + 3) / 4)};
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const bool xb = x != nullptr && x->dtype == BDH_BF16, yb = y->dtype == BDH_BF16;
+  if (xb)
+    return yb ? launch_ln_rows_o<bf16_t, bf16_t>(a, out->dtype, grid, s)
+              : launch_ln_rows_o<bf16_t, float>(a, out->dtype, grid, s);
+  return yb ? launch_ln_rows_o<float, bf16_t>(a, out->dtype, grid, s)
+            : launch_ln_rows_o<float, float>(a, out->dtype, grid, s);
+}
 
 extern "C" int bdh_relu_mul(const bdh_tensor4* x, const bdh_tensor4* y, const bdh_tensor4* out,
                             bdh_stream stream) {

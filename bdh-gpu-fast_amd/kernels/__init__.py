@@ -42,6 +42,7 @@ from .hip_attn import (
     has_hip_ext,
     gated_gemm,
     has_hip_kernel,
+    layer_norm_rows,
     relu_mul,
     small_gemm,
     tril_decode,
@@ -82,6 +83,7 @@ __all__ = [
     "relu_mul",
     "gated_gemm",
     "small_gemm",
+    "layer_norm_rows",
     "tril_rope_score_v",
     "tril_decode",
     "has_hip_ext",

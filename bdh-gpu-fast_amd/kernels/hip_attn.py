@@ -140,6 +140,13 @@ def gated_gemm(y: torch.Tensor, wt: torch.Tensor, x: torch.Tensor) -> torch.Tens
     return ext.gated_gemm(y, wt, x)
 
 
+def layer_norm_rows(y: torch.Tensor, x: Optional[torch.Tensor] = None,
+                    out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
+    """``LN(y)`` or ``LN(x + LN(y))`` over the last dim on the GPU (bdh.py:565-574, 731-750)."""
+    ext = _require(y, x)
+    return ext.layer_norm_rows(_last_dim_unit(y), _last_dim_unit(x) if x is not None else None, out_dtype)
+
+
 def small_gemm(a: torch.Tensor, b: torch.Tensor, out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
     """``a @ b`` for few rows of a on the GPU, split over K (the decoder product of a decode step)."""
     ext = _require(a, b)

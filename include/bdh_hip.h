@@ -231,6 +231,17 @@ int bdh_small_gemm(const bdh_tensor4* a, const bdh_tensor4* b, const bdh_tensor4
                    void* workspace, size_t workspace_bytes, bdh_stream stream);
 
 /*
+ * LayerNorm over the last dim (no affine, eps 1e-5, fp32 arithmetic) of the
+ * rows of 4-D views: out = LN(y), or with x (not NULL) out = LN(x + LN(y)).
+ * Replaces the model's _ln (reference bdh.py:565-574, F.layer_norm without
+ * weights) and _residual_ln (bdh.py:731-750, LN(x + LN(y_mlp))) in one pass.
+ * x, y, out: one shape, each f32 or bf16 (out rounded once); D = size[3] a
+ * multiple of 64, at most 1024, with D/64 a power of two.
+ */
+int bdh_layer_norm_rows(const bdh_tensor4* x, const bdh_tensor4* y,
+                        const bdh_tensor4* out, bdh_stream stream);
+
+/*
  * Per-kernel timing (measurement support; no counterpart in the reference).
  * While enabled, every kernel the library launches is bracketed by HIP events
  * on its stream.  bdh_profile_collect() waits for the recorded events and

@@ -11,7 +11,8 @@
   error against the fp32 step no larger than the eager-attention AMP step's
   (both are about 3-6e-2 on the weight gradients, from the model's bf16
   GEMMs; the attention kernels add nothing measurable);
-* ``generate`` end to end.
+* ``generate`` end to end;
+* the row LayerNorm (LN(y), LN(x + LN(y))) against F.layer_norm.
 """
 
 from __future__ import annotations
@@ -19,6 +20,7 @@ from __future__ import annotations
 import numpy as np
 import pytest
 import torch
+import torch.nn.functional as F
 
 from helpers import rel_fro
 from oracle import bdh_model_oracle as M
@@ -201,3 +203,26 @@ def test_small_gemm_matches_reference(shape, odt):
     want = a.float() @ b.float()
     assert got.shape == (M, D) and got.dtype == odt
     assert rel_fro(got.float().cpu().numpy(), want.numpy()) <= (1e-5 if odt == torch.float32 else 1e-2)
+
+
+@pytest.mark.parametrize("D", [64, 256, 512, 1024])
+@pytest.mark.parametrize("dy,dx,do", [(torch.bfloat16, None, torch.bfloat16), (torch.float32, None, torch.float32),
+                                      (torch.bfloat16, torch.float32, torch.float32),
+                                      (torch.float32, torch.bfloat16, torch.bfloat16)])
+def test_layer_norm_rows_matches_reference(D, dy, dx, do):
+    """LN(y) and LN(x + LN(y)) (no affine, eps 1e-5) against F.layer_norm in fp32
+    on the CPU: fp32 outputs within 1e-5, bf16 outputs within bf16 rounding
+    (2^-8 relative); y a permuted (strided) view; rows with a large offset."""
+    print(f"layer_norm_rows D={D} y={dy} x={dx} out={do}", flush=True)
+    g = torch.Generator().manual_seed(D)
+    y = (3.0 * torch.randn(2, 37, 3, D, generator=g) + 100.0).to(dy)
+    x = torch.randn(2, 3, 37, D, generator=g).to(dx) if dx is not None else None
+    yv = y.to(DEV).permute(0, 2, 1, 3)  # (2, 3, 37, D), strided rows
+    got = ext.layer_norm_rows(yv, x.to(DEV) if x is not None else None, out_dtype=do)
+    ln = lambda t: F.layer_norm(t, (D,), eps=1e-5)  # noqa: E731
+    want = ln(y.float().permute(0, 2, 1, 3))
+    if x is not None:
+        want = ln(x.float() + want)
+    assert got.shape == want.shape and got.dtype == do
+    tol = 1e-5 if do == torch.float32 else 2.0 ** -8
+    assert rel_fro(got.float().cpu().numpy(), want.numpy()) <= tol
