@@ -31,10 +31,12 @@ __all__ = [
     "version",
     "tril_score_v",
     "tril_score_v_hip",
+    "tril_score_v_cpu",
     "tril_score_v_past",
     "tril_rope_score_v",
     "tril_decode",
     "tril_decode_hip",
+    "tril_decode_cpu",
     "tril_score_v_bwd",
     "keeps_scores",
     "tril_score_v_save",
@@ -326,6 +328,39 @@ def tril_rope_score_v(
         )
     _check(rc, "tril_rope_score_v")
     return out
+
+
+# ------------------------------------------------------------ CPU entries
+def _acc_dtype(t: torch.Tensor) -> torch.dtype:
+    return torch.float32 if t.dtype in (torch.float16, torch.bfloat16) else t.dtype
+
+
+def _require_cpu(*ts: torch.Tensor) -> None:
+    for t in ts:
+        if t.device.type != "cpu":
+            raise RuntimeError(f"bdh_hip_ext CPU entry: tensors must be on the CPU, got {t.device}")
+
+
+def tril_score_v_cpu(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
+    """CPU cold op, ``tril(q @ k^T, -1) @ v`` in torch, fp32 accumulation for 16-bit
+    inputs and the result in q's dtype: the entry the reference module exports
+    beside its device kernel (csrc/tril_attn_bind.cpp:29 -> tril_attn_cpu.cpp:160-174).
+    The device path never comes here."""
+    _require_cpu(q, k, v)
+    acc = _acc_dtype(q)
+    s = torch.matmul(q.to(acc), k.to(acc).transpose(-2, -1).contiguous())
+    s.tril_(-1)
+    return torch.matmul(s, v.to(acc)).to(q.dtype)
+
+
+def tril_decode_cpu(q: torch.Tensor, k_past: torch.Tensor, v_past: torch.Tensor) -> torch.Tensor:
+    """CPU decode, ``(q @ k_past^T) @ v_past`` in torch (fp32 accumulation for 16-bit
+    inputs, result in q's dtype); reference csrc/tril_attn_bind.cpp:32 ->
+    tril_attn_cpu.cpp:212-238."""
+    _require_cpu(q, k_past, v_past)
+    acc = _acc_dtype(q)
+    s = torch.matmul(q.to(acc), k_past.to(acc).transpose(-2, -1).contiguous())
+    return torch.matmul(s, v_past.to(acc)).to(q.dtype)
 
 
 # -------------------------------------------------------------------- decode

@@ -648,6 +648,7 @@ extern "C" int bdh_small_gemm(const bdh_tensor4* a, const bdh_tensor4* b, const 
   if ((M * D + 63) / 64 >= (int64_t(1) << 31)) return BDH_ERR_SHAPE;
   const SmallGemmPlan p = small_gemm_plan(M, K, D);
   if (workspace == nullptr || workspace_bytes < p.ws_bytes) return BDH_ERR_WORKSPACE;
+  if ((reinterpret_cast<uintptr_t>(workspace) & 3) != 0) return BDH_ERR_WORKSPACE;  // fp32 partials
   if ((M + kTile - 1) / kTile > 65535 || p.nsplit > 65535) return BDH_ERR_SHAPE;
   SmallGemmArgs g;
   g.a = static_cast<const bf16_t*>(a->data);
@@ -664,7 +665,9 @@ extern "C" int bdh_small_gemm(const bdh_tensor4* a, const bdh_tensor4* b, const 
   hipStream_t s = static_cast<hipStream_t>(stream);
   const dim3 grid{unsigned((D + kTile - 1) / kTile), unsigned(p.nsplit), unsigned((M + kTile - 1) / kTile)};
   BDH_LAUNCH("k_small_gemm", k_small_gemm, grid, dim3(kNT), 0, s, g);
-  if (D % 4 == 0) {
+  // the 16-byte reduce needs 16-byte aligned partial rows: D % 4 == 0 and an
+  // aligned workspace (a caller may pass any pointer)
+  if (D % 4 == 0 && (reinterpret_cast<uintptr_t>(workspace) & 15) == 0) {
     const unsigned rg4 = unsigned((M * D / 4 + 63) / 64);
     if (out->dtype == BDH_BF16)
       BDH_LAUNCH("k_small_gemm_reduce", k_small_gemm_reduce4<bf16_t>, dim3(rg4), dim3(256), 0, s, g.part,

@@ -13,9 +13,10 @@ Opt-in long-sequence switch, same knobs as the reference::
     export BDH_ATTN_AUTO_COLD_THRESHOLD=...   # cold T > thr -> hip (mirrors AUTO_THRESHOLD)
 
 With AUTO on and base ``eager``, lengths above the threshold switch to
-``hip`` when the library is loaded and a ROCm device is visible, otherwise
-stay ``eager`` (the reference switched to triton|blocked,
-attention_dispatch.py:203-260).  An explicit ``hip`` is never silently
+``hip`` when the library is loaded, a ROCm device is visible and the operands
+are ROCm tensors in fp32/bf16; otherwise they stay ``eager`` (the reference
+switched to triton|blocked, attention_dispatch.py:203-260, and never to a
+backend that raises).  An explicit ``hip`` is never silently
 replaced: a missing library or CPU tensors raise ``RuntimeError``.
 
 ``hip`` with gradients: when autograd needs gradients of Q or V, ``bdh_attn``
@@ -120,27 +121,50 @@ def attn_auto_cold_threshold() -> int:
     return attn_auto_threshold() if _ATTN_AUTO_COLD_THR is None else _ATTN_AUTO_COLD_THR
 
 
-def _resolve_auto_impl(length: int, threshold: int) -> ImplName:
-    """One strict AUTO gate: above the threshold prefer ``hip`` when it can run."""
+_HIP_DTYPES = (torch.float32, torch.bfloat16)
+
+
+def _hip_can_take(tensors) -> bool:
+    """Whether the HIP library accepts these operands: ROCm device tensors in
+    fp32 or bf16 (``None`` entries are ignored)."""
+    return all(t is None or (t.is_cuda and t.dtype in _HIP_DTYPES) for t in tensors)
+
+
+def _resolve_auto_impl(length: int, threshold: int, tensors=None) -> ImplName:
+    """One strict AUTO gate: above the threshold prefer ``hip`` when it can run.
+
+    Like the reference's switch (attention_dispatch.py:203-260), AUTO never
+    picks a backend that would raise: with operands given, ``hip`` is chosen
+    only when they are ROCm tensors in fp32/bf16; CPU tensors, other dtypes,
+    a missing library or no device keep ``eager``.
+    """
     if int(length) <= int(threshold):
         return "eager"
-    return "hip" if hip_attn.hip_available() else "eager"
+    if not hip_attn.hip_available():
+        return "eager"
+    if tensors is not None and not _hip_can_take(tensors):
+        return "eager"
+    return "hip"
 
 
-def resolve_decode_impl(past_len: int, requested: str | None = None) -> ImplName:
-    """T=1 decode backend with the optional AUTO switch (reference :210-231)."""
+def resolve_decode_impl(past_len: int, requested: str | None = None, *, tensors=None) -> ImplName:
+    """T=1 decode backend with the optional AUTO switch (reference :210-231).
+
+    ``tensors`` (the operands) lets AUTO keep ``eager`` for inputs the HIP
+    library does not take; an explicit ``hip`` is returned as requested.
+    """
     name = resolve_attn_impl(requested)
     if name != "eager" or not attn_auto_enabled():
         return name
-    return _resolve_auto_impl(past_len, attn_auto_threshold())
+    return _resolve_auto_impl(past_len, attn_auto_threshold(), tensors)
 
 
-def resolve_cold_impl(seq_len: int, requested: str | None = None) -> ImplName:
+def resolve_cold_impl(seq_len: int, requested: str | None = None, *, tensors=None) -> ImplName:
     """Cold/prefill backend with the optional AUTO switch (reference :234-260)."""
     name = resolve_attn_impl(requested)
     if name != "eager" or not attn_auto_enabled():
         return name
-    return _resolve_auto_impl(seq_len, attn_auto_cold_threshold())
+    return _resolve_auto_impl(seq_len, attn_auto_cold_threshold(), tensors)
 
 
 def _needs_grad(*ts: torch.Tensor) -> bool:
@@ -156,7 +180,7 @@ def bdh_attn(
     use_autograd_fn: Optional[bool] = None,
 ) -> torch.Tensor:
     """``tril(Q @ K.T, -1) @ V`` with the selected backend (reference :263-308)."""
-    name = resolve_cold_impl(int(Q.size(2)), requested=impl)
+    name = resolve_cold_impl(int(Q.size(2)), requested=impl, tensors=(Q, K, V))
     if use_autograd_fn is None:
         use_autograd_fn = _env_autograd_enabled()
     if name == "hip" and not use_autograd_fn and _needs_grad(Q, K, V):
@@ -184,7 +208,7 @@ def bdh_attn_rope(
     the kernel's operand loads (and can write ``R(x)`` into ``out_kr``, the KR
     cache slot); ``eager`` does the same two steps with torch ops.
     """
-    name = resolve_cold_impl(int(x.size(2)), requested=impl)
+    name = resolve_cold_impl(int(x.size(2)), requested=impl, tensors=(x, V, freqs))
     if name == "hip":
         if _needs_grad(x, V):
             if out_kr is not None:
@@ -212,7 +236,7 @@ def bdh_attn_past(
     reach a new row; ``eager`` recomputes past||new with torch ops as the
     reference does.  Inference only under ``hip`` (no autograd).
     """
-    name = resolve_cold_impl(int(K.size(2)), requested=impl)
+    name = resolve_cold_impl(int(K.size(2)), requested=impl, tensors=(Q, K, V))
     if name == "eager":
         return eager_past_attn(Q, K, V, int(past))
     if _needs_grad(Q, K, V):
@@ -230,7 +254,7 @@ def bdh_attn_decode(
 ) -> torch.Tensor:
     """Queries against the packed past only (reference :311-347); never T x T."""
     del block_size  # tiling is internal to the HIP kernel
-    name = resolve_decode_impl(int(K_past.size(2)), requested=impl)
+    name = resolve_decode_impl(int(K_past.size(2)), requested=impl, tensors=(Q, K_past, V_past))
     if name == "eager":
         return eager_decode_attn(Q, K_past, V_past)
     return hip_attn.tril_decode(Q, K_past, V_past)

@@ -227,11 +227,6 @@ def check_pair_freqs(freqs: torch.Tensor) -> None:
     _PAIR_CHECKED[key] = True
 
 
-def pick_hip_cold_tiles(T: int) -> Tuple[int, int]:
-    """Tile edge used by the HIP cold kernels (128 x 128 output tiles)."""
-    return 128, 128
-
-
 def ext_status() -> str:
     """Human-readable status (reference kernels/cuda_attn.py:505-513)."""
     if _ext is None:
@@ -256,7 +251,6 @@ __all__ = [
     "tril_score_v_bwd",
     "tril_rope_score_v_bwd",
     "check_pair_freqs",
-    "pick_hip_cold_tiles",
     "ext_status",
     "_check_cold_shapes",
     "_check_decode_shapes",

@@ -29,27 +29,38 @@ from .rope import (
 ImplName = Literal["eager", "hip"]
 _VALID = ("eager", "hip")
 
-_ROPE_IMPL_ENV: object | None = object()
-_ROPE_IMPL_RESOLVED: ImplName = "eager"
+
+def _parse_rope_impl(raw: str | None) -> ImplName:
+    name = (raw or "eager").strip().lower()
+    if name not in _VALID:
+        raise ValueError(f"BDH_ROPE_IMPL must be {'|'.join(_VALID)}, got {name!r}")
+    return name  # type: ignore[return-value]
+
+
+class _EnvChoice:
+    """``BDH_ROPE_IMPL`` parsed once per distinct raw value of the variable."""
+
+    def __init__(self) -> None:
+        self.raw: str | None = None
+        self.value: ImplName | None = None
+
+    def get(self) -> ImplName:
+        raw = os.environ.get("BDH_ROPE_IMPL", "eager")
+        if self.value is None or raw != self.raw:
+            self.value = _parse_rope_impl(raw)  # raises before the cache is touched
+            self.raw = raw
+        return self.value
+
+
+_rope_env = _EnvChoice()
 
 
 def resolve_rope_impl(requested: str | None = None) -> ImplName:
-    """Resolve ``BDH_ROPE_IMPL`` (or an explicit override); the env string is cached."""
-    global _ROPE_IMPL_ENV, _ROPE_IMPL_RESOLVED
+    """Backend for RoPE apply: ``requested`` if given, else ``BDH_ROPE_IMPL``
+    (default ``eager``).  Unknown names raise ``ValueError``."""
     if requested is not None:
-        raw = (requested or "eager").strip().lower()
-        if raw not in _VALID:
-            raise ValueError(f"BDH_ROPE_IMPL must be {'|'.join(_VALID)}, got {raw!r}")
-        return raw  # type: ignore[return-value]
-    env = os.environ.get("BDH_ROPE_IMPL", "eager")
-    if env is _ROPE_IMPL_ENV or env == _ROPE_IMPL_ENV:
-        return _ROPE_IMPL_RESOLVED
-    raw = (env or "eager").strip().lower()
-    if raw not in _VALID:
-        raise ValueError(f"BDH_ROPE_IMPL must be {'|'.join(_VALID)}, got {raw!r}")
-    _ROPE_IMPL_ENV = env
-    _ROPE_IMPL_RESOLVED = raw  # type: ignore[assignment]
-    return _ROPE_IMPL_RESOLVED
+        return _parse_rope_impl(requested)
+    return _rope_env.get()
 
 
 def bdh_rope_rotate(

@@ -224,7 +224,9 @@ int bdh_gated_gemm(const bdh_tensor4* y, const bdh_tensor4* wt, const bdh_tensor
  * For the decoder product of a decode step (bdh.py:927-945, `_mlp_merge`'s
  * F.linear with M = batch rows, K = nh*N, D = n_embd), where a library GEMM
  * walks the whole K with a few tiles.  out is bf16 or fp32.  The workspace
- * holds the fp32 partial sums of the K splits.
+ * holds the fp32 partial sums of the K splits: it must be 4-byte aligned
+ * (else BDH_ERR_WORKSPACE); a 16-byte aligned one takes the vectorized split
+ * reduction.
  */
 size_t bdh_small_gemm_workspace(int64_t M, int64_t K, int64_t D);
 int bdh_small_gemm(const bdh_tensor4* a, const bdh_tensor4* b, const bdh_tensor4* out,

@@ -1,8 +1,8 @@
 """Write ``fixtures.npz``: seeded inputs and CPU-oracle outputs at small shapes.
 
-The fixtures pin the oracle against regressions (tests/test_golden.py
-recomputes them) and give the GPU tests reference outputs that do not depend
-on running the oracle.  Inputs follow the BASELINE seeds: latent
+The fixtures pin the oracle against regressions
+(tests/test_surface.py::test_golden_fixtures_reproduce recomputes them) and
+give the GPU tests reference outputs that do not depend on running the oracle.  Inputs follow the BASELINE seeds: latent
 Q = relu(0.32 * N(0,1)) (seed 0), V ~ N(0,1) (seed 1), dY ~ N(0,1) (seed 2).
 
 Run from the repo root:  ``python tests/golden/make_fixtures.py``

@@ -73,7 +73,8 @@ def test_self_backward_permuted_view_fp32_out():
 
 def test_self_backward_c4_properties():
     """C4 at full size: dQ and dV are linear in dO, and doubling is exact in
-    bf16 and fp32, so the bits must match; slab (0, 0) against the oracle."""
+    bf16 and fp32, so the bits must match; batch element 0 (all four heads:
+    dV sums over them) against the oracle for both dQ and dV."""
     B, H, T, N, D = 16, 4, 1024, 8192, 256
     g = torch.Generator(device=DEV).manual_seed(0)
     q = torch.relu(0.32 * torch.randn(B, H, T, N, generator=g, device=DEV)).to(BF)
@@ -84,9 +85,11 @@ def test_self_backward_c4_properties():
     assert torch.equal(dq2, dq1 * 2)
     assert torch.equal(dv2, dv1 * 2)
     assert torch.isfinite(dq1).all().item()
-    # slab (0, 0): its gradient depends only on q[0,0], v[0], dO[0,0] for dQ
-    wq, _ = O.self_attn_backward(np_of(q[:1, :1]), np_of(v[:1]), np_of(d[:1, :1]))
-    assert rel_fro(np_of(dq1[:1, :1]), wq) <= TOL[BF]
+    # batch element 0 depends only on q[0], v[0], dO[0]
+    wq, wv = O.self_attn_backward(np_of(q[:1]), np_of(v[:1]), np_of(d[:1]))
+    eq, ev = rel_fro(np_of(dq1[:1]), wq), rel_fro(np_of(dv1[:1]), wv)
+    print(f"C4 batch 0: dQ rel {eq:.3e}, dV rel {ev:.3e}", flush=True)
+    assert eq <= TOL[BF] and ev <= TOL[BF]
 
 
 @pytest.mark.parametrize("shape", SHAPES)

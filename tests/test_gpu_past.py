@@ -90,8 +90,8 @@ def test_past_on_capacity_strided_cache_and_fp32_v(dtype):
 
 def test_past_c1_chunk_matches_full_recompute_bf16():
     """A C1-width chunk (N = 8192, D = 256): the last 256 rows of a 1024-row
-    sequence equal the same rows of the full cold op on the GPU (itself checked
-    against the oracle), the reference's recompute-and-slice."""
+    sequence against the oracle, and against the same rows of the full cold op
+    on the GPU (the reference's recompute-and-slice)."""
     B, H, T, past, N, D = 1, 4, 256, 768, 8192, 256
     g = torch.Generator(device=DEV).manual_seed(5)
     k = torch.relu(0.32 * torch.randn(B, H, past + T, N, generator=g, device=DEV)).to(torch.bfloat16)
@@ -99,6 +99,11 @@ def test_past_c1_chunk_matches_full_recompute_bf16():
     got = ext.tril_score_v_past(k[:, :, past:], k, v, past)
     full = ext.tril_score_v(k, k, v)[:, :, past:]
     assert rel_fro(np_of(got), np_of(full)) <= TOL[torch.bfloat16]
+    kk = np_of(k)
+    want = O.tril_score_v_past(kk[:, :, past:], kk, np_of(v), past)
+    err = rel_fro(np_of(got), want)
+    print(f"C1-width chunk past={past}: rel {err:.3e}", flush=True)
+    assert err <= TOL[torch.bfloat16]
 
 
 def test_past_dispatch_and_errors():

@@ -153,6 +153,64 @@ def test_auto_thresholds_contract(K, monkeypatch):
     assert K.resolve_decode_impl(513) == ("hip" if torch.cuda.is_available() else "eager")
 
 
+def test_auto_keeps_eager_for_operands_hip_cannot_take(K, monkeypatch):
+    """AUTO never switches to a backend that would raise: with the library and a
+    device reported present, CPU tensors (or float64) above the threshold still
+    take the eager path and return its result (reference AUTO falls back to a
+    working path, attention_dispatch.py:203-260)."""
+    from kernels import attention_dispatch as d, hip_attn
+
+    monkeypatch.setattr(hip_attn, "hip_available", lambda: True)
+    monkeypatch.setenv("BDH_ATTN_AUTO", "1")
+    monkeypatch.setenv("BDH_ATTN_AUTO_THRESHOLD", "4")
+    g = torch.Generator().manual_seed(0)
+    q = torch.relu(0.32 * torch.randn(1, 2, 9, 8, generator=g))
+    v = torch.randn(1, 1, 9, 5, generator=g)
+    assert d.resolve_cold_impl(9, tensors=(q, q, v)) == "eager"
+    assert d.resolve_cold_impl(9) == "hip"  # no operands given: library and device decide
+    assert d.resolve_decode_impl(9, tensors=(q[:, :, :1], q, v)) == "eager"
+    want = K.bdh_attn(q, q, v, impl="eager")
+    assert torch.equal(K.bdh_attn(q, q, v), want)
+    assert torch.equal(K.bdh_attn_decode(q[:, :, -1:], q, v), K.bdh_attn_decode(q[:, :, -1:], q, v, impl="eager"))
+    assert torch.equal(K.bdh_attn_past(q[:, :, 4:], q, v, 4), K.bdh_attn_past(q[:, :, 4:], q, v, 4, impl="eager"))
+    f = K.get_freqs(8)
+    assert torch.equal(K.bdh_attn_rope(q, v, f, 0), K.bdh_attn_rope(q, v, f, 0, impl="eager"))
+    q64 = q.double()
+    assert d.resolve_cold_impl(9, tensors=(q64, q64, v.double())) == "eager"
+    # an explicit hip is never replaced
+    with pytest.raises(RuntimeError):
+        K.bdh_attn(q, q, v, impl="hip")
+
+
+def test_native_module_name_of_the_reference_dispatches_by_device():
+    """``bdh_cuda_ext`` (the import name of reference kernels/cuda_attn.py:84-88)
+    reports has_cuda and runs CPU tensors through its torch CPU entries, which
+    reproduce the reference's known answers exactly and accumulate 16-bit inputs
+    in fp32 (tril_attn_bind.cpp:29,32)."""
+    import bdh_cuda_ext as ce
+    import bdh_hip_ext as ext
+
+    assert ce.has_cuda is True and ce.has_hip is True and ce.lib_path == ext.lib_path
+    ka = json.loads((GOLDEN / "known_answers.json").read_text())
+    c = ka["raw_tril_fwd_bwd"]
+    q, k, v = (torch.tensor(c[n]) for n in ("q", "k", "v"))
+    assert torch.equal(ce.tril_score_v(q, k, v), torch.tensor(c["out"]))
+    assert torch.equal(ext.tril_score_v_cpu(q, k, v), torch.tensor(c["out"]))
+    d = ka["decode_raw"]
+    qd, kd, vd = (torch.tensor(d[n]) for n in ("q", "k_past", "v_past"))
+    assert torch.equal(ce.tril_decode(qd, kd, vd), torch.tensor(d["out"]))
+    g = torch.Generator().manual_seed(3)
+    x = torch.relu(0.32 * torch.randn(2, 2, 40, 32, generator=g))
+    vv = torch.randn(2, 1, 40, 16, generator=g)
+    want = O.tril_score_v_cpu(O.bf16_round(x.numpy()), O.bf16_round(x.numpy()), O.bf16_round(vv.numpy()))
+    got = ce.tril_score_v(x.bfloat16(), x.bfloat16(), vv.bfloat16())
+    assert got.dtype == torch.bfloat16
+    # fp32 accumulation: only the final rounding to bf16 separates it from the fp32 oracle
+    assert float(np.abs(got.float().numpy() - want).max() / np.abs(want).max()) < 2 ** -8
+    with pytest.raises(RuntimeError, match="CPU"):
+        ext.tril_score_v_cpu(x.to("meta"), x.to("meta"), vv.to("meta"))
+
+
 def test_eager_paths_match_oracle_and_known_answers(K):
     ka = json.loads((GOLDEN / "known_answers.json").read_text())
     c = ka["raw_tril_fwd_bwd"]
