@@ -37,6 +37,7 @@ __all__ = [
     "tril_decode",
     "tril_decode_hip",
     "tril_decode_cpu",
+    "tril_decode_noalloc",
     "tril_score_v_bwd",
     "keeps_scores",
     "tril_score_v_save",
@@ -66,6 +67,7 @@ EXPORTED_SYMBOLS = (
     "bdh_tril_rope_score_v",
     "bdh_tril_decode_workspace",
     "bdh_tril_decode",
+    "bdh_tril_decode_noalloc",
     "bdh_rope_rotate",
     "bdh_tril_score_v_bwd_workspace",
     "bdh_tril_score_v_bwd",
@@ -125,6 +127,7 @@ def _load():
         "bdh_tril_rope_score_v": (ctypes.c_int, [P, P, P, fp, i64, P, vp, sz, vp]),
         "bdh_tril_decode_workspace": (sz, [i64, i64, i64, i64, i64, i64]),
         "bdh_tril_decode": (ctypes.c_int, [P, P, P, P, vp, sz, vp]),
+        "bdh_tril_decode_noalloc": (ctypes.c_int, [P, P, P, P, vp]),
         "bdh_rope_rotate": (ctypes.c_int, [P, P, P, P, i32, vp]),
         "bdh_tril_score_v_bwd_workspace": (sz, [i64, i64, i64, i64, i64, i64, i32]),
         "bdh_tril_score_v_bwd": (ctypes.c_int, [P, P, P, P, P, P, P, vp, sz, vp]),
@@ -383,6 +386,26 @@ def tril_decode(q: torch.Tensor, k_past: torch.Tensor, v_past: torch.Tensor) -> 
 
 
 tril_decode_hip = tril_decode
+
+
+def tril_decode_noalloc(
+    q: torch.Tensor, k_past: torch.Tensor, v_past: torch.Tensor, out: Optional[torch.Tensor] = None
+) -> torch.Tensor:
+    """Decode through ``bdh_tril_decode_noalloc``: no workspace; the partial sums
+    go to the library's per-GPU scratch array, so calls that overlap in time on
+    one GPU race.  ``out`` (B, H, Tq, Dv) defaults to a fresh tensor in q's dtype
+    (the entry point itself allocates nothing)."""
+    dev = _require_device(q, k_past, v_past, out)
+    B, H, Tq, _ = q.shape
+    if out is None:
+        out = torch.empty(B, H, Tq, v_past.size(-1), dtype=q.dtype, device=dev)
+    with torch.cuda.device(dev):
+        rc = _lib.bdh_tril_decode_noalloc(
+            ctypes.byref(_t4(q)), ctypes.byref(_t4(k_past)), ctypes.byref(_t4(v_past)), ctypes.byref(_t4(out)),
+            _stream(dev),
+        )
+    _check(rc, "tril_decode_noalloc")
+    return out
 
 
 # ------------------------------------------------------------------ backward

@@ -57,6 +57,7 @@ extern "C" const char* bdh_error_string(int code) {
     case BDH_ERR_LAUNCH: return "HIP kernel launch failed";
     case BDH_ERR_ARG: return "invalid argument";
     case BDH_ERR_ALIAS: return "output overlaps an input";
+    case BDH_ERR_SCRATCH: return "input needs more scratch than the no-allocation entry point holds";
     default: return "unknown error";
   }
 }

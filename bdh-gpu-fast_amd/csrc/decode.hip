@@ -11,6 +11,8 @@
 // elements per 512-element stride), reduces the dot product across the wave
 // with shuffles, and records the score in LDS; then all 256 threads form the
 // partial out[d] = sum_s score_s V[s,d] with coalesced V row reads.
+#include <mutex>
+
 #include "common.h"
 
 namespace bdh {
@@ -213,16 +215,27 @@ extern "C" size_t bdh_tril_decode_workspace(int64_t B, int64_t H, int64_t Tq, in
   return size_t(n_chunks(S)) * size_t(B * H * Tq) * size_t(Dv) * sizeof(float);
 }
 
-extern "C" int bdh_tril_decode(const bdh_tensor4* q, const bdh_tensor4* k, const bdh_tensor4* v,
-                               const bdh_tensor4* out, void* workspace, size_t workspace_bytes,
-                               bdh_stream stream) {
+namespace bdh {
+namespace {
+
+// Shape/dtype contract of decode (kernels/cuda_attn.py:114-131,
+// csrc/tril_attn_cpu.cpp:214-223) and the launch plan: part_bytes is the
+// partial-sum storage the chosen kernels need.
+struct DecodePlan {
+  DecodeArgs a;
+  bool fast = false;
+  int64_t nred = 0;
+  size_t part_bytes = 0;
+};
+
+int decode_plan(const bdh_tensor4* q, const bdh_tensor4* k, const bdh_tensor4* v, const bdh_tensor4* out,
+                DecodePlan& p) {
   BDH_TRY(check_view(q));
   BDH_TRY(check_view(k));
   BDH_TRY(check_view(v));
   BDH_TRY(check_view(out));
   const int64_t B = q->size[0], H = q->size[1], Tq = q->size[2], Dk = q->size[3];
   const int64_t S = k->size[2], Dv = v->size[3];
-  // Contract of kernels/cuda_attn.py:114-131 / csrc/tril_attn_cpu.cpp:214-223.
   if (k->size[0] != B || k->size[1] != H || k->size[3] != Dk) return BDH_ERR_SHAPE;
   if (v->size[0] != B || v->size[2] != S) return BDH_ERR_SHAPE;
   if (v->size[1] != 1 && v->size[1] != H) return BDH_ERR_SHAPE;
@@ -231,13 +244,7 @@ extern "C" int bdh_tril_decode(const bdh_tensor4* q, const bdh_tensor4* k, const
   if (views_overlap(out, q) || views_overlap(out, k) || views_overlap(out, v)) return BDH_ERR_ALIAS;
   if (B * H * Tq > 65535 || n_chunks(S) > int64_t(1) << 30) return BDH_ERR_SHAPE;
   if ((Dk + kChunk) * int64_t(sizeof(float)) > 64 * 1024) return BDH_ERR_SHAPE;
-  if (numel4(out) == 0) return BDH_OK;
-  const int64_t nchunk = n_chunks(S);
-  const size_t need = bdh_tril_decode_workspace(B, H, Tq, S, Dk, Dv);
-  if (workspace == nullptr || workspace_bytes < need) return BDH_ERR_WORKSPACE;
-  hipStream_t st = static_cast<hipStream_t>(stream);
-
-  DecodeArgs a;
+  DecodeArgs& a = p.a;
   a.q = view_of(q);
   a.q.s1 = q->stride[1];
   a.k = view_of(k);
@@ -250,36 +257,97 @@ extern "C" int bdh_tril_decode(const bdh_tensor4* q, const bdh_tensor4* k, const
   a.Dv = Dv;
   a.Hv = v->size[1];
   a.vec_k = vec16_ok(k) ? 1 : 0;
-  a.part = static_cast<float*>(workspace);
+  a.part = nullptr;
   a.rows = B * H * Tq;
-  // bf16 cache path: fewer, larger key chunks (the workspace for kChunk-key
-  // chunks covers them)
-  const bool fast = q->dtype == BDH_BF16 && k->dtype == BDH_BF16 && vec16_ok(q) && vec16_ok(k) &&
-                    Dk % 2048 == 0 && Dk * 2 + kDecChunkB * 4 <= 64 * 1024 && S > 0;
-  int64_t nred = nchunk;
-  if (fast) {
-    nred = (S + kDecChunkB - 1) / kDecChunkB;
-    const dim3 grid((unsigned)nred, unsigned(a.rows));
-    const size_t shm = size_t(kDecChunkB) * sizeof(float) + size_t(Dk) * 2;
+  // bf16 cache path: fewer, larger key chunks
+  p.fast = q->dtype == BDH_BF16 && k->dtype == BDH_BF16 && vec16_ok(q) && vec16_ok(k) && Dk % 2048 == 0 &&
+           Dk * 2 + kDecChunkB * 4 <= 64 * 1024 && S > 0;
+  p.nred = p.fast ? (S + kDecChunkB - 1) / kDecChunkB : n_chunks(S);
+  p.part_bytes = size_t(p.nred) * size_t(a.rows) * size_t(Dv) * sizeof(float);
+  return BDH_OK;
+}
+
+// The partial kernels write every (chunk, row, column) of part, so part needs
+// no clearing between calls.
+int decode_run(const DecodePlan& p, const bdh_tensor4* q, const bdh_tensor4* k, const bdh_tensor4* v,
+               const bdh_tensor4* out, float* part, hipStream_t st) {
+  DecodeArgs a = p.a;
+  a.part = part;
+  if (p.fast) {
+    const dim3 grid((unsigned)p.nred, unsigned(a.rows));
+    const size_t shm = size_t(kDecChunkB) * sizeof(float) + size_t(a.Dk) * 2;
     if (v->dtype == BDH_BF16)
       BDH_LAUNCH("k_decode_bf16", k_decode_bf16<bf16_t>, grid, dim3(kDecNT), shm, st, a);
     else
       BDH_LAUNCH("k_decode_bf16", k_decode_bf16<float>, grid, dim3(kDecNT), shm, st, a);
   } else {
-    const int rc = q->dtype == BDH_BF16 ? pick_k<bf16_t>(a, nchunk, k->dtype, v->dtype, st)
-                                        : pick_k<float>(a, nchunk, k->dtype, v->dtype, st);
+    const int rc = q->dtype == BDH_BF16 ? pick_k<bf16_t>(a, p.nred, k->dtype, v->dtype, st)
+                                        : pick_k<float>(a, p.nred, k->dtype, v->dtype, st);
     if (rc != BDH_OK) return rc;
   }
-
   View o = view_of(out);
   o.s1 = out->stride[1];
-  const int64_t total = a.rows * Dv;
+  const int64_t total = a.rows * a.Dv;
   dim3 grid((unsigned)((total + kDecNT - 1) / kDecNT));
   if (out->dtype == BDH_BF16)
-    BDH_LAUNCH("k_decode_reduce", k_decode_reduce<bf16_t>, grid, dim3(kDecNT), 0, st, a.part, nred,
-               a.rows, Dv, o, H, Tq);
+    BDH_LAUNCH("k_decode_reduce", k_decode_reduce<bf16_t>, grid, dim3(kDecNT), 0, st, a.part, p.nred, a.rows,
+               a.Dv, o, a.H, a.Tq);
   else
-    BDH_LAUNCH("k_decode_reduce", k_decode_reduce<float>, grid, dim3(kDecNT), 0, st, a.part, nred,
-               a.rows, Dv, o, H, Tq);
+    BDH_LAUNCH("k_decode_reduce", k_decode_reduce<float>, grid, dim3(kDecNT), 0, st, a.part, p.nred, a.rows,
+               a.Dv, o, a.H, a.Tq);
   return BDH_OK;
+}
+
+}  // namespace
+}  // namespace bdh
+
+extern "C" int bdh_tril_decode(const bdh_tensor4* q, const bdh_tensor4* k, const bdh_tensor4* v,
+                               const bdh_tensor4* out, void* workspace, size_t workspace_bytes,
+                               bdh_stream stream) {
+  DecodePlan p;
+  BDH_TRY(decode_plan(q, k, v, out, p));
+  if (numel4(out) == 0) return BDH_OK;
+  const size_t need = bdh_tril_decode_workspace(q->size[0], q->size[1], q->size[2], k->size[2], q->size[3],
+                                                v->size[3]);
+  if (workspace == nullptr || workspace_bytes < need) return BDH_ERR_WORKSPACE;
+  return decode_run(p, q, k, v, out, static_cast<float*>(workspace), static_cast<hipStream_t>(stream));
+}
+
+// ------------------------------------------------------- no allocation
+// The partial sums of bdh_tril_decode_noalloc live in this library-owned
+// array: every GPU the library runs on holds its own copy (allocated when the
+// code object loads on that device, kept until the process ends).  In host
+// code `scratch` only names the symbol; its device address comes from
+// hipGetSymbolAddress with the device current, once per device.
+static __device__ __align__(256) uint8_t scratch[BDH_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of the current device's scratch array (looked up on the
+// first call on that device), or nullptr when the lookup fails.
+void* scratch_of_current_device() {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || ptr == nullptr) return nullptr;
+    g_scratch_ptr[dev] = ptr;
+  }
+  return g_scratch_ptr[dev];
+}
+}  // namespace
+
+extern "C" int bdh_tril_decode_noalloc(const bdh_tensor4* q, const bdh_tensor4* k, const bdh_tensor4* v,
+                                       const bdh_tensor4* out, bdh_stream stream) {
+  DecodePlan p;
+  BDH_TRY(decode_plan(q, k, v, out, p));
+  if (numel4(out) == 0) return BDH_OK;
+  if (p.part_bytes > size_t(BDH_NOALLOC_SCRATCH_BYTES)) return BDH_ERR_SCRATCH;
+  void* part = scratch_of_current_device();
+  if (part == nullptr) return BDH_ERR_LAUNCH;
+  return decode_run(p, q, k, v, out, static_cast<float*>(part), static_cast<hipStream_t>(stream));
 }

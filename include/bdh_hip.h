@@ -41,7 +41,8 @@ enum {
   BDH_ERR_WORKSPACE = 4, /* workspace missing or smaller than required     */
   BDH_ERR_LAUNCH = 5,    /* the HIP runtime rejected a kernel launch       */
   BDH_ERR_ARG = 6,       /* other invalid argument (NULL pointer, range)   */
-  BDH_ERR_ALIAS = 7      /* an output overlaps an input it must not alias  */
+  BDH_ERR_ALIAS = 7,     /* an output overlaps an input it must not alias  */
+  BDH_ERR_SCRATCH = 8    /* larger than the no-allocation scratch holds    */
 };
 
 typedef struct bdh_tensor4 {
@@ -119,6 +120,25 @@ size_t bdh_tril_decode_workspace(int64_t B, int64_t H, int64_t Tq, int64_t S,
 int bdh_tril_decode(const bdh_tensor4* q, const bdh_tensor4* k_past,
                     const bdh_tensor4* v_past, const bdh_tensor4* out,
                     void* workspace, size_t workspace_bytes, bdh_stream stream);
+
+/*
+ * Decode that allocates nothing and takes no workspace.  It has no
+ * counterpart in the reference: it is for callers that cannot call hipMalloc
+ * or hand in a workspace (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid allocation).  Same operands, kernels and results as
+ * bdh_tril_decode.  The partial sums go to a library-owned device array of
+ * BDH_NOALLOC_SCRATCH_BYTES per GPU (each GPU the library runs on holds one
+ * until the process ends); inputs whose partials exceed it (B*H*Tq * Dv * 4
+ * bytes per 64 past keys on the bf16 path, per 32 otherwise; C3's B*H = 256,
+ * Dv = 256 fits S <= 4096) return BDH_ERR_SCRATCH.  The current device must be
+ * the tensors' device.  Every call on one GPU shares that GPU's array: calls
+ * that overlap in time on one GPU (other streams, other threads) race and must
+ * be serialised by the caller.
+ */
+#define BDH_NOALLOC_SCRATCH_BYTES (16u << 20)
+int bdh_tril_decode_noalloc(const bdh_tensor4* q, const bdh_tensor4* k_past,
+                            const bdh_tensor4* v_past, const bdh_tensor4* out,
+                            bdh_stream stream);
 
 /*
  * RoPE apply: out = rotate(v, cos, sin) over adjacent pairs.
