@@ -300,6 +300,57 @@ constexpr bool sy_rot_conj(int wt, int u) { return REL && (wt == 0 ? u >= 2 : (u
 template <bool REL>
 constexpr int sy_rot_tidx(int wt, int u) { return !REL ? u : (wt == 0 ? ((u == 1 || u == 2) ? 1 : 0) : 0); }
 
+// Partial score tiles are stored in MFMA fragment order: a tile's 32 x 32
+// block held by wave slot ws (the wave, or wave & 3 on diagonal tiles) as its
+// m-th accumulator is fragment slot k = ws * nm + m (nm = 8 full, 9
+// diagonal) of 1024 bf16: lane l's 16 values, pairs (2q, 2q + 1) packed into
+// dword q, dwords 0-3 at element 8 l and dwords 4-7 at 512 + 8 l.  Value r of
+// lane l is block element (8 (r / 4) + 4 (l / 32) + r % 4, l % 32).  Each
+// wave writes its 2 KB slots with two 1 KB coalesced stores.
+// sy_slot_of maps a block (rb, cb) of a tile to its slot: the inverse of the
+// epilogue's block mapping (relative RoPE reorders row groups), built at
+// compile time for full tiles and the lower blocks of diagonal tiles.
+struct SySlotTab {
+  uint8_t full[2][64];  // [relative][8 rb + cb]
+  uint8_t diag[2][64];  // [relative][8 rb + cb], rb >= cb
+};
+constexpr SySlotTab sy_make_slots() {
+  SySlotTab t{};
+  for (int rel = 0; rel < 2; ++rel) {
+    for (int ws = 0; ws < 8; ++ws)
+      for (int m = 0; m < 8; ++m) {
+        const int wm = ws >> 2, wn = ws & 3;
+        const int rb = (rel && wm == 1) ? 7 - (m >> 1) : 4 * wm + (m >> 1);
+        const int cb = (rel && wn >= 2) ? 11 - 2 * wn - (m & 1) : 2 * wn + (m & 1);
+        t.full[rel][8 * rb + cb] = uint8_t(ws * 8 + m);
+      }
+    for (int ws = 0; ws < 4; ++ws)
+      for (int m = 0; m < 9; ++m) {
+        int gi = kSyDiag[ws].bi[m], gj = kSyDiag[ws].bj[m];
+        if (rel) {
+          gi = gi < 4 ? gi : 11 - gi;
+          gj = gj < 4 ? gj : 11 - gj;
+        }
+        const int rb = gi > gj ? gi : gj, cb = gi > gj ? gj : gi;
+        t.diag[rel][8 * rb + cb] = uint8_t(ws * 9 + m);
+      }
+  }
+  return t;
+}
+constexpr SySlotTab kSySlots = sy_make_slots();
+// element offset (in a partial tile) of the 16-byte piece `half` of lane l of
+// block (rb, cb)
+__device__ __forceinline__ int sy_piece(bool diag_tile, int rel, int rb, int cb, int l, int half) {
+  const int k = diag_tile ? kSySlots.diag[rel][8 * rb + cb] : kSySlots.full[rel][8 * rb + cb];
+  return k * 1024 + half * 512 + l * 8;
+}
+// rows (in the block) of the eight values of piece `half` of lane l, in
+// order: value 2q' + e is row sy_piece_row(l, half, q', e)
+__device__ __forceinline__ int sy_piece_row(int l, int half, int qq, int e) {
+  const int r = 2 * (4 * half + qq) + e;
+  return 8 * (r >> 2) + 4 * (l >> 5) + (r & 3);
+}
+
 // RM: 0 no RoPE; 1 RoPE at absolute positions (table row t = position
 // rope_start + t); 2 RoPE relative to each tile's centre.  Scores depend only
 // on position differences, so rotating the rows of tile (ta, tb) by their
@@ -724,33 +775,17 @@ __global__ __launch_bounds__(kSyThreads, 1) void k_sy_scores(const SyArgs a) {
       return;
     }
     if (tile_out < 0) return;
-    bf16_t* dst = a.part + ((int64_t(slab) * a.ntl + tile_out) * S + split) * kSyTileElems;
-    // Partial tiles are stored as bf16 (halving their traffic; the scores are
-    // bf16 MFMA operands of the score x V product anyway).  Lane pairs swap one
-    // value so each lane writes two adjacent columns of one row.
-    const bool even = (lane & 1) == 0;
+    // partial tile(s) as bf16 in fragment order (see sy_piece)
+    const int wslot = WT == 0 ? w : (w & 3);
+    bf16_t* dst = a.part + ((int64_t(slab) * a.ntl + tile_out) * S + split) * kSyTileElems + wslot * NM * 1024 +
+                  lane * 8;
     sy_static_for<NM>([&](auto mc) {
       constexpr int m = decltype(mc)::value;
-      int rb, cb;
-      if constexpr (WT == 0) {
-        const int wm = w >> 2, wn = w & 3;
-        rb = (REL && wm == 1) ? 7 - (m >> 1) : 4 * wm + (m >> 1);
-        cb = (REL && wn >= 2) ? 11 - 2 * wn - (m & 1) : 2 * wn + (m & 1);
-      } else {
-        constexpr int gi = REL ? P::grp(P::bi(m)) : P::bi(m);
-        constexpr int gj = REL ? P::grp(P::bj(m)) : P::bj(m);
-        rb = gi > gj ? gi : gj;
-        cb = gi > gj ? gj : gi;
-      }
+      uint32_t pk[8];
 #pragma unroll
-      for (int r = 0; r < 16; r += 2) {
-        const float send = even ? acc[m][r + 1] : acc[m][r];
-        const float recv = __shfl_xor(send, 1, 64);
-        const int row = rb * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3) + (even ? 0 : 1);
-        const int col = cb * 32 + ((lane & 31) & ~1);
-        const uint32_t w2 = even ? pack_bf2(acc[m][r], recv) : pack_bf2(recv, acc[m][r + 1]);
-        *reinterpret_cast<uint32_t*>(dst + row * kSyTile + col) = w2;
-      }
+      for (int r = 0; r < 8; ++r) pk[r] = pack_bf2(acc[m][2 * r], acc[m][2 * r + 1]);
+      *reinterpret_cast<u32x4*>(dst + m * 1024) = u32x4{pk[0], pk[1], pk[2], pk[3]};
+      *reinterpret_cast<u32x4*>(dst + m * 1024 + 512) = u32x4{pk[4], pk[5], pk[6], pk[7]};
     });
   };
   if constexpr (REL) {
@@ -986,23 +1021,30 @@ __global__ __launch_bounds__(256) void k_dv_sy(const DvsArgs a) {
   const int ic0 = j0 / 64, nic = (a.T + 63) / 64;  // chunks of i: i >= j0 (i > j)
   const int tj = j0 >> 8;
 
-  // builder roles: M rows li = tid / 4, 16 columns from lj; dO chunks e = tid + 256 u
-  const int li = tid >> 2, lj = (tid & 3) * 16;
+  // builder roles: M pieces (fragment-ordered partial tiles, see sy_piece):
+  // piece e of this thread is 32 x 32 block mbi = (tid + 256 e) / 128 of the
+  // 64 x 64 (i, j) chunk (rows i: mbi / 2, columns j: mbi % 2), lane
+  // ((tid & 127) >> 1), half tid & 1; dO chunks e = tid + 256 u
+  const int pl = (tid & 127) >> 1, ph = tid & 1;
   uint4 mp[NS][2];
   uint4 dp[8];
   auto load_chunk = [&](int h, int ic) {
     const int i0 = ic * 64;
     const int ti = i0 >> 8;
     const int slab = b * a.H + h;
-    const int gi = i0 + li;
-    const bf16_t* p = a.part + ((int64_t(slab) * a.ntl + ti * (ti + 1) / 2 + tj) * a.nsplit) * kSyTileElems +
-                      (gi & 255) * kSyTile + ((j0 + lj) & 255);
+    const bool dt = ti == tj;
+    const bf16_t* p = a.part + ((int64_t(slab) * a.ntl + ti * (ti + 1) / 2 + tj) * a.nsplit) * kSyTileElems;
 #pragma unroll
-    for (int sp = 0; sp < NS; ++sp)
+    for (int e = 0; e < 2; ++e) {
+      const int mbi = (tid >> 7) + 2 * e;
+      const int rbk = ((i0 & 255) >> 5) + (mbi >> 1), cbk = ((j0 & 255) >> 5) + (mbi & 1);
+      // (no blocks above a diagonal tile's diagonal: read the diagonal block, masked below)
+      const int off = sy_piece(dt, 0, rbk, dt && cbk > rbk ? rbk : cbk, pl, ph);
 #pragma unroll
-      for (int e = 0; e < 2; ++e)
-        mp[sp][e] = sp < a.nsplit ? *reinterpret_cast<const uint4*>(p + int64_t(sp) * kSyTileElems + 8 * e)
+      for (int sp = 0; sp < NS; ++sp)
+        mp[sp][e] = sp < a.nsplit ? *reinterpret_cast<const uint4*>(p + int64_t(sp) * kSyTileElems + off)
                                   : uint4{0u, 0u, 0u, 0u};
+    }
     const bf16_t* dob = a.dO + b * a.d0 + h * a.d1;
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
@@ -1013,7 +1055,6 @@ __global__ __launch_bounds__(256) void k_dv_sy(const DvsArgs a) {
     }
   };
   auto store_chunk = [&](int ic) {
-    const int gi = ic * 64 + li;
 #pragma unroll
     for (int e = 0; e < 2; ++e) {
       float sacc[8];
@@ -1028,16 +1069,16 @@ __global__ __launch_bounds__(256) void k_dv_sy(const DvsArgs a) {
           sacc[2 * q + 1] += __uint_as_float(xw[q] & 0xffff0000u);
         }
       }
-      uint32_t pk[4];
+      const int mbi = (tid >> 7) + 2 * e;
+      const int lj = (mbi & 1) * 32 + (pl & 31), gj = j0 + lj;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int gj = j0 + lj + 8 * e + 2 * q;
-        const float lo = (gi < a.T && gi > gj) ? sacc[2 * q] : 0.f;
-        const float hi = (gi < a.T && gi > gj + 1) ? sacc[2 * q + 1] : 0.f;
-        pk[q] = pack_bf2(lo, hi);
-      }
-      const int c = (lj >> 3) + e;
-      *reinterpret_cast<u32x4*>(mblk + li * 128 + ((c ^ (2 * (li & 3))) * 16)) = u32x4{pk[0], pk[1], pk[2], pk[3]};
+      for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const int li = (mbi >> 1) * 32 + sy_piece_row(pl, ph, q, u), gi = ic * 64 + li;
+          const float val = (gi < a.T && gi > gj) ? sacc[2 * q + u] : 0.f;
+          *reinterpret_cast<bf16_t*>(mblk + li * 128 + (((lj >> 3) ^ (2 * (li & 3))) * 16) + (lj & 7) * 2) = f2bf(val);
+        }
     }
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
@@ -1125,6 +1166,8 @@ struct SvArgs {
   int t0 = 0;          // packed index of the first stored tile
   int rb0 = 0;         // first 64-row block (queries at an offset)
   int past = 0;        // rows below past are not stored; row i is stored at i - past
+  int rel = 0;         // the tiles came from the relative-RoPE score kernel (fragment slot order)
+  int self = 1;        // Q = K: diagonal tiles hold their 36 lower blocks (else every tile is full)
 };
 
 template <typename TO, typename TV, int NS>
@@ -1151,12 +1194,12 @@ __global__ __launch_bounds__(512, 1) void k_sy_sv(const SvArgs a) {
   const bf16_t* pslab = a.part + int64_t(slab) * a.ntl * a.nsplit * kSyTileElems;
   const TV* vb = static_cast<const TV*>(a.v.p) + b * a.v.s0 + hv * a.v.s1;
 
-  // block builder: row lr, keys [lk, +8) of the chunk; V rows vr0 + 16 u,
-  // 16-byte chunk vc of each (u = 0..3)
-  const int lr = tid >> 3, lk = (tid & 7) * 8;
-  const int gi = r0 + lr;
-  const int ti = min(gi, a.T - 1) >> 8;
-  const bool row_ok = gi < a.T;
+  // block builder: one 16-byte piece of the fragment-ordered partial tiles
+  // per split: 32 x 32 block sbi = (rows srh, keys skh) of the 64 x 64 chunk,
+  // lane pl, half ph (8 values of one key column); V rows vr0 + 16 u, 16-byte
+  // chunk vc of each (u = 0..3)
+  const int sbi = tid >> 7, srh = sbi >> 1, skh = sbi & 1, pl = (tid & 127) >> 1, ph = tid & 1;
+  const int ti = r0 >> 8;  // the tile row of all rows of this block (64 | 256)
   const int vr0 = tid >> 5, vc = tid & 31;
   // Loads are unconditional, from clamped addresses: splits past nsplit
   // re-read the last split (not summed), V rows past T re-read row T - 1 (their
@@ -1172,8 +1215,14 @@ __global__ __launch_bounds__(512, 1) void k_sy_sv(const SvArgs a) {
   auto load_chunk = [&](int ck, auto slotc) __attribute__((always_inline)) {
     constexpr int k = decltype(slotc)::value;
     const int j0 = ck * 64;
-    const int tile = ti * (ti + 1) / 2 + (j0 >> 8) - a.t0;
-    const bf16_t* p = pslab + int64_t(tile) * a.nsplit * kSyTileElems + (gi & 255) * kSyTile + ((j0 + lk) & 255);
+    const int tj = j0 >> 8;
+    const int tile = ti * (ti + 1) / 2 + tj - a.t0;
+    const int rbk = ((r0 & 255) >> 5) + srh, cbk = ((j0 & 255) >> 5) + skh;
+    // a diagonal tile has no blocks above its diagonal: read the diagonal block
+    // instead (masked to zero in store_chunk)
+    const bool dt = a.self && ti == tj;
+    const bf16_t* p = pslab + int64_t(tile) * a.nsplit * kSyTileElems +
+                      sy_piece(dt, a.rel, rbk, dt && cbk > rbk ? rbk : cbk, pl, ph);
 #pragma unroll
     for (int sp = 0; sp < NS; ++sp)
       pr[k][sp] = *reinterpret_cast<const uint4*>(p + int64_t(min(sp, a.nsplit - 1)) * kSyTileElems);
@@ -1184,10 +1233,10 @@ __global__ __launch_bounds__(512, 1) void k_sy_sv(const SvArgs a) {
       for (int l = 0; l < VL; ++l) vr[k][u][l] = *reinterpret_cast<const uint4*>(vp + 4 * l);
     }
   };
-  // split sum, mask (j < i, j < T), one rounding; then the V block as bf16
+  // split sum, mask (j < i < T), one rounding, into the row-major score
+  // block; then the V block as bf16
   auto store_chunk = [&](int ck, auto slotc) __attribute__((always_inline)) {
     constexpr int k = decltype(slotc)::value;
-    const int j0 = ck * 64 + lk;
     float sacc[8];
 #pragma unroll
     for (int q = 0; q < 8; ++q) sacc[q] = 0.f;
@@ -1201,16 +1250,15 @@ __global__ __launch_bounds__(512, 1) void k_sy_sv(const SvArgs a) {
         sacc[2 * q + 1] += __uint_as_float(xw[q] & 0xffff0000u);
       }
     }
-    uint32_t pk[4];
+    const int key = skh * 32 + (pl & 31), gj = ck * 64 + key;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int j = j0 + 2 * q;
-      const float lo = (row_ok && j < gi) ? sacc[2 * q] : 0.f;
-      const float hi = (row_ok && j + 1 < gi) ? sacc[2 * q + 1] : 0.f;
-      pk[q] = pack_bf2(lo, hi);
-    }
-    const int kc = lk >> 3;
-    *reinterpret_cast<u32x4*>(blk + lr * 128 + ((kc ^ ((lr >> 1) & 7)) * 16)) = u32x4{pk[0], pk[1], pk[2], pk[3]};
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const int lr = srh * 32 + sy_piece_row(pl, ph, q, e), gi = r0 + lr;
+        const float val = (gi < a.T && gj < gi) ? sacc[2 * q + e] : 0.f;
+        *reinterpret_cast<bf16_t*>(blk + lr * 128 + (((key >> 3) ^ ((lr >> 1) & 7)) * 16) + (key & 7) * 2) = f2bf(val);
+      }
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const int r = vr0 + 16 * u, c = vc;
@@ -1535,6 +1583,8 @@ int sy_run(const bdh_tensor4* q, const bdh_tensor4* k, const bdh_tensor4* v, con
   sa.t0 = p.t0;
   sa.rb0 = int(past / 64);
   sa.past = int(past);
+  sa.rel = rel ? 1 : 0;
+  sa.self = self ? 1 : 0;
   const dim3 gsv(unsigned((T + 63) / 64 - sa.rb0), unsigned(nslab));
   const bool o16 = out->dtype == BDH_BF16, v16 = v->dtype == BDH_BF16;
   // one launch per 256 columns of V (the score tiles are read again by each)

@@ -147,7 +147,8 @@ def _ran_score_tiles(fn):
         names = {n for n, _ in ext.profile_collect()}
     finally:
         ext.profile_enable(False)
-    assert "k_sy_scores" in names, names
+    # the score-tile kernel, alone or with score x V fused into its tail
+    assert names & {"k_sy_scores", "k_sy_scores_sv"}, names
     return out
 
 
@@ -225,6 +226,45 @@ def test_bf16_fused_rope_stage_limit(N, table):
         names = {n for n, _ in ext.profile_collect()}
     finally:
         ext.profile_enable(False)
-    assert "k_sy_scores" in names and ("k_rope_table" in names) == table, names
+    assert names & {"k_sy_scores", "k_sy_scores_sv"} and ("k_rope_table" in names) == table, names
     assert rel_fro(got, want) <= TOL[BF]
     assert not got[:, :, 0].any()
+
+
+
+REPRO_SHAPES = [
+    # B, H, T, N, D, Hv, v dtype, out dtype
+    (1, 1, 300, 512, 64, 1, BF, BF),  # two row tiles, split 8
+    (2, 4, 512, 1024, 256, 1, BF, BF),  # C1 layout
+    (1, 2, 700, 256, 96, 2, BF, torch.float32),  # three row tiles, a lone diagonal tile
+    (3, 1, 257, 256, 32, 1, torch.float32, BF),  # fp32 V, one-row second tile
+]
+
+
+@pytest.mark.parametrize("shape", REPRO_SHAPES)
+def test_score_v_matches_oracle_and_is_reproducible(shape):
+    """Split-K self attention, with and without fused RoPE: against the oracle,
+    and repeated calls give the same bits (the split sums run in a fixed order)."""
+    B, H, T, N, D, Hv, vdt, odt = shape
+    print(f"score x V reproducible {shape}", flush=True)
+    x = _bf(latent((B, H, T, N), 51))
+    v = normal((B, Hv, T, D), 52)
+    v = _bf(v) if vdt == BF else v
+    xd, vd = to_dev(x, BF), to_dev(v, vdt)
+    freqs = O.get_freqs(N)
+    fd = torch.from_numpy(freqs).to(DEV)
+
+    def call(rope):
+        if rope:
+            return ext.tril_rope_score_v(xd, vd, fd, 3, out=torch.empty(B, H, T, D, dtype=odt, device=DEV))
+        return ext.tril_score_v(xd, xd, vd)
+
+    for rope in (False, True):
+        first = call(rope)
+        for _ in range(3):
+            assert torch.equal(call(rope), first)
+        want = O.tril_rope_score_v(x, v, freqs, 3, bf16=True)[0] if rope else O.tril_score_v_cpu(x, x, v)
+        err = rel_fro(np_of(first), want)
+        print(f"  rope={rope}: rel {err:.3e}", flush=True)
+        assert err <= TOL[BF]
+        assert not first[:, :, 0].any().item()
