@@ -7,7 +7,9 @@ bdh.py:947-1193), so the hot path can be measured where the model calls it:
 * prefill tok/s (configs C2 and C5): one forward over (B, T) tokens;
 * decode tok/s (config C3): ``generate`` with a packed KR/V cache, the new
   token's RoPE(x) written straight into its cache slot and attention read
-  from capacity-strided cache views (no cast copies of the past);
+  from capacity-strided cache views (no cast copies of the past); or, with
+  ``cache_manager=True``, through ``bdh_cache.CacheManager`` driven by
+  bdh.py's own call sequence (bdh.py:1000-1036);
 * a training step (C4 at model level): forward, cross entropy, backward.
 
 Per layer (x: (B, T, D), LayerNorm without affine, eps 1e-5):
@@ -34,6 +36,7 @@ import torch.nn.functional as F
 from torch import nn
 
 import kernels
+from bdh_cache import CacheManager
 
 
 @dataclasses.dataclass
@@ -162,6 +165,18 @@ def _gated_product(x_bthn: torch.Tensor, y_ln: torch.Tensor, w: torch.Tensor, wt
     return kernels.relu_mul(x_bthn, y.view(nh, B, T, N).permute(1, 2, 0, 3))
 
 
+def _follows(past: torch.Tensor, new: torch.Tensor) -> Optional[torch.Tensor]:
+    """past||new as one view when ``new`` is the rows right after ``past`` in the
+    same buffer (the reserved slot after the committed rows), else None."""
+    if (past.untyped_storage().data_ptr() != new.untyped_storage().data_ptr() or past.stride() != new.stride()
+            or past.dtype != new.dtype or past.shape[:-2] != new.shape[:-2] or past.size(-1) != new.size(-1)):
+        return None
+    if new.storage_offset() != past.storage_offset() + past.size(-2) * past.stride(-2):
+        return None
+    return past.as_strided((*past.shape[:-2], past.size(-2) + new.size(-2), past.size(-1)), past.stride(),
+                           past.storage_offset())
+
+
 class BDH(nn.Module):
     """BDH language model; parameter names and shapes follow bdh_baseline.py:80-102."""
 
@@ -198,9 +213,51 @@ class BDH(nn.Module):
         return prep
 
     # ----------------------------------------------------------- attention
+    def _attention_managed(self, level, x_sparse, v_tok, cache: CacheManager, impl, cos_sin):
+        """One layer against a ``CacheManager`` in bdh.py's order: reserve
+        before get_past and RoPE into the slot when the storage dtype is the
+        compute dtype and v matches it, else get_past, attention, append
+        (bdh.py:1000-1036, 389-461)."""
+        T = x_sparse.size(2)
+        out_kr = None
+        if not torch.is_grad_enabled() and cache.storage_matches_compute and v_tok.dtype == cache.storage_dtype:
+            out_kr, dst_v = cache.reserve(level, T)
+            past_kr, past_v = cache.get_past(level)
+            dst_v.copy_(v_tok)
+            v_tok = dst_v
+        else:
+            past_kr, past_v = cache.get_past(level)
+        if past_kr is None and T > 1 and impl == "hip":
+            # cold prefill: the fused kernel also leaves RoPE(x) for the cache
+            qr = out_kr if out_kr is not None else torch.empty_like(x_sparse, memory_format=torch.contiguous_format)
+            out = kernels.bdh_attn_rope(x_sparse, v_tok, self.freqs, 0, out_kr=qr, impl="hip")
+        else:
+            qr = kernels.bdh_rope_rotate(x_sparse, *cos_sin, out=out_kr, impl=impl)
+            if past_kr is None:
+                out = (x_sparse.new_zeros(x_sparse.size(0), x_sparse.size(1), 1, v_tok.size(-1)) if T == 1
+                       else kernels.bdh_attn(qr, qr, v_tok, impl=impl))
+            elif T == 1:
+                out = kernels.bdh_attn_decode(qr, past_kr, past_v, impl=impl)
+            else:
+                S = past_kr.size(2)
+                kr_all, v_all = _follows(past_kr, qr), _follows(past_v, v_tok)
+                if kr_all is None or v_all is None:
+                    kr_all = qr.new_empty(qr.size(0), qr.size(1), S + T, qr.size(3))
+                    kr_all[:, :, :S].copy_(past_kr)
+                    kr_all[:, :, S:].copy_(qr)
+                    v_all = v_tok.new_empty(v_tok.size(0), 1, S + T, v_tok.size(3))
+                    v_all[:, :, :S].copy_(past_v)
+                    v_all[:, :, S:].copy_(v_tok)
+                out = kernels.bdh_attn_past(kr_all[:, :, S:], kr_all, v_all, S, impl=impl)
+        if out_kr is None:
+            cache.append(level, qr, v_tok)
+        return out
+
     def _attention(self, level, x_sparse, v_tok, rope_start, cache, impl, cos_sin):
         """RoPE + strict-tril attention of one layer (bdh.py:348-483 flow)."""
         T = x_sparse.size(2)
+        if isinstance(cache, CacheManager):
+            return self._attention_managed(level, x_sparse, v_tok, cache, impl, cos_sin)
         if cache is None:
             if impl == "hip":
                 return kernels.bdh_attn_rope(x_sparse, v_tok, self.freqs, rope_start, impl="hip")
@@ -227,7 +284,7 @@ class BDH(nn.Module):
         idx: torch.Tensor,
         targets: Optional[torch.Tensor] = None,
         *,
-        cache: Optional[KVCache] = None,
+        cache: Optional[KVCache | CacheManager] = None,
         impl: Optional[str] = None,
         last_only: bool = False,
     ):
@@ -266,7 +323,9 @@ class BDH(nn.Module):
                 xy = x_bthn * _encode_heads(_ln(y_kv), self.encoder_v)
                 y_mlp = xy.view(B, T, nh * N) @ self.decoder
             x = _ln_fast(y_mlp, x) if fast else _ln(x + _ln(y_mlp))
-        if cache is not None:
+        if isinstance(cache, CacheManager):
+            cache.commit()
+        elif cache is not None:
             cache.commit(T)
         if last_only:
             x = x[:, -1:]
@@ -302,12 +361,26 @@ class BDH(nn.Module):
         amp_dtype: Optional[torch.dtype] = None,
         impl: Optional[str] = None,
         generator: Optional[torch.Generator] = None,
+        cache_manager: bool = False,
+        decode_views: Optional[bool] = None,
     ) -> torch.Tensor:
         """Prompt prefill into a packed cache, then one cached forward per new
-        token (bdh.py:1074-1193).  Returns (B, prompt + max_new_tokens) tokens."""
+        token (bdh.py:1074-1193).  Returns (B, prompt + max_new_tokens) tokens.
+
+        ``cache_manager=True`` uses ``CacheManager`` as bdh.py's generate builds
+        it (compute fp32, storage ``cache_dtype``; bdh.py:1115-1123);
+        ``decode_views`` is passed to it, and defaults to whether the decode
+        runs on the HIP kernels."""
         B, P = idx.shape
-        dtype = cache_dtype or amp_dtype or torch.float32
-        cache = KVCache(self.config, B, P + max_new_tokens, dtype, idx.device)
+        if cache_manager:
+            if decode_views is None:
+                decode_views = kernels.resolve_attn_impl(impl) == "hip"
+            cache = CacheManager.from_config(self.config, batch_size=B, max_seq=P + max_new_tokens, device=idx.device,
+                                             compute_dtype=torch.float32, storage_dtype=cache_dtype,
+                                             decode_views=decode_views)
+        else:
+            dtype = cache_dtype or amp_dtype or torch.float32
+            cache = KVCache(self.config, B, P + max_new_tokens, dtype, idx.device)
         out = torch.empty(B, P + max_new_tokens, dtype=idx.dtype, device=idx.device)
         out[:, :P] = idx
         ctx = (torch.autocast(idx.device.type, dtype=amp_dtype) if amp_dtype is not None

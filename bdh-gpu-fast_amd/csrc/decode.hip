@@ -1,15 +1,16 @@
 // KV-cache decode step for gfx950: out = (q K_past^T) V_past.
 //
 // HBM-bound: every past key row (N = 8192 elements) is read exactly once per
-// query row.  Work is split over the past (chunks of kChunk keys per
-// workgroup) so a B*H = 256 row batch still fills the chip; partial outputs
-// over chunks are summed by a second small kernel (the op is linear in the
-// scores, so no renormalisation is needed).
+// query row.  Work is split over the past (chunks of keys per workgroup) so a
+// B*H = 256 row batch still fills the chip; partial outputs over chunks are
+// summed by a second small kernel (the op is linear in the scores, so no
+// renormalisation is needed).
 //
-// Per workgroup: the query row is staged in LDS as fp32; each wave64 streams
-// one key row at a time with 16-byte loads (each lane covers 8 bf16 / 4 fp32
-// elements per 512-element stride), reduces the dot product across the wave
-// with shuffles, and records the score in LDS; then all 256 threads form the
+// Three score kernels share that shape: k_decode_bf16 (bf16 q and keys,
+// v_dot2 products), k_decode_f32q (fp32 arithmetic, fp32 or bf16 keys, q of
+// either dtype) and k_decode_partial (any strides and widths).  Each wave64
+// streams key rows with 16-byte loads, reduces the dot product across the wave
+// with shuffles and records the score in LDS; then all 256 threads form the
 // partial out[d] = sum_s score_s V[s,d] with coalesced V row reads.
 #include <mutex>
 
@@ -171,6 +172,119 @@ __global__ __launch_bounds__(kDecNT) void k_decode_bf16(DecodeArgs a) {
   }
 }
 
+// fp32 arithmetic against fp32 or bf16 keys, q of either dtype: the
+// reference's decode computes in fp32 (its cache casts a 16-bit past up
+// before the products), and widening bf16 to fp32 is exact, so reading a bf16
+// cache in place gives the products of its fp32 cast copy without the copy.
+// q is staged once per workgroup as fp32 in LDS, arranged so that the 16-byte
+// key piece a lane loads (EK elements) meets its q values in EK / 4
+// contiguous 16-byte LDS reads: float4 plane p of piece c sits at
+// qs[(NP c + p) 64 + lane].  Each wave scores two key rows at a time with
+// eight 16-byte loads in flight per lane; then the 256 threads form the
+// chunk's partial out[d] = sum_s score_s V[s,d].  Needs Dk a multiple of
+// 64 EK and 16-byte aligned q and key rows.
+template <typename TK>
+__device__ __forceinline__ float dot_piece(const u32x4& w, const float4* qs4, int np_stride, float acc) {
+  if constexpr (sizeof(TK) == 4) {
+    const float4 q = qs4[0];
+    acc = fmaf(__uint_as_float(w.x), q.x, acc);
+    acc = fmaf(__uint_as_float(w.y), q.y, acc);
+    acc = fmaf(__uint_as_float(w.z), q.z, acc);
+    return fmaf(__uint_as_float(w.w), q.w, acc);
+  } else {
+    const float4 qa = qs4[0], qb = qs4[np_stride];
+    const uint32_t w0 = w.x, w1 = w.y, w2 = w.z, w3 = w.w;
+    acc = fmaf(__uint_as_float(w0 << 16), qa.x, acc);
+    acc = fmaf(__uint_as_float(w0 & 0xffff0000u), qa.y, acc);
+    acc = fmaf(__uint_as_float(w1 << 16), qa.z, acc);
+    acc = fmaf(__uint_as_float(w1 & 0xffff0000u), qa.w, acc);
+    acc = fmaf(__uint_as_float(w2 << 16), qb.x, acc);
+    acc = fmaf(__uint_as_float(w2 & 0xffff0000u), qb.y, acc);
+    acc = fmaf(__uint_as_float(w3 << 16), qb.z, acc);
+    return fmaf(__uint_as_float(w3 & 0xffff0000u), qb.w, acc);
+  }
+}
+
+template <typename TQ, typename TK, typename TV>
+__global__ __launch_bounds__(kDecNT) void k_decode_f32q(DecodeArgs a) {
+  constexpr int EK = 16 / int(sizeof(TK));  // key elements per 16-byte piece
+  constexpr int NP = EK / 4;                // float4 planes of q per piece
+  extern __shared__ float smem[];
+  float* sc = smem;                                         // kDecChunkB scores
+  float4* qs = reinterpret_cast<float4*>(smem + kDecChunkB);  // Dk / 4 float4
+  const int64_t row = blockIdx.y;
+  const int64_t t = row % a.Tq, bh = row / a.Tq;
+  const int64_t h = bh % a.H, b = bh / a.H;
+  const int64_t hv = a.Hv == 1 ? 0 : h;
+  const TQ* qp = static_cast<const TQ*>(a.q.p) + b * a.q.s0 + h * a.q.s1 + t * a.q.s2;
+  for (int64_t i = threadIdx.x; i < a.Dk / 4; i += kDecNT) {
+    const int64_t l = i & 63, cp = i >> 6;
+    const int64_t e = ((cp / NP) * 64 + l) * EK + (cp % NP) * 4;
+    float4 v;
+    if constexpr (sizeof(TQ) == 4) {
+      v = *reinterpret_cast<const float4*>(qp + e);
+    } else {
+      const u32x2 w = *reinterpret_cast<const u32x2*>(qp + e);
+      const uint32_t w0 = w.x, w1 = w.y;
+      v = make_float4(__uint_as_float(w0 << 16), __uint_as_float(w0 & 0xffff0000u), __uint_as_float(w1 << 16),
+                      __uint_as_float(w1 & 0xffff0000u));
+    }
+    qs[i] = v;
+  }
+  __syncthreads();
+
+  const int64_t s0 = int64_t(blockIdx.x) * kDecChunkB;
+  const int64_t s1 = min(a.S, s0 + kDecChunkB);
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const TK* kb = static_cast<const TK*>(a.k.p) + b * a.k.s0 + h * a.k.s1;
+  const int nc = int(a.Dk / (64 * EK));  // 16-byte pieces per lane per key row
+  const float4* ql = qs + lane;
+  // keys s0 + wave + 4 j of this wave, in pairs (s, s + 4)
+  for (int64_t s = s0 + wave; s < s1; s += 8) {
+    const bool two = s + 4 < s1;
+    const TK* k0 = kb + s * a.k.s2 + lane * EK;
+    const TK* k1 = kb + (two ? s + 4 : s) * a.k.s2 + lane * EK;
+    float acc0 = 0.f, acc1 = 0.f;
+    int c = 0;
+    for (; c + 4 <= nc; c += 4) {
+      u32x4 x0[4], x1[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        x0[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(k0 + (c + u) * 64 * EK));
+        x1[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(k1 + (c + u) * 64 * EK));
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const float4* q = ql + (NP * (c + u)) * 64;
+        acc0 = dot_piece<TK>(x0[u], q, 64, acc0);
+        acc1 = dot_piece<TK>(x1[u], q, 64, acc1);
+      }
+    }
+    for (; c < nc; ++c) {
+      const u32x4 x0 = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(k0 + c * 64 * EK));
+      const u32x4 x1 = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(k1 + c * 64 * EK));
+      const float4* q = ql + (NP * c) * 64;
+      acc0 = dot_piece<TK>(x0, q, 64, acc0);
+      acc1 = dot_piece<TK>(x1, q, 64, acc1);
+    }
+    acc0 = wave_sum(acc0);
+    acc1 = wave_sum(acc1);
+    if (lane == 0) {
+      sc[s - s0] = acc0;
+      if (two) sc[s + 4 - s0] = acc1;
+    }
+  }
+  __syncthreads();
+
+  const TV* vb = static_cast<const TV*>(a.v.p) + b * a.v.s0 + hv * a.v.s1;
+  float* out = a.part + (int64_t(blockIdx.x) * a.rows + row) * a.Dv;
+  for (int64_t d = threadIdx.x; d < a.Dv; d += kDecNT) {
+    float o = 0.f;
+    for (int64_t s = s0; s < s1; ++s) o += sc[s - s0] * to_f(vb[s * a.v.s2 + d]);
+    out[d] = o;
+  }
+}
+
 template <typename TO>
 __global__ __launch_bounds__(kDecNT) void k_decode_reduce(const float* part, int64_t nchunk, int64_t rows,
                                                           int64_t Dv, View o, int64_t H, int64_t Tq) {
@@ -205,6 +319,25 @@ static int pick_k(const DecodeArgs& a, int64_t nchunk, int32_t kdt, int32_t vdt,
   return kdt == BDH_BF16 ? pick_v<TQ, bf16_t>(a, nchunk, vdt, s) : pick_v<TQ, float>(a, nchunk, vdt, s);
 }
 
+template <typename TQ, typename TK, typename TV>
+static int launch_f32q_t(const DecodeArgs& a, int64_t nred, hipStream_t s) {
+  const dim3 grid((unsigned)nred, unsigned(a.rows));
+  const size_t shm = size_t(kDecChunkB) * sizeof(float) + size_t(a.Dk) * sizeof(float);
+  BDH_LAUNCH("k_decode_f32q", (k_decode_f32q<TQ, TK, TV>), grid, dim3(kDecNT), shm, s, a);
+  return BDH_OK;
+}
+
+template <typename TQ, typename TK>
+static int launch_f32q_v(const DecodeArgs& a, int64_t nred, int32_t vdt, hipStream_t s) {
+  return vdt == BDH_BF16 ? launch_f32q_t<TQ, TK, bf16_t>(a, nred, s) : launch_f32q_t<TQ, TK, float>(a, nred, s);
+}
+
+static int launch_f32q(const DecodeArgs& a, int64_t nred, int32_t qdt, int32_t kdt, int32_t vdt, hipStream_t s) {
+  if (qdt == BDH_BF16)
+    return kdt == BDH_BF16 ? launch_f32q_v<bf16_t, bf16_t>(a, nred, vdt, s) : launch_f32q_v<bf16_t, float>(a, nred, vdt, s);
+  return kdt == BDH_BF16 ? launch_f32q_v<float, bf16_t>(a, nred, vdt, s) : launch_f32q_v<float, float>(a, nred, vdt, s);
+}
+
 }  // namespace bdh
 
 using namespace bdh;
@@ -221,9 +354,10 @@ namespace {
 // Shape/dtype contract of decode (kernels/cuda_attn.py:114-131,
 // csrc/tril_attn_cpu.cpp:214-223) and the launch plan: part_bytes is the
 // partial-sum storage the chosen kernels need.
+enum DecodeKind { kDecGeneric = 0, kDecBf16 = 1, kDecF32q = 2 };
 struct DecodePlan {
   DecodeArgs a;
-  bool fast = false;
+  DecodeKind kind = kDecGeneric;
   int64_t nred = 0;
   size_t part_bytes = 0;
 };
@@ -259,10 +393,16 @@ int decode_plan(const bdh_tensor4* q, const bdh_tensor4* k, const bdh_tensor4* v
   a.vec_k = vec16_ok(k) ? 1 : 0;
   a.part = nullptr;
   a.rows = B * H * Tq;
-  // bf16 cache path: fewer, larger key chunks
-  p.fast = q->dtype == BDH_BF16 && k->dtype == BDH_BF16 && vec16_ok(q) && vec16_ok(k) && Dk % 2048 == 0 &&
-           Dk * 2 + kDecChunkB * 4 <= 64 * 1024 && S > 0;
-  p.nred = p.fast ? (S + kDecChunkB - 1) / kDecChunkB : n_chunks(S);
+  // streaming kernels (64-key chunks) where q and the key rows allow
+  // 16-byte pieces; the generic kernel otherwise
+  const bool vec = vec16_ok(q) && vec16_ok(k) && S > 0;
+  if (vec && q->dtype == BDH_BF16 && k->dtype == BDH_BF16 && Dk % 2048 == 0 && Dk * 2 + kDecChunkB * 4 <= 64 * 1024)
+    p.kind = kDecBf16;
+  else if (vec && Dk % (64 * (k->dtype == BDH_BF16 ? 8 : 4)) == 0 && Dk * 4 + kDecChunkB * 4 <= 64 * 1024)
+    p.kind = kDecF32q;
+  else
+    p.kind = kDecGeneric;
+  p.nred = p.kind == kDecGeneric ? n_chunks(S) : (S + kDecChunkB - 1) / kDecChunkB;
   p.part_bytes = size_t(p.nred) * size_t(a.rows) * size_t(Dv) * sizeof(float);
   return BDH_OK;
 }
@@ -273,13 +413,16 @@ int decode_run(const DecodePlan& p, const bdh_tensor4* q, const bdh_tensor4* k, 
                const bdh_tensor4* out, float* part, hipStream_t st) {
   DecodeArgs a = p.a;
   a.part = part;
-  if (p.fast) {
+  if (p.kind == kDecBf16) {
     const dim3 grid((unsigned)p.nred, unsigned(a.rows));
     const size_t shm = size_t(kDecChunkB) * sizeof(float) + size_t(a.Dk) * 2;
     if (v->dtype == BDH_BF16)
       BDH_LAUNCH("k_decode_bf16", k_decode_bf16<bf16_t>, grid, dim3(kDecNT), shm, st, a);
     else
       BDH_LAUNCH("k_decode_bf16", k_decode_bf16<float>, grid, dim3(kDecNT), shm, st, a);
+  } else if (p.kind == kDecF32q) {
+    const int rc = launch_f32q(a, p.nred, q->dtype, k->dtype, v->dtype, st);
+    if (rc != BDH_OK) return rc;
   } else {
     const int rc = q->dtype == BDH_BF16 ? pick_k<bf16_t>(a, p.nred, k->dtype, v->dtype, st)
                                         : pick_k<float>(a, p.nred, k->dtype, v->dtype, st);

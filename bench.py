@@ -348,22 +348,7 @@ def run_extra(torch, ext, kernels, dev, steps, warmup, x, v) -> dict:
     out["c1_torch_eager_gpu_on_qr"] = {"us": ms_e * 1e3, "tflops": F / ms_e / 1e9}
     log(f"[bench] unfused {ms * 1e3:.1f} us, rope {ms_r * 1e3:.1f} us, torch eager {ms_e * 1e3:.1f} us")
 
-    # Decode step (C3): B=64 nh=4 N=8192 D=256, bf16 cache read in place.
-    Bd, nhd, Nd, Dd = (C3[k] for k in ("B", "nh", "N", "D"))
-    cap = max(C3["S"]) + 1
-    g = torch.Generator(device=dev).manual_seed(5)
-    kcache = torch.relu(0.32 * torch.randn(Bd, nhd, cap, Nd, generator=g, device=dev)).to(torch.bfloat16)
-    vcache = torch.randn(Bd, 1, cap, Dd, generator=g, device=dev).to(torch.bfloat16)
-    q = torch.relu(0.32 * torch.randn(Bd, nhd, 1, Nd, generator=g, device=dev)).to(torch.bfloat16)
-    dec = {}
-    for S in C3["S"]:
-        kp, vp = kcache.narrow(2, 0, S), vcache.narrow(2, 0, S)
-        ms_d = time_steps(lambda: kernels.bdh_attn_decode(q, kp, vp, impl="hip"), steps * 4, warmup)
-        by = 2 * (Bd * nhd * S * Nd + Bd * S * Dd + Bd * nhd * Nd + Bd * nhd * Dd)
-        dec[str(S)] = {"us": ms_d * 1e3, "gbs": by / ms_d / 1e6, "frac_hbm": by / ms_d / 1e6 / PEAK_HBM_GBS}
-    out["c3_decode_step_per_layer"] = dec
-    log(f"[bench] decode: {json.dumps(dec)}")
-    del kcache, vcache
+    out.update(run_decode(torch, kernels, dev, steps, warmup))
 
     # Training op (C4): fwd + merged-gradient bwd, bf16.
     B4, nh4, T4, N4, D4 = (C4[k] for k in ("B", "nh", "T", "N", "D"))
@@ -388,6 +373,58 @@ def run_extra(torch, ext, kernels, dev, steps, warmup, x, v) -> dict:
         ms_t = time_steps(fn, max(2, steps // 2), 1)
         out[key] = {"us": ms_t * 1e3, "tflops": F4 / ms_t / 1e9, "frac_bf16_peak": F4 / ms_t / 1e9 / PEAK_BF16_TFLOPS}
         log(f"[bench] {key}: {ms_t * 1e3:.1f} us, {F4 / ms_t / 1e9:.1f} TFLOP/s")
+    return out
+
+
+def run_decode(torch, kernels, dev, steps, warmup) -> dict:
+    """C3 decode-step legs: the bf16 cache read in place at each C3 past, and the
+    routes of the reference generate's caches at the longest past."""
+    out: dict = {}
+    # Decode step (C3): B=64 nh=4 N=8192 D=256, bf16 cache read in place.
+    Bd, nhd, Nd, Dd = (C3[k] for k in ("B", "nh", "N", "D"))
+    cap = max(C3["S"]) + 1
+    g = torch.Generator(device=dev).manual_seed(5)
+    kcache = torch.relu(0.32 * torch.randn(Bd, nhd, cap, Nd, generator=g, device=dev)).to(torch.bfloat16)
+    vcache = torch.randn(Bd, 1, cap, Dd, generator=g, device=dev).to(torch.bfloat16)
+    q = torch.relu(0.32 * torch.randn(Bd, nhd, 1, Nd, generator=g, device=dev)).to(torch.bfloat16)
+    dec = {}
+    for S in C3["S"]:
+        kp, vp = kcache.narrow(2, 0, S), vcache.narrow(2, 0, S)
+        ms_d = time_steps(lambda: kernels.bdh_attn_decode(q, kp, vp, impl="hip"), steps * 4, warmup)
+        by = 2 * (Bd * nhd * S * Nd + Bd * S * Dd + Bd * nhd * Nd + Bd * nhd * Dd)
+        dec[str(S)] = {"us": ms_d * 1e3, "gbs": by / ms_d / 1e6, "frac_hbm": by / ms_d / 1e6 / PEAK_HBM_GBS}
+    out["c3_decode_step_per_layer"] = dec
+    log(f"[bench] decode: {json.dumps(dec)}")
+
+    # The caches the reference's generate builds (compute fp32, bdh.py:1115-1123),
+    # at the longest C3 past:
+    #  * fp32_cache: cache_dtype=None, fp32 q and past (k_decode_f32q);
+    #  * bf16_cache_reference_cast: bf16 storage, the past cast up to fp32 by
+    #    the reference CacheManager.get_past (bdh_cache.py:238-243) on every
+    #    layer step, timed with the decode it feeds (bf16 q, fp32 past);
+    #  * bf16_cache_storage_views: the package's CacheManager hands the bf16
+    #    views to the HIP decode (no cast).
+    S = max(C3["S"])
+    kp, vp = kcache.narrow(2, 0, S), vcache.narrow(2, 0, S)
+    k32, v32 = kcache.float(), vcache.float()
+    q32 = q.float()
+    elems = Bd * nhd * S * Nd + Bd * S * Dd + Bd * nhd * Nd + Bd * nhd * Dd
+    routes = {
+        "fp32_cache": (lambda: kernels.bdh_attn_decode(q32, k32.narrow(2, 0, S), v32.narrow(2, 0, S), impl="hip"), 4),
+        "bf16_cache_reference_cast": (lambda: kernels.bdh_attn_decode(q, kp.to(torch.float32), vp.to(torch.float32),
+                                                                      impl="hip"), 2),
+        "bf16_cache_storage_views": (lambda: kernels.bdh_attn_decode(q, kp, vp, impl="hip"), 2),
+    }
+    rt = {}
+    for name, (fn, width) in routes.items():
+        ms_d = time_steps(fn, steps * 2, warmup)
+        rt[name] = {"S": S, "us": ms_d * 1e3, "cache_bytes_per_elem": width,
+                    "gbs_cache_bytes": width * elems / ms_d / 1e6}
+    rt["views_speedup_over_cast"] = rt["bf16_cache_reference_cast"]["us"] / rt["bf16_cache_storage_views"]["us"]
+    out["c3_decode_reference_cache_routes"] = rt
+    log(f"[bench] decode routes: {json.dumps(rt)}")
+    del kcache, vcache, k32, v32
+
     return out
 
 
@@ -442,21 +479,30 @@ def run_models(torch, ext, dev, only=None) -> dict:
     g = torch.Generator(device=dev).manual_seed(2)
     prompt = torch.randint(0, 256, (c["B"], c["prompt"]), generator=g, device=dev)
     leg = {"B": c["B"], "prompt": c["prompt"], "new_tokens": c["new"], "top_k": c["top_k"], "cache": "bf16"}
-    for impl in impls:
-        log(f"[bench] c3_generate {impl} ...")
+    # hip: the harness's own cache; hip_cache_manager: bdh_cache.CacheManager in
+    # bdh.py's call order, storage-dtype views to the decode;
+    # hip_cache_manager_reference_cast: the same with the reference's get_past
+    # casts (bf16 past copied up to fp32 on every layer step)
+    variants = [("hip", {}), ("hip_cache_manager", {"cache_manager": True}),
+                ("hip_cache_manager_reference_cast", {"cache_manager": True, "decode_views": False})]
+    if "eager" in impls:
+        variants.append(("eager", {}))
+    for key, kw in variants:
+        impl = "eager" if key == "eager" else "hip"
+        log(f"[bench] c3_generate {key} ...")
 
         def gen():
             return m.generate(prompt, c["new"], top_k=c["top_k"], cache_dtype=torch.bfloat16,
                               amp_dtype=torch.bfloat16, impl=impl,
-                              generator=torch.Generator(device=dev).manual_seed(c["seed"]))
+                              generator=torch.Generator(device=dev).manual_seed(c["seed"]), **kw)
         gen()  # warm-up (allocator, library)
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         gen()
         torch.cuda.synchronize()
         s = time.perf_counter() - t0
-        leg[impl] = {"s": s, "tok_s": c["B"] * c["new"] / s}
-        if impl == "hip":
+        leg[key] = {"s": s, "tok_s": c["B"] * c["new"] / s}
+        if key == "hip":
             ext.profile_enable(True)
             gen()
             rec = ext.profile_collect()
@@ -470,7 +516,9 @@ def run_models(torch, ext, dev, only=None) -> dict:
             leg[impl]["library_kernels_ms"] = sum(t for _, t in rec)
     out["c3_generate"] = leg
     log(f"[bench] c3_generate: hip {leg['hip']['tok_s']:.0f} tok/s ({leg['hip']['s']:.3f} s; decode attention "
-        f"{leg['hip']['decode_attention_ms']:.1f} ms, {leg['hip']['decode_attention_gbs']:.0f} GB/s)"
+        f"{leg['hip']['decode_attention_ms']:.1f} ms, {leg['hip']['decode_attention_gbs']:.0f} GB/s); "
+        f"CacheManager {leg['hip_cache_manager']['tok_s']:.0f} tok/s, with the reference's casts "
+        f"{leg['hip_cache_manager_reference_cast']['tok_s']:.0f} tok/s"
         + (f", eager {leg['eager']['tok_s']:.0f} tok/s" if "eager" in leg else ""))
     del m
     torch.cuda.empty_cache()
