@@ -7,10 +7,10 @@
   cache, one-token decode over capacity-strided bf16 cache views, a chunk
   after a past on the score-tile path) against the uncached forward;
 * a training step (cross entropy, backward through the HIP attention
-  backward): at fp32 equal to the step with eager attention; under AMP, its
-  error against the fp32 step no larger than the eager-attention AMP step's
-  (both are about 3-6e-2 on the weight gradients, from the model's bf16
-  GEMMs; the attention kernels add nothing measurable);
+  backward): at fp32 equal to the step with eager attention; under AMP, the
+  bf16 attention's effect on the gradients (against the same AMP step with
+  fp32 attention) no larger than that of the reference's eager bf16
+  attention measured the same way;
 * ``generate`` end to end;
 * the row LayerNorm (LN(y), LN(x + LN(y))) against F.layer_norm.
 """
@@ -100,12 +100,36 @@ def test_cached_paths_match_uncached_forward(dtype):
     assert rel_fro(got, full.float().cpu().numpy()) <= tol
 
 
-def _grads(p, idx, tgt, impl, amp, device=DEV):
+def _grads(p, idx, tgt, impl, amp, device=DEV, fp32_attention=False):
+    """Parameter gradients (and the loss) of one training step.  With
+    ``fp32_attention`` the layer's RoPE + attention runs in fp32 whatever the
+    autocast state (on the GPU through the HIP fp32 kernels, on the CPU through
+    torch), while every other product keeps its autocast dtype."""
     m = _model(p, mult=8, device=device)
     idx, tgt = idx.to(device), tgt.to(device)
-    with torch.autocast(torch.device(device).type, dtype=torch.bfloat16, enabled=amp):
-        _, loss = m(idx, tgt, impl=impl)
-    loss.backward()
+    orig_rope, orig_attn, orig_rot = H.kernels.bdh_attn_rope, H.kernels.bdh_attn, H.kernels.bdh_rope_rotate
+    if fp32_attention:
+        def rope32(x, v, freqs, rope_start=0, **kw):
+            with torch.autocast(torch.device(device).type, enabled=False):
+                return orig_rope(x.float(), v.float(), freqs, rope_start, impl=kw.get("impl"))
+
+        def attn32(q, k, v, **kw):
+            with torch.autocast(torch.device(device).type, enabled=False):
+                qf = q.float()
+                return orig_attn(qf, qf if k is q else k.float(), v.float(), impl=kw.get("impl"))
+
+        def rot32(x, cos, sin, out=None, **kw):
+            assert out is None
+            with torch.autocast(torch.device(device).type, enabled=False):
+                return orig_rot(x.float(), cos, sin, impl=kw.get("impl"))
+
+        H.kernels.bdh_attn_rope, H.kernels.bdh_attn, H.kernels.bdh_rope_rotate = rope32, attn32, rot32
+    try:
+        with torch.autocast(torch.device(device).type, dtype=torch.bfloat16, enabled=amp):
+            _, loss = m(idx, tgt, impl=impl)
+        loss.backward()
+    finally:
+        H.kernels.bdh_attn_rope, H.kernels.bdh_attn, H.kernels.bdh_rope_rotate = orig_rope, orig_attn, orig_rot
     g = {n: q.grad.float().cpu().numpy() for n, q in m.named_parameters()}
     g["loss"] = np.array([loss.item()])
     return g
@@ -113,27 +137,37 @@ def _grads(p, idx, tgt, impl, amp, device=DEV):
 
 @pytest.mark.parametrize("amp", [False, True])
 def test_train_step_gradients(amp):
-    """fp32: HIP attention gradients equal eager attention's (1e-4).  AMP:
-    against the fp32 step, the HIP step's error is within 2e-2 or no worse
-    than 1.25x the eager-attention AMP step's own error (the model's bf16
-    GEMMs contribute to both).  The eager AMP step runs on the CPU: its
-    autograd makes bf16 batched products on transposed views, which have
-    faulted ROCm GPUs."""
+    """fp32: HIP attention gradients equal eager attention's (1e-4).
+
+    AMP: the attention's own precision is isolated by holding everything else
+    fixed.  The HIP step (bf16 attention) is compared with the same AMP step
+    whose attention runs in fp32 (same device, same bf16 GEMMs); its effect on
+    every gradient must be no larger than the effect of the reference's own
+    AMP attention (eager: RoPE products and S rounded to bf16) measured the
+    same way, eager bf16 against eager fp32 attention.  That effect is
+    3-5e-2 on the weight gradients at this shape: at the model level the
+    reference's AMP attention already moves gradients by more than the op-level
+    2e-2, which the attention op itself meets (C4 and the backward tests).  The
+    eager pair runs on the CPU: its autograd makes bf16 batched products on
+    transposed views, which have faulted ROCm GPUs."""
     print(f"harness train step amp={amp}", flush=True)
     p = M.init_params(2, 64, 2, 256, 256, seed=17)
     idx = torch.from_numpy(np.random.default_rng(18).integers(0, 256, (2, 200))).to(DEV)
     tgt = torch.from_numpy(np.random.default_rng(19).integers(0, 256, (2, 200))).to(DEV)
-    ref = _grads(p, idx, tgt, "eager", False)
-    hip = _grads(p, idx, tgt, "hip", amp)
     if not amp:
+        ref = _grads(p, idx, tgt, "eager", False)
+        hip = _grads(p, idx, tgt, "hip", False)
         for n in ref:
             assert rel_fro(hip[n], ref[n]) <= 1e-4, n
         return
+    hip = _grads(p, idx, tgt, "hip", True)
+    hip32 = _grads(p, idx, tgt, "hip", True, fp32_attention=True)
     eag = _grads(p, idx, tgt, "eager", True, device="cpu")
-    for n in ref:
-        e_hip, e_eag = rel_fro(hip[n], ref[n]), rel_fro(eag[n], ref[n])
-        print(f"  {n}: hip {e_hip:.3e} eager {e_eag:.3e}", flush=True)
-        assert e_hip <= max(2e-2, 1.25 * e_eag), n
+    eag32 = _grads(p, idx, tgt, "eager", True, device="cpu", fp32_attention=True)
+    for n in hip:
+        e_hip, e_eag = rel_fro(hip[n], hip32[n]), rel_fro(eag[n], eag32[n])
+        print(f"  {n}: bf16 vs fp32 attention: hip {e_hip:.3e} eager {e_eag:.3e}", flush=True)
+        assert e_hip <= max(2e-2, 1.05 * e_eag), n
 
 
 def test_generate_end_to_end_bf16():
