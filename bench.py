@@ -7,7 +7,8 @@ HIP kernels (``kernels.bdh_attn_rope(impl="hip")``), inputs resident in HBM.
 One step = one call over the whole batch.  Throughput is the algorithmic
 F = B*nh*(N+D)*T*(T-1) flops per step (strict lower triangle; RoPE's
 elementwise work is not counted) divided by the measured step time.  The step
-runs untimed for 0.2 s, then W warmup steps, then exactly K timed steps
+first runs untimed until two consecutive 20-step windows agree within 2 %
+(at least 0.2 s, at most 3 s), then W warmup steps, then exactly K timed steps
 (defaults K = 200, W = 100), synchronised on both sides.
 
 The JSON line also carries:
@@ -17,15 +18,21 @@ The JSON line also carries:
     against the 2.5 PFLOP/s bf16 dense MFMA peak.  ``traffic`` is the HBM
     bytes per launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE runs
     (profiles/<kernel>_c1_bf16_pmc.txt) when present, else null.
+  * ``device``: CU count, architecture, the shader clock amd-smi reports while
+    the step runs back to back, and how the settle phase ended.
   * ``cpu_baseline``: the CPU oracle (numpy restatement of the reference CPU
-    path, fp32, BLAS threads as reported) on a bounded sample of the same
-    workload, in the same unit.
-  * ``extra``: other hot-path legs (decode step GB/s at C3, training op
-    fwd+bwd TFLOP/s at C4, the unfused path and torch eager on the GPU).
+    path, fp32, BLAS threads as reported) on bounded samples: C1 (the
+    headline's unit), the C2 model, C3 decode attention (integrated over a
+    generate), the C4 training op and the C5 attention op; ``gpu_beside_cpu``
+    puts each GPU figure of the line next to its CPU sample.
+  * ``extra``: other hot-path legs (C1 in fp32 against the fp32 MFMA peak,
+    the C5 attention op, decode step GB/s at C3, training op fwd+bwd TFLOP/s
+    at C4, the unfused path and torch eager on the GPU).
   * ``models``: the model harness (``bdh_harness.BDH``, random N(0, 0.02^2)
-    weights, uniform byte tokens) at C2 and C5 (prefill tok/s, bf16 autocast)
-    and C3 (``generate`` tok/s with a bf16 packed cache), HIP attention beside
-    the same model with eager attention.
+    weights, uniform byte tokens) at C2 and C5 (prefill tok/s, bf16 autocast),
+    a C2 training step (AMP forward, backward, AdamW), and C3 (``generate``
+    tok/s with a bf16 packed cache), HIP attention beside the same model with
+    eager attention.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extra] [--no-models]
        python bench.py --model c2|c5|c3     (one model leg, HIP path only)
@@ -50,6 +57,7 @@ for _p in (str(ROOT), str(ROOT / "bdh-gpu-fast_amd")):
 METRIC = "tril-attn TFLOP/s & %MFMA peak; BDH prefill tok/s; decode tok/s + HBM GB/s"
 PEAK_BF16_TFLOPS = 2500.0
 PEAK_HBM_GBS = 8000.0
+PEAK_FP32_TFLOPS = 157.3
 C1 = dict(B=8, nh=4, T=512, N=8192, D=256)
 C3 = dict(B=64, nh=4, N=8192, D=256, S=(256, 384, 511))
 C4 = dict(B=16, nh=4, T=1024, N=8192, D=256)
@@ -67,27 +75,87 @@ def attn_flops(B, nh, T, N, D) -> float:
     return float(B * nh * (N + D) * T * (T - 1))
 
 
-def settle(fn, seconds: float = 0.2) -> None:
-    """Run the step untimed for ``seconds``: the first ~100 steps of a cold
-    process run up to 10% slower (clocks and queues settling), which a short
-    warmup would leave in the timed region."""
-    import time
+def settle(fn, window: int = 20, tol: float = 0.02, max_s: float = 3.0, min_s: float = 0.2) -> dict:
+    """Run the step untimed until its rate has settled: consecutive windows of
+    ``window`` steps (HIP events) until two in a row agree within ``tol``,
+    after at least ``min_s`` seconds and at most ``max_s``.  The first ~100
+    steps of a cold process run up to 10% slower (clocks and queues settling),
+    which a short warmup would leave in the timed region.  Returns the window
+    times (ms per step) and whether they converged."""
     import torch
 
-    t_end = time.perf_counter() + seconds
+    t_end = time.perf_counter() + max_s
+    t_min = time.perf_counter() + min_s
+    hist: list = []
+    converged = False
     while time.perf_counter() < t_end:
-        for _ in range(4):
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(window):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        hist.append(e0.elapsed_time(e1) / window)
+        if len(hist) >= 2 and time.perf_counter() >= t_min and abs(hist[-1] - hist[-2]) <= tol * hist[-2]:
+            converged = True
+            break
+    return {"windows": len(hist), "last_ms": hist[-2:], "converged": converged}
+
+
+def sample_sclk(fn, seconds: float = 1.5) -> dict:
+    """Shader clock while ``fn`` runs back to back: amd-smi's per-XCD gfx
+    clocks (MHz), sampled from a thread during a busy window.  Best effort:
+    None fields when amd-smi is not available."""
+    import subprocess
+    import threading
+
+    import torch
+
+    samples: list = []
+
+    def poll():
+        for _ in range(3):
+            try:
+                r = subprocess.run(["amd-smi", "metric", "-g", "0", "--clock", "--json"], capture_output=True,
+                                   text=True, timeout=10)
+                data = json.loads(r.stdout)
+                clk = data["gpu_data"][0]["clock"] if isinstance(data, dict) else data[0]["clock"]
+                vals = [v["clk"]["value"] for k, v in clk.items() if k.startswith("gfx_") and isinstance(v, dict)]
+                vals = [float(x) for x in vals if isinstance(x, (int, float))]
+                if vals:
+                    samples.append(sum(vals) / len(vals))
+            except Exception:  # pragma: no cover - informational only
+                return
+
+    th = threading.Thread(target=poll, daemon=True)
+    t_end = time.perf_counter() + seconds
+    th.start()
+    while time.perf_counter() < t_end or th.is_alive():
+        for _ in range(8):
             fn()
         torch.cuda.synchronize()
+        if time.perf_counter() > t_end + 30:
+            break
+    th.join(timeout=1)
+    props = torch.cuda.get_device_properties(0)
+    return {
+        "sclk_mhz_busy": round(statistics.mean(samples), 1) if samples else None,
+        "sclk_samples": len(samples),
+        "cus": int(props.multi_processor_count),
+        "arch": str(getattr(props, "gcnArchName", "")),
+        "device": str(props.name),
+    }
 
 
 def time_steps(fn, steps: int, warmup: int, settle_s: float = 0.2) -> float:
     """ms per step over exactly ``steps`` calls, synchronised on both sides,
-    after ``settle`` for ``settle_s`` seconds and ``warmup`` untimed calls."""
+    after a short settle (at least ``settle_s`` seconds, until two 20-step
+    windows agree within 2 %) and ``warmup`` untimed calls."""
     import torch
 
     if settle_s > 0:
-        settle(fn, settle_s)
+        settle(fn, max_s=max(settle_s, 1.0), min_s=settle_s)
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
@@ -171,6 +239,74 @@ def cpu_baseline(reps: int = 3) -> dict:
         M.bdh_forward(p, idx)
         mt.append(time.perf_counter() - t)
     mmed = statistics.median(mt)
+
+    # C4 (training op): forward + analytic merged backward on one of 16 batch
+    # elements, fp32 (the reference's CPU path: tril_attn_cpu.cpp forward,
+    # attention_bwd.py blocked backward).
+    n4, T4, N4, D4 = C4["nh"], C4["T"], C4["N"], C4["D"]
+    x4 = np.maximum(rng.standard_normal((1, n4, T4, N4), dtype=np.float32) * np.float32(0.32), 0)
+    v4 = rng.standard_normal((1, 1, T4, D4), dtype=np.float32)
+    d4 = rng.standard_normal((1, n4, T4, D4), dtype=np.float32)
+
+    def c4():
+        O.tril_score_v_cpu(x4, x4, v4)
+        O.self_attn_backward(x4, v4, d4)
+
+    c4()
+    t4 = []
+    for _ in range(2):
+        t = time.perf_counter()
+        c4()
+        t4.append(time.perf_counter() - t)
+    m4 = statistics.median(t4)
+    F4 = 3 * attn_flops(1, n4, T4, N4, D4)
+    del x4, v4, d4
+
+    # C5 (long prefill): the fused RoPE attention op on one of 4 batch
+    # elements at the C5 width (nh=8, T=2048, N=8192, D=512).
+    n5, T5, D5 = C5["nh"], C5["T"], C5["D"]
+    N5 = C5["mult"] * D5 // n5
+    x5 = np.maximum(rng.standard_normal((1, n5, T5, N5), dtype=np.float32) * np.float32(0.32), 0)
+    v5 = rng.standard_normal((1, 1, T5, D5), dtype=np.float32)
+    f5 = O.get_freqs(N5)
+    O.tril_rope_score_v(x5, v5, f5, 0)
+    t5 = []
+    for _ in range(2):
+        t = time.perf_counter()
+        O.tril_rope_score_v(x5, v5, f5, 0)
+        t5.append(time.perf_counter() - t)
+    m5 = statistics.median(t5)
+    F5 = attn_flops(1, n5, T5, N5, D5)
+    del x5, v5
+
+    # C3 (decode): one layer step of the decode attention at S = 256, 384,
+    # 511 on 8 of the 64 sequences (scaled by 8), a straight line through the
+    # three fitted by least squares, summed over the 256 generated tokens
+    # (S = 256 .. 511) and the 6 layers: the attention seconds of one C3
+    # generate on the CPU.
+    Bs3, n3, N3, D3 = 8, C3["nh"], C3["N"], C3["D"]
+    Smax = max(C3["S"])
+    k3 = np.maximum(rng.standard_normal((Bs3, n3, Smax, N3), dtype=np.float32) * np.float32(0.32), 0)
+    v3 = rng.standard_normal((Bs3, 1, Smax, D3), dtype=np.float32)
+    q3 = np.maximum(rng.standard_normal((Bs3, n3, 1, N3), dtype=np.float32) * np.float32(0.32), 0)
+    per_s = {}
+    for S in C3["S"]:
+        kp, vp = k3[:, :, :S], v3[:, :, :S]
+        O.tril_decode_cpu(q3, kp, vp)
+        ts = []
+        for _ in range(reps):
+            t = time.perf_counter()
+            O.tril_decode_cpu(q3, kp, vp)
+            ts.append(time.perf_counter() - t)
+        per_s[S] = statistics.median(ts) * (C3["B"] // Bs3)
+    Ss = np.array(list(per_s), dtype=np.float64)
+    ys = np.array([per_s[S] for S in per_s])
+    b1, b0 = np.polyfit(Ss, ys, 1)
+    steps = np.arange(C3_GEN["prompt"], C3_GEN["prompt"] + C3_GEN["new"], dtype=np.float64)
+    total3 = float(np.sum(b0 + b1 * steps)) * C3_GEN["n_layer"]
+    by3 = sum(4 * (C3["B"] * n3 * S * N3 + C3["B"] * S * D3) for S in range(C3_GEN["prompt"], C3_GEN["prompt"] + C3_GEN["new"]))
+    by3 *= C3_GEN["n_layer"]
+    del k3, v3
     return {
         "value": F / med / 1e12,
         "unit": "TFLOP/s",
@@ -185,6 +321,32 @@ def cpu_baseline(reps: int = 3) -> dict:
                 "sample": f"C2 model (L=6 D=256 nh=4 N=8192) fp32 forward of B=1 of 32 sequences, T=512 "
                 f"(oracle/bdh_model_oracle.py), median of {reps} after 1 warmup, {mmed * 1e3:.0f} ms per sequence",
             }
+        },
+        "configs": {
+            "c3_decode_attention": {
+                "value": C3_GEN["B"] * C3_GEN["new"] / total3,
+                "unit": "tok/s (decode attention only)",
+                "seconds_per_generate": total3,
+                "gbs_fp32_cache": by3 / total3 / 1e9,
+                "per_layer_step_ms": {str(S): t * 1e3 for S, t in per_s.items()},
+                "sample": f"C3 decode attention, fp32 (oracle tril_decode_cpu): one layer step at S = 256/384/511 on 8 "
+                f"of 64 sequences, times 8, median of {reps} after 1 warmup; a line through the three, summed over "
+                f"S = 256..511 and 6 layers",
+            },
+            "c4_train_op": {
+                "value": F4 / m4 / 1e12,
+                "unit": "TFLOP/s",
+                "ms_per_call": m4 * 1e3,
+                "sample": f"C4 fp32 forward + analytic merged backward (oracle tril_score_v_cpu + self_attn_backward) "
+                f"on B=1 of 16 (nh=4 T=1024 N=8192 D=256), median of 2 after 1 warmup, {m4:.2f} s per call",
+            },
+            "c5_attention_op": {
+                "value": F5 / m5 / 1e12,
+                "unit": "TFLOP/s",
+                "ms_per_call": m5 * 1e3,
+                "sample": f"C5 fp32 RoPE + strict-tril attention (oracle tril_rope_score_v) on B=1 of 4 (nh=8 T=2048 "
+                f"N=8192 D=512), median of 2 after 1 warmup, {m5:.2f} s per call",
+            },
         },
     }
 
@@ -250,7 +412,8 @@ def main() -> int:
         log(f"[bench] calibration multiply: {CALIB_BYTES} bytes read, {CALIB_BYTES} bytes written")
         del src, dst
 
-    settle(step)
+    settled = settle(step)
+    log(f"[bench] settle: {settled}")
     launches0 = ext.launch_count()
     ms = time_steps(step, args.steps, args.warmup, settle_s=0)
     assert ext.launch_count() - launches0 == args.steps + args.warmup, "HIP library calls missing"
@@ -278,6 +441,9 @@ def main() -> int:
         "algorithmic_flops_per_launch": F_scores,
     }
     log(f"[bench] kernels: {roofline['kernels_us']} -> {kname} {achieved:.1f} TFLOP/s")
+    device = sample_sclk(step)
+    device["settle"] = settled
+    log(f"[bench] device: {device}")
 
     extra: dict = {}
     if not args.no_extra:
@@ -293,6 +459,28 @@ def main() -> int:
         cpu = cpu_baseline()
         log(f"[bench] cpu baseline: {cpu['value']:.4f} TFLOP/s on {cpu['cores']} threads; "
             f"C2 model {cpu['models']['c2_prefill']['tok_s']:.0f} tok/s")
+
+    if cpu is not None:
+        # the GPU figure of each config beside its CPU sample (same unit)
+        side = {"c1": {"unit": "TFLOP/s", "gpu_bf16": value, "cpu_fp32": cpu["value"]}}
+        cc = cpu["configs"]
+        if "c1_fp32_fused_rope" in extra:
+            side["c1"]["gpu_fp32"] = extra["c1_fp32_fused_rope"]["tflops"]
+        if "c4_train_op_fwd_bwd" in extra:
+            side["c4"] = {"unit": "TFLOP/s", "gpu_bf16": extra["c4_train_op_fwd_bwd"]["tflops"],
+                          "cpu_fp32": cc["c4_train_op"]["value"]}
+        if "c5_attention_op" in extra:
+            side["c5"] = {"unit": "TFLOP/s", "gpu_bf16": extra["c5_attention_op"]["tflops"],
+                          "cpu_fp32": cc["c5_attention_op"]["value"]}
+        c3g = models.get("c3_generate", {}).get("hip", {})
+        if c3g.get("decode_attention_ms"):
+            side["c3"] = {"unit": "tok/s (decode attention only)",
+                          "gpu_bf16_cache": C3_GEN["B"] * C3_GEN["new"] / (c3g["decode_attention_ms"] * 1e-3),
+                          "cpu_fp32": cc["c3_decode_attention"]["value"]}
+        if "c2_prefill" in models:
+            side["c2"] = {"unit": "tok/s", "gpu_bf16": models["c2_prefill"]["hip"]["tok_s"],
+                          "cpu_fp32": cpu["models"]["c2_prefill"]["tok_s"]}
+        cpu["gpu_beside_cpu"] = side
 
     line = {
         "metric": METRIC,
@@ -318,6 +506,7 @@ def main() -> int:
             "frac_of_bf16_peak": value / PEAK_BF16_TFLOPS,
         },
         "roofline": roofline,
+        "device": device,
         "cpu_baseline": cpu,
         "extra": extra,
         "models": models,
@@ -347,6 +536,30 @@ def run_extra(torch, ext, kernels, dev, steps, warmup, x, v) -> dict:
     ms_e = time_steps(eager, steps, warmup)
     out["c1_torch_eager_gpu_on_qr"] = {"us": ms_e * 1e3, "tflops": F / ms_e / 1e9}
     log(f"[bench] unfused {ms * 1e3:.1f} us, rope {ms_r * 1e3:.1f} us, torch eager {ms_e * 1e3:.1f} us")
+
+    # C1 as BASELINE.json states it: fp32 in and out (the fp32 HIP path),
+    # against the fp32 MFMA peak.
+    x32, v32 = x.float(), v.float()
+    ms_32 = time_steps(lambda: kernels.bdh_attn_rope(x32, v32, freqs, 0, impl="hip"), max(3, steps // 2), 2)
+    out["c1_fp32_fused_rope"] = {"us": ms_32 * 1e3, "tflops": F / ms_32 / 1e9,
+                                 "frac_fp32_peak": F / ms_32 / 1e9 / PEAK_FP32_TFLOPS}
+    log(f"[bench] C1 fp32: {ms_32 * 1e3:.1f} us, {F / ms_32 / 1e9:.1f} TFLOP/s")
+    del x32, v32
+
+    # C5 attention op alone at its full width (B=4 nh=8 T=2048 N=8192 D=512,
+    # bf16, fused RoPE): the attention of one C5 layer.
+    B5, n5, T5, D5 = C5["B"], C5["nh"], C5["T"], C5["D"]
+    N5 = C5["mult"] * D5 // n5
+    g5 = torch.Generator(device=dev).manual_seed(0)
+    x5 = torch.relu(0.32 * torch.randn(B5, n5, T5, N5, generator=g5, device=dev)).to(torch.bfloat16)
+    v5 = torch.randn(B5, 1, T5, D5, generator=g5, device=dev).to(torch.bfloat16)
+    f5 = kernels.get_freqs(N5).to(dev)
+    F5 = attn_flops(B5, n5, T5, N5, D5)
+    ms_5 = time_steps(lambda: kernels.bdh_attn_rope(x5, v5, f5, 0, impl="hip"), max(3, steps // 4), 2)
+    out["c5_attention_op"] = {"us": ms_5 * 1e3, "tflops": F5 / ms_5 / 1e9,
+                              "frac_bf16_peak": F5 / ms_5 / 1e9 / PEAK_BF16_TFLOPS}
+    log(f"[bench] C5 attention op: {ms_5 * 1e3:.1f} us, {F5 / ms_5 / 1e9:.1f} TFLOP/s")
+    del x5, v5
 
     out.update(run_decode(torch, kernels, dev, steps, warmup))
 
@@ -472,6 +685,8 @@ def run_models(torch, ext, dev, only=None) -> dict:
         del m, idx
         torch.cuda.empty_cache()
 
+    if only is None or only == "c2":
+        out["c2_train_step"] = run_train_step(torch, ext, dev, build)
     if only is not None and only != "c3":
         return out
     c = C3_GEN
@@ -523,6 +738,42 @@ def run_models(torch, ext, dev, only=None) -> dict:
     del m
     torch.cuda.empty_cache()
     return out
+
+
+def run_train_step(torch, ext, dev, build) -> dict:
+    """Model-level training step at the C2 configuration (L=6 D=256 nh=4
+    N=8192, B=32 T=512) under bf16 autocast: forward with cross entropy,
+    backward through the HIP attention autograd functions, one AdamW step
+    (the work of train.py's train_step, reference train.py:997-1034)."""
+    c = C2
+    m = build(c)
+    opt = torch.optim.AdamW(m.parameters(), lr=1e-4, foreach=True)
+    g = torch.Generator(device=dev).manual_seed(3)
+    idx = torch.randint(0, 256, (c["B"], c["T"]), generator=g, device=dev)
+    tgt = torch.randint(0, 256, (c["B"], c["T"]), generator=g, device=dev)
+
+    def step():
+        opt.zero_grad(set_to_none=True)
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            _, loss = m(idx, tgt, impl="hip")
+        loss.backward()
+        opt.step()
+
+    log("[bench] c2_train_step hip ...")
+    launches0 = ext.launch_count()
+    ms = time_steps(step, 3, 1, settle_s=0)
+    assert ext.launch_count() > launches0, "HIP library calls missing in the training step"
+    leg = {"B": c["B"], "T": c["T"], "n_layer": c["n_layer"], "amp": "bf16", "optimizer": "AdamW",
+           "ms": ms, "tok_s": c["B"] * c["T"] / (ms * 1e-3)}
+    ext.profile_enable(True)
+    step()
+    rec = ext.profile_collect()
+    ext.profile_enable(False)
+    leg["attention_kernels_ms"] = sum(t for n, t in rec if n not in ("k_gated_gemm", "k_relu_mul"))
+    log(f"[bench] c2_train_step: {ms:.1f} ms, {leg['tok_s']:.0f} tok/s (attention kernels {leg['attention_kernels_ms']:.2f} ms)")
+    del m, opt
+    torch.cuda.empty_cache()
+    return leg
 
 
 if __name__ == "__main__":
