@@ -477,14 +477,22 @@ def tril_score_v_bwd_saved(
 
 
 def tril_rope_score_v_bwd(
-    x: torch.Tensor, v: torch.Tensor, dout: torch.Tensor, freqs: torch.Tensor, rope_start: int = 0
+    x: torch.Tensor,
+    v: torch.Tensor,
+    dout: torch.Tensor,
+    freqs: torch.Tensor,
+    rope_start: int = 0,
+    *,
+    dv: Optional[torch.Tensor] = None,
 ) -> Tuple[torch.Tensor, torch.Tensor]:
-    """Gradients ``(dx, dv)`` of :func:`tril_rope_score_v`."""
-    dev = _require_device(x, v, dout)
+    """Gradients ``(dx, dv)`` of :func:`tril_rope_score_v` (``dv`` may be passed
+    in any float dtype; it defaults to ``v``'s)."""
+    dev = _require_device(x, v, dout, dv)
     B, H, T, N = x.shape
     f, fptr = _freqs_ptr(freqs, N, dev)
     dx = torch.empty_like(x, memory_format=torch.contiguous_format)
-    dv = torch.empty_like(v, memory_format=torch.contiguous_format)
+    if dv is None:
+        dv = torch.empty_like(v, memory_format=torch.contiguous_format)
     with torch.cuda.device(dev):
         need = _lib.bdh_tril_rope_score_v_bwd_workspace(B, H, v.size(1), T, N, v.size(-1), _dtype_code(x))
         ws, nb = _workspace(need, dev)

@@ -231,11 +231,14 @@ struct BwdPlan {
   FwdPlan f;
   int64_t tpad;
   size_t g_off, ws_bytes;
+  // bf16 with RoPE on the MFMA path: [table + score tiles | R(x) bf16 |
+  // G bf16 | R^T-bound dQ fp32]
+  size_t r_sy = 0, r_qr = 0, r_g = 0, r_dq = 0, r_end = 0;
 };
 
 // saved: the score tiles come from the forward's workspace, so the first
-// region is not needed.
-BwdPlan plan_bwd(int64_t B, int64_t H, int64_t T, int64_t K, bool bf, bool saved = false) {
+// region is not needed.  rope (bf16): room for the MFMA route as well.
+BwdPlan plan_bwd(int64_t B, int64_t H, int64_t T, int64_t K, bool bf, bool saved = false, bool rope = false) {
   BwdPlan p;
   p.f = plan_fwd(B, H, T, K, bf);
   p.tpad = p.f.nt * kTile;
@@ -243,7 +246,70 @@ BwdPlan plan_bwd(int64_t B, int64_t H, int64_t T, int64_t K, bool bf, bool saved
   // of the MFMA path, whichever is larger
   p.g_off = saved ? 0 : align_up(std::max(p.f.ws_bytes, bf ? sy_bwd_workspace(B, H, T, K) : size_t(0)), 256);
   p.ws_bytes = p.g_off + size_t(B * H) * size_t(p.tpad) * size_t(p.tpad) * (bf ? 2 : 4);
+  if (rope && bf) {
+    p.r_sy = sy_rope_scores_workspace(B, H, T, K);
+    if (p.r_sy > 0) {
+      const size_t x_elems = size_t(B * H) * size_t(T) * size_t(K);
+      p.r_qr = align_up(p.r_sy, 256);
+      p.r_g = align_up(p.r_qr + x_elems * 2, 256);
+      p.r_dq = align_up(p.r_g + size_t(B * H) * size_t(p.tpad) * size_t(p.tpad) * 2, 256);
+      p.r_end = p.r_dq + x_elems * 4;
+      p.ws_bytes = std::max(p.ws_bytes, p.r_end);
+    }
+  }
   return p;
+}
+
+bool rows16b(const bdh_tensor4* t) {
+  if ((reinterpret_cast<uintptr_t>(t->data) & 15) != 0) return false;
+  for (int i = 0; i < 3; ++i)
+    if (t->size[i] > 1 && (t->stride[i] * esize(t->dtype)) % 16 != 0) return false;
+  return true;
+}
+
+// bf16 self attention with RoPE on the MFMA path: one absolute-position score
+// kernel recomputes M's tiles and writes R(x) into the workspace; dV from the
+// tiles, G from dO and V, dR = G R(x) in fp32, then dx = R^T(dR) with the
+// score kernel's (cos, sin) table.  kNotEligible (nothing launched) outside
+// its shapes.
+int rope_fast_bwd(const bdh_tensor4* x, const bdh_tensor4* v, const bdh_tensor4* dout, const bdh_tensor4* dx,
+                  const bdh_tensor4* dv, const float* freqs, int64_t rope_start, void* ws, size_t ws_bytes,
+                  const BwdPlan& p, hipStream_t s) {
+  const int64_t B = x->size[0], H = x->size[1], T = x->size[2], N = x->size[3];
+  const int64_t D = v->size[3];
+  if (p.r_end == 0 || ws_bytes < p.r_end) return kNotEligible;
+  if (dout->dtype != BDH_BF16 || v->dtype != BDH_BF16) return kNotEligible;
+  if (D < 64 || D > 256 || D % 64 != 0 || N % 256 != 0 || T > 65535) return kNotEligible;
+  if (!rows16b(dout) || !rows16b(v) || !rows16b(dx) || !rows16b(dv)) return kNotEligible;
+  if (dx->dtype != BDH_BF16 && dx->dtype != BDH_F32) return kNotEligible;
+  if (p.tpad % 32 != 0 || p.tpad * p.tpad * 2 >= (int64_t(1) << 31)) return kNotEligible;
+  if (((T - 1) * std::max(dout->stride[2], v->stride[2]) + D) * 2 >= (int64_t(1) << 31)) return kNotEligible;
+  char* w = static_cast<char*>(ws);
+  bdh_tensor4 qr{};
+  qr.data = w + p.r_qr;
+  qr.size[0] = B;
+  qr.size[1] = H;
+  qr.size[2] = T;
+  qr.size[3] = N;
+  qr.stride[3] = 1;
+  qr.stride[2] = N;
+  qr.stride[1] = T * N;
+  qr.stride[0] = H * T * N;
+  qr.dtype = BDH_BF16;
+  bdh_tensor4 gq = qr;
+  gq.data = w + p.r_dq;
+  gq.dtype = BDH_F32;
+  const void* tiles = nullptr;
+  int rc = sy_rope_scores(x, v, freqs, rope_start, &qr, ws, p.r_sy, s, &tiles);
+  if (rc != BDH_OK) return rc;  // kNotEligible before anything ran
+  // the checks above cover the remaining steps; a step that still declines
+  // is reported as an error rather than leaving partial results
+  auto step = [](int r) { return r == kNotEligible ? int(BDH_ERR_SHAPE) : r; };
+  if (numel4(dv) > 0) BDH_TRY(step(sy_bwd_dv(&qr, v, dout, dv, nullptr, 0, s, tiles)));
+  if (numel4(dx) == 0) return BDH_OK;
+  BDH_TRY(step(sy_bwd_g(dout, v, w + p.r_g, p.tpad, s)));
+  BDH_TRY(step(sy_dq(w + p.r_g, p.tpad, &qr, &gq, s)));
+  return step(sy_rope_unrotate(static_cast<const float*>(gq.data), ws, B, H, T, N, dx, s));
 }
 
 bool vec4_rows(const bdh_tensor4* t) {
@@ -344,9 +410,14 @@ int run_bwd(const bdh_tensor4* q, const bdh_tensor4* k, const bdh_tensor4* v, co
   const bool rope = freqs != nullptr;
   if (numel4(dq) == 0 && numel4(dv) == 0) return BDH_OK;
   if (saved != nullptr && !(self && bf && !rope)) return BDH_ERR_ARG;
-  const BwdPlan p = plan_bwd(B, H, T, N, bf, saved != nullptr);
+  const BwdPlan p = plan_bwd(B, H, T, N, bf, saved != nullptr, rope && self);
   if (ws == nullptr || ws_bytes < p.ws_bytes) return BDH_ERR_WORKSPACE;
   const int64_t BH = B * H;
+
+  if (self && bf && rope) {
+    const int rc = rope_fast_bwd(q, v, dout, dq, dv, freqs, rope_start, ws, ws_bytes, p, s);
+    if (rc != kNotEligible) return rc;
+  }
 
   // bf16 self attention without RoPE: score tiles by the forward score kernel
   // (or saved by the forward) and dV from them (syrk.hip), in place of steps
@@ -519,7 +590,7 @@ extern "C" size_t bdh_tril_rope_score_v_bwd_workspace(int64_t B, int64_t H, int6
                                                       int64_t N, int64_t Dv, int32_t x_dtype) {
   (void)Hv;
   (void)Dv;
-  return plan_bwd(B, H, T, N, x_dtype == BDH_BF16).ws_bytes;
+  return plan_bwd(B, H, T, N, x_dtype == BDH_BF16, false, true).ws_bytes;
 }
 
 extern "C" int bdh_tril_rope_score_v_bwd(const bdh_tensor4* x, const bdh_tensor4* v, const bdh_tensor4* dout,

@@ -242,6 +242,43 @@ __global__ __launch_bounds__(256) void k_rope_table(const float* __restrict__ fr
   cs[(int64_t(m >> 4) * T + t) * 16 + (m & 15)] = rope_cs(float(rope_start + t), freqs[2 * m]);
 }
 
+// The transpose rotation RoPE^T (the backward of RoPE) with the table's
+// (cos, sin): dx[2m] = g[2m] c + g[2m+1] s, dx[2m+1] = g[2m+1] c - g[2m] s,
+// fp32 arithmetic, one rounding to TO.  g is fp32, contiguous (B*H, T, N);
+// dx any (B, H, T) strides with 16-byte rows.  Thread: 8 elements (4 pairs)
+// of row t of slab z; grid (N / 2048 rounded up, T, B*H).
+template <typename TO>
+__global__ __launch_bounds__(256) void k_rope_unrotate(const float* __restrict__ g, const uint32_t* __restrict__ cs,
+                                                       int H, int T, int N, TO* __restrict__ dx, int64_t o0,
+                                                       int64_t o1, int64_t o2) {
+  const int t = blockIdx.y, z = blockIdx.z;
+  const int e = (blockIdx.x * 256 + threadIdx.x) * 8;
+  if (e >= N) return;
+  const int m = e >> 1;  // first pair; m % 4 == 0, so its four entries are one 16-byte run
+  const float* gp = g + (int64_t(z) * T + t) * N + e;
+  const float4 g0 = *reinterpret_cast<const float4*>(gp);
+  const float4 g1 = *reinterpret_cast<const float4*>(gp + 4);
+  const u32x4 c4 = *reinterpret_cast<const u32x4*>(cs + (int64_t(m >> 4) * T + t) * 16 + (m & 15));
+  const float gv[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+  const uint32_t cw[4] = {c4.x, c4.y, c4.z, c4.w};
+  float y[8];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const float c = __uint_as_float(cw[q] << 16), sn = __uint_as_float(cw[q] & 0xffff0000u);
+    y[2 * q] = fmaf(gv[2 * q], c, gv[2 * q + 1] * sn);
+    y[2 * q + 1] = fmaf(gv[2 * q + 1], c, -(gv[2 * q] * sn));
+  }
+  const int b = z / H, h = z - b * H;
+  TO* op = dx + b * o0 + h * o1 + int64_t(t) * o2 + e;
+  if constexpr (sizeof(TO) == 2) {
+    *reinterpret_cast<u32x4*>(op) =
+        u32x4{pack_bf2(y[0], y[1]), pack_bf2(y[2], y[3]), pack_bf2(y[4], y[5]), pack_bf2(y[6], y[7])};
+  } else {
+    *reinterpret_cast<float4*>(op) = make_float4(y[0], y[1], y[2], y[3]);
+    *reinterpret_cast<float4*>(op + 4) = make_float4(y[4], y[5], y[6], y[7]);
+  }
+}
+
 // Diagonal tiles (Q = K) in pairs: the 36 lower 32x32 blocks of one diagonal
 // tile are split into four wave programs of 9 blocks; waves 0-3 run them on
 // the first tile of the pair and waves 4-7 on the second, so each SIMD issues
@@ -1606,6 +1643,43 @@ int sy_cold(const bdh_tensor4* q, const bdh_tensor4* k, const bdh_tensor4* v, co
             const float* freqs, int64_t rope_start, const bdh_tensor4* qr, void* ws, size_t ws_bytes,
             hipStream_t s) {
   return sy_run(q, k, v, out, freqs, rope_start, qr, 0, ws, ws_bytes, s);
+}
+
+// Backward of the fused RoPE op, first step: the score tiles of R(x) R(x)^T
+// (absolute positions) with R(x) written to qr, without score x V.  The
+// workspace holds the (cos, sin) table of the absolute positions first, then
+// the score tiles.
+size_t sy_rope_scores_workspace(int64_t B, int64_t H, int64_t T, int64_t N) {
+  const SyPlan p = sy_plan(B * H, T, N, true, true, 0);
+  return p.ok ? p.ws_bytes : 0;
+}
+
+int sy_rope_scores(const bdh_tensor4* x, const bdh_tensor4* v, const float* freqs, int64_t rope_start,
+                   const bdh_tensor4* qr, void* ws, size_t ws_bytes, hipStream_t s, const void** tiles) {
+  SyPlan p;
+  bool self = false;
+  if (qr == nullptr || !sy_cold_check(x, x, v, true, qr, p, self) || !self) return kNotEligible;
+  bdh_tensor4 none = *v;  // shape of an empty output: no score x V
+  none.size[2] = 0;
+  const int rc = sy_run(x, x, v, &none, freqs, rope_start, qr, 0, ws, ws_bytes, s);
+  if (rc == BDH_OK && tiles != nullptr) *tiles = static_cast<const char*>(ws) + p.table_bytes;
+  return rc;
+}
+
+// dx = RoPE^T(g) with the table sy_rope_scores left at the start of ws.
+int sy_rope_unrotate(const float* g, const void* ws, int64_t B, int64_t H, int64_t T, int64_t N,
+                     const bdh_tensor4* dx, hipStream_t s) {
+  if (N % 8 != 0 || T > 65535 || B * H > 65535 || !rows16(dx)) return kNotEligible;
+  if (dx->dtype != BDH_BF16 && dx->dtype != BDH_F32) return kNotEligible;
+  const dim3 grid(unsigned((N / 8 + 255) / 256), unsigned(T), unsigned(B * H));
+  const uint32_t* cs = static_cast<const uint32_t*>(ws);
+  if (dx->dtype == BDH_BF16)
+    BDH_LAUNCH("k_rope_unrotate", k_rope_unrotate<bf16_t>, grid, dim3(256), 0, s, g, cs, int(H), int(T), int(N),
+               static_cast<bf16_t*>(dx->data), dx->stride[0], dx->stride[1], dx->stride[2]);
+  else
+    BDH_LAUNCH("k_rope_unrotate", k_rope_unrotate<float>, grid, dim3(256), 0, s, g, cs, int(H), int(T), int(N),
+               static_cast<float*>(dx->data), dx->stride[0], dx->stride[1], dx->stride[2]);
+  return BDH_OK;
 }
 
 size_t sy_past_workspace(int64_t B, int64_t H, int64_t Tk, int64_t past, int64_t N, int64_t Dv) {

@@ -153,8 +153,13 @@ class TrilRopeSelfAttnFn(torch.autograd.Function):
     @staticmethod
     def backward(ctx, dO):  # type: ignore[override]
         x, V, freqs = ctx.saved_tensors
-        dx, dV = hip_attn.tril_rope_score_v_bwd(x, V, dO.to(x.dtype), freqs, ctx.rope_start)
-        return dx, dV.to(V.dtype), None, None, None
+        # bf16 x: V enters the products as bf16, as in the forward (and as the
+        # reference's autocast matmul casts it), which lets the backward run on
+        # the MFMA kernels; dV comes back in V's own dtype
+        Vc = V.to(x.dtype) if x.dtype == torch.bfloat16 else V
+        dV = torch.empty_like(V, memory_format=torch.contiguous_format)
+        dx, dV = hip_attn.tril_rope_score_v_bwd(x, Vc, dO.to(x.dtype), freqs, ctx.rope_start, dv=dV)
+        return dx, dV, None, None, None
 
 
 def strict_tril_attn(Q, K, V, *, impl: Optional[str] = None, use_fn: Optional[bool] = None):

@@ -201,10 +201,10 @@ def tril_score_v_bwd_saved(x, v, dout, scores):
     return ext.tril_score_v_bwd_saved(_last_dim_unit(x), _last_dim_unit(v), _last_dim_unit(dout), scores)
 
 
-def tril_rope_score_v_bwd(x, v, dout, freqs, rope_start: int = 0):
+def tril_rope_score_v_bwd(x, v, dout, freqs, rope_start: int = 0, *, dv=None):
     ext = _require(x, v, dout)
     return ext.tril_rope_score_v_bwd(
-        _last_dim_unit(x), _last_dim_unit(v), _last_dim_unit(dout), freqs, int(rope_start)
+        _last_dim_unit(x), _last_dim_unit(v), _last_dim_unit(dout), freqs, int(rope_start), dv=dv
     )
 
 
