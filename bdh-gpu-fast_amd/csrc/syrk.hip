@@ -231,7 +231,7 @@ __device__ __forceinline__ f32x16 mma(bf16x8 a, bf16x8 b, f32x16 c) {
 // both make their entries here, so they are the same bits.
 __device__ __forceinline__ uint32_t rope_cs(float pos, float freq) {
   const float ph = __fmul_rn(pos, freq);
-  const float fr = ph - floorf(ph);
+  const float fr = __builtin_amdgcn_fractf(ph);  // ph - floor(ph): ph >= 0
   return pack_bf2(__builtin_amdgcn_cosf(fr), __builtin_amdgcn_sinf(fr));
 }
 
