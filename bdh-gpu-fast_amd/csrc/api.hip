@@ -29,18 +29,14 @@ hipEvent_t take_event() {
 }
 }  // namespace
 
-int prof_begin(const char* name, hipStream_t s) {
+int prof_begin(const char* name, hipEvent_t* start, hipEvent_t* stop) {
   if (!g_prof_on || g_recs.size() >= kMaxRecs) return -1;
   ProfRec r{name, take_event(), take_event()};
   if (!r.start || !r.stop) return -1;
-  if (hipEventRecord(r.start, s) != hipSuccess) return -1;
   g_recs.push_back(r);
+  *start = r.start;
+  *stop = r.stop;
   return int(g_recs.size()) - 1;
-}
-
-void prof_end(int slot, hipStream_t s) {
-  if (slot < 0 || size_t(slot) >= g_recs.size()) return;
-  (void)hipEventRecord(g_recs[slot].stop, s);
 }
 
 }  // namespace bdh

@@ -1,6 +1,7 @@
 // Shared host/device helpers for the gfx950 BDH attention library.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -64,8 +65,9 @@ struct View {
 namespace bdh {
 
 // Kernel launch bookkeeping shared by all entry points (profiling events).
-int prof_begin(const char* name, hipStream_t s);
-void prof_end(int slot, hipStream_t s);
+// Profiling (bdh_profile_enable): the start and stop events of the next
+// launch named `name`, or -1 (no events) when profiling is off.
+int prof_begin(const char* name, hipEvent_t* start, hipEvent_t* stop);
 
 inline int64_t numel4(const bdh_tensor4* t) {
   return t->size[0] * t->size[1] * t->size[2] * t->size[3];
@@ -129,12 +131,18 @@ inline size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
     if (_rc != BDH_OK) return _rc;  \
   } while (0)
 
-// Launch a kernel on `stream`, bracketed by profiling events when enabled.
-#define BDH_LAUNCH(name, kernel, grid, block, shmem, stream, ...)          \
-  do {                                                                    \
-    int _slot = bdh::prof_begin(name, stream);                            \
-    hipLaunchKernelGGL(kernel, grid, block, shmem, stream, __VA_ARGS__);   \
-    hipError_t _e = hipGetLastError();                                    \
-    bdh::prof_end(_slot, stream);                                         \
-    if (_e != hipSuccess) return BDH_ERR_LAUNCH;                          \
+// Launch a kernel on `stream`.  When profiling is enabled the launch carries
+// start and stop events that the runtime stamps when the kernel itself
+// starts and ends (hipExtLaunchKernelGGL), so the recorded time is the
+// kernel's execution, without the dispatch gaps around it.
+#define BDH_LAUNCH(name, kernel, grid, block, shmem, stream, ...)                                   \
+  do {                                                                                            \
+    hipEvent_t _e0 = nullptr, _e1 = nullptr;                                                      \
+    const int _slot = bdh::prof_begin(name, &_e0, &_e1);                                          \
+    if (_slot >= 0)                                                                               \
+      hipExtLaunchKernelGGL(kernel, grid, block, shmem, stream, _e0, _e1, 0, __VA_ARGS__);         \
+    else                                                                                          \
+      hipLaunchKernelGGL(kernel, grid, block, shmem, stream, __VA_ARGS__);                        \
+    hipError_t _e = hipGetLastError();                                                            \
+    if (_e != hipSuccess) return BDH_ERR_LAUNCH;                                                  \
   } while (0)

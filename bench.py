@@ -13,9 +13,14 @@ first runs untimed until two consecutive 20-step windows agree within 2 %
 
 The JSON line also carries:
   * ``roofline``: the dominant kernel (``k_sy_scores``, the score tiles QR QR^T)
-    timed with HIP events on its launch stream over a timed region of the same
-    K steps; achieved = its algorithmic flops B*nh*N*T*(T-1) / mean duration,
-    against the 2.5 PFLOP/s bf16 dense MFMA peak.  ``traffic`` is the HBM
+    timed over the K timed steps themselves: each launch carries HIP start/stop
+    events that the runtime stamps at the kernel's own start and end
+    (hipExtLaunchKernelGGL on the launch stream, no extra stream work);
+    achieved = its algorithmic flops B*nh*N*T*(T-1) / mean duration, against
+    the 2.5 PFLOP/s bf16 dense MFMA peak.  ``kernels_us_isolated`` and
+    ``frac_isolated`` repeat the measurement with a synchronisation after
+    every step (no kernel overlapping the previous one's tail, as under a
+    profiler's kernel trace).  ``traffic`` is the HBM
     bytes per launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE runs
     (profiles/<kernel>_c1_bf16_pmc.txt) when present, else null.
   * ``device``: CU count, architecture, the shader clock amd-smi reports while
@@ -103,10 +108,13 @@ def settle(fn, window: int = 20, tol: float = 0.02, max_s: float = 3.0, min_s: f
     return {"windows": len(hist), "last_ms": hist[-2:], "converged": converged}
 
 
-def sample_sclk(fn, seconds: float = 1.5) -> dict:
+def sample_sclk(fn, seconds: float = 1.5, n_samples: int = 6) -> dict:
     """Shader clock while ``fn`` runs back to back: amd-smi's per-XCD gfx
-    clocks (MHz), sampled from a thread during a busy window.  Best effort:
-    None fields when amd-smi is not available."""
+    clocks (MHz, averaged over the XCDs), sampled ``n_samples`` times from a
+    thread during a busy window.  One amd-smi reading is an instantaneous
+    value and can land in a momentary idle dip, so the line reports the
+    median and every sample.  Best effort: None fields when amd-smi is not
+    available."""
     import subprocess
     import threading
 
@@ -115,7 +123,7 @@ def sample_sclk(fn, seconds: float = 1.5) -> dict:
     samples: list = []
 
     def poll():
-        for _ in range(3):
+        for _ in range(n_samples):
             try:
                 r = subprocess.run(["amd-smi", "metric", "-g", "0", "--clock", "--json"], capture_output=True,
                                    text=True, timeout=10)
@@ -140,8 +148,8 @@ def sample_sclk(fn, seconds: float = 1.5) -> dict:
     th.join(timeout=1)
     props = torch.cuda.get_device_properties(0)
     return {
-        "sclk_mhz_busy": round(statistics.mean(samples), 1) if samples else None,
-        "sclk_samples": len(samples),
+        "sclk_mhz_busy": round(statistics.median(samples), 1) if samples else None,
+        "sclk_samples_mhz": [round(x, 1) for x in samples],
         "cus": int(props.multi_processor_count),
         "arch": str(getattr(props, "gcnArchName", "")),
         "device": str(props.name),
@@ -169,8 +177,11 @@ def time_steps(fn, steps: int, warmup: int, settle_s: float = 0.2) -> float:
     return t0.elapsed_time(t1) / steps
 
 
-def kernel_means(fn, steps: int) -> dict:
-    """Mean per-kernel duration (ms) from the library's HIP events on the launch stream."""
+def kernel_means(fn, steps: int, isolated: bool = False) -> dict:
+    """Mean per-kernel duration (ms) from the library's HIP events: each launch
+    carries start/stop events the runtime stamps when the kernel itself starts
+    and ends (hipExtLaunchKernelGGL).  ``isolated``: a synchronisation after
+    every step, so no kernel overlaps the previous one's tail."""
     import torch
     import bdh_hip_ext as ext
 
@@ -179,10 +190,16 @@ def kernel_means(fn, steps: int) -> dict:
     try:
         for _ in range(steps):
             fn()
+            if isolated:
+                torch.cuda.synchronize()
         torch.cuda.synchronize()
         recs = ext.profile_collect()
     finally:
         ext.profile_enable(False)
+    return _agg(recs, steps)
+
+
+def _agg(recs, steps: int) -> dict:
     agg: dict = {}
     for name, ms in recs:
         agg.setdefault(name, []).append(ms)
@@ -362,6 +379,13 @@ def main() -> int:
     ap.add_argument("--model", choices=("c2", "c5", "c3"), default=None,
                     help="run only this model-harness leg on the HIP path (for profiling) and print its JSON")
     ap.add_argument(
+        "--pmc-targets",
+        action="store_true",
+        help="run only the profiled kernels a few times each (for rocprofv3 counter passes): the C1 fused "
+        "forward, the C4 training op, one C2 layer's gated GEMM, the C3 decode step at S=511, the C2 "
+        "training step's RoPE backward, and the calibration multiply",
+    )
+    ap.add_argument(
         "--calibrate",
         action="store_true",
         help="also run one elementwise multiply over CALIB_BYTES (the reference point that scales "
@@ -389,6 +413,9 @@ def main() -> int:
     if args.model is not None:
         print(json.dumps(run_models(torch, ext, dev, only=args.model)), flush=True)
         return 0
+    if args.pmc_targets:
+        run_pmc_targets(torch, ext, kernels, dev)
+        return 0
 
     B, nh, T, N, D = (C1[k] for k in ("B", "nh", "T", "N", "D"))
     gq = torch.Generator(device=dev).manual_seed(0)
@@ -415,13 +442,24 @@ def main() -> int:
     settled = settle(step)
     log(f"[bench] settle: {settled}")
     launches0 = ext.launch_count()
-    ms = time_steps(step, args.steps, args.warmup, settle_s=0)
+    # the per-kernel events ride on the launches of the timed steps (stamped
+    # by the runtime at kernel start and end; no extra stream work)
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    ext.profile_enable(True)
+    try:
+        ms = time_steps(step, args.steps, 0, settle_s=0)
+        live = _agg(ext.profile_collect(), args.steps)
+    finally:
+        ext.profile_enable(False)
     assert ext.launch_count() - launches0 == args.steps + args.warmup, "HIP library calls missing"
     F = attn_flops(B, nh, T, N, D)
     value = F / (ms * 1e-3) / 1e12
     log(f"[bench] fused RoPE tril-attn fwd C1 bf16: {ms * 1e3:.1f} us/step, {value:.1f} TFLOP/s")
 
-    means = kernel_means(step, args.steps)
+    means = live
+    isolated = kernel_means(step, args.steps, isolated=True)
     kname = max(means, key=lambda k: means[k][0] * means[k][1])  # dominant kernel of the step
     k_ms = means[kname][0]
     # the score tiles R R^T over the strict lower triangle: B*nh*N*T*(T-1) flops
@@ -438,6 +476,8 @@ def main() -> int:
         "traffic": traffic,
         "kernel_us": k_ms * 1e3,
         "kernels_us": {k: round(v[0] * 1e3, 2) for k, v in means.items()},
+        "kernels_us_isolated": {k: round(v[0] * 1e3, 2) for k, v in isolated.items()},
+        "frac_isolated": F_scores / (isolated[kname][0] * 1e-3) / 1e12 / PEAK_BF16_TFLOPS,
         "algorithmic_flops_per_launch": F_scores,
     }
     log(f"[bench] kernels: {roofline['kernels_us']} -> {kname} {achieved:.1f} TFLOP/s")
@@ -738,6 +778,64 @@ def run_models(torch, ext, dev, only=None) -> dict:
     del m
     torch.cuda.empty_cache()
     return out
+
+
+def run_pmc_targets(torch, ext, kernels, dev, reps: int = 3) -> None:
+    """The kernels the committed counter tables cover, ``reps`` calls each on
+    synthetic inputs of their configuration (rocprofv3 --pmc runs this with
+    --kernel-include-regex to pick them), then one calibration multiply over
+    CALIB_BYTES (the reference point that scales FETCH_SIZE / WRITE_SIZE)."""
+    bf = torch.bfloat16
+    g = torch.Generator(device=dev).manual_seed(0)
+    # C1 fused forward (k_sy_scores, k_sy_sv)
+    B, nh, T, N, D = (C1[k] for k in ("B", "nh", "T", "N", "D"))
+    x = torch.relu(0.32 * torch.randn(B, nh, T, N, generator=g, device=dev)).to(bf)
+    v = torch.randn(B, 1, T, D, generator=g, device=dev).to(bf)
+    f = kernels.get_freqs(N).to(dev)
+    for _ in range(reps):
+        kernels.bdh_attn_rope(x, v, f, 0, impl="hip")
+    del x, v
+    # C4 training op (k_sy_scores, k_dv_sy, G, k_dq_sy)
+    B4, n4, T4, N4, D4 = (C4[k] for k in ("B", "nh", "T", "N", "D"))
+    q4 = torch.relu(0.32 * torch.randn(B4, n4, T4, N4, generator=g, device=dev)).to(bf)
+    v4 = torch.randn(B4, 1, T4, D4, generator=g, device=dev).to(bf)
+    d4 = torch.randn(B4, n4, T4, D4, generator=g, device=dev).to(bf)
+    for _ in range(reps):
+        _, sc = ext.tril_score_v_save(q4, v4)
+        ext.tril_score_v_bwd_saved(q4, v4, d4, sc)
+    del q4, v4, d4, sc
+    # one C2 layer's gated product (k_gated_gemm): y (B, nh, T, D), encoder_v^T (nh, N, D), x (B, T, nh, N)
+    c = C2
+    N2 = c["mult"] * c["D"] // c["nh"]
+    y = torch.randn(c["B"], c["nh"], c["T"], c["D"], generator=g, device=dev).to(bf)
+    wt = (0.02 * torch.randn(c["nh"], N2, c["D"], generator=g, device=dev)).to(bf)
+    xb = torch.relu(torch.randn(c["B"], c["T"], c["nh"], N2, generator=g, device=dev)).to(bf)
+    for _ in range(reps):
+        kernels.gated_gemm(y, wt, xb)
+    del y, wt, xb
+    # the C2 training step's attention backward (fused RoPE, bf16): one layer
+    x2 = torch.relu(0.32 * torch.randn(c["B"], c["nh"], c["T"], N2, generator=g, device=dev)).to(bf)
+    v2 = torch.randn(c["B"], 1, c["T"], c["D"], generator=g, device=dev).to(bf)
+    d2 = torch.randn(c["B"], c["nh"], c["T"], c["D"], generator=g, device=dev).to(bf)
+    f2 = kernels.get_freqs(N2).to(dev)
+    for _ in range(reps):
+        ext.tril_rope_score_v_bwd(x2, v2, d2, f2, 0)
+    del x2, v2, d2
+    # C3 decode step at the longest past (k_decode_bf16)
+    Bd, nhd, Nd, Dd = (C3[k] for k in ("B", "nh", "N", "D"))
+    S = max(C3["S"])
+    kc = torch.relu(0.32 * torch.randn(Bd, nhd, S + 1, Nd, generator=g, device=dev)).to(bf)
+    vc = torch.randn(Bd, 1, S + 1, Dd, generator=g, device=dev).to(bf)
+    qd = torch.relu(0.32 * torch.randn(Bd, nhd, 1, Nd, generator=g, device=dev)).to(bf)
+    for _ in range(reps):
+        kernels.bdh_attn_decode(qd, kc.narrow(2, 0, S), vc.narrow(2, 0, S), impl="hip")
+    del kc, vc, qd
+    torch.cuda.synchronize()
+    src = torch.ones(CALIB_BYTES // 4, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    torch.mul(src, 2.0, out=dst)
+    torch.cuda.synchronize()
+    log(f"[bench] pmc targets done ({reps} calls each; calibration multiply over {CALIB_BYTES} bytes)")
 
 
 def run_train_step(torch, ext, dev, build) -> dict:
