@@ -224,7 +224,19 @@ __global__ __launch_bounds__(512, 2) void k_gated_gemm(const GatedArgs a) {
     if (s + 1 < nst) stage(s + 1, S1());
   }
 
-  // epilogue: relu(acc) as bf16 into the LDS output tile, then the gated product
+  // epilogue: the tile's x chunks are loaded first (all in flight at once,
+  // from clamped addresses), then relu(acc) goes as bf16 into the LDS output
+  // tile, then the gated product.  Thread tid takes 16-byte chunk tid & 15 of
+  // rows (tid >> 4) + 32 e.
+  constexpr int kEp = (kGM * kGN / 8) / 512;
+  const int cc = tid & 15, n = n0 + cc * 8;
+  uint4 xr[kEp];
+#pragma unroll
+  for (int e = 0; e < kEp; ++e) {
+    const int m = min(m0 + (tid >> 4) + 32 * e, a.M - 1);
+    const int b = m / a.T, tt = m - b * a.T;
+    xr[e] = *reinterpret_cast<const uint4*>(a.x + b * a.x0 + tt * a.x1 + h * a.x2 + min(n, a.N - 8));
+  }
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
@@ -237,18 +249,21 @@ __global__ __launch_bounds__(512, 2) void k_gated_gemm(const GatedArgs a) {
       }
   __syncthreads();
 #pragma unroll
-  for (int e = 0; e < (kGM * kGN / 8) / 512; ++e) {
-    const int ch = tid + 512 * e;
-    const int row = ch >> 4, cc = ch & 15;
-    const int m = m0 + row, n = n0 + cc * 8;
-    if (m >= a.M || n >= a.N) continue;
-    const int b = m / a.T, tt = m - b * a.T;
-    float fy[8], fx[8], fo[8];
+  for (int e = 0; e < kEp; ++e) {
+    const int row = (tid >> 4) + 32 * e;
+    const int m = m0 + row;
+    float fy[8], fo[8];
     load8(reinterpret_cast<const bf16_t*>(g_lds + row * kGOutRow + cc * 16), fy);
-    load8(a.x + b * a.x0 + tt * a.x1 + h * a.x2 + n, fx);
+    const uint32_t xw[4] = {xr[e].x, xr[e].y, xr[e].z, xr[e].w};
 #pragma unroll
-    for (int i = 0; i < 8; ++i) fo[i] = fx[i] * fy[i];
-    store8(a.o + b * a.o0 + tt * a.o1 + h * a.o2 + n, fo);
+    for (int i = 0; i < 4; ++i) {
+      fo[2 * i] = __uint_as_float(xw[i] << 16) * fy[2 * i];
+      fo[2 * i + 1] = __uint_as_float(xw[i] & 0xffff0000u) * fy[2 * i + 1];
+    }
+    if (m < a.M && n < a.N) {
+      const int b = m / a.T, tt = m - b * a.T;
+      store8(a.o + b * a.o0 + tt * a.o1 + h * a.o2 + n, fo);
+    }
   }
 }
 

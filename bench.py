@@ -21,8 +21,9 @@ The JSON line also carries:
     ``frac_isolated`` repeat the measurement with a synchronisation after
     every step (no kernel overlapping the previous one's tail, as under a
     profiler's kernel trace).  ``traffic`` is the HBM
-    bytes per launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE runs
-    (profiles/<kernel>_c1_bf16_pmc.txt) when present, else null.
+    bytes per launch from the committed rocprofv3 counter runs (read requests
+    by size, 128 x TCC_EA0_RDREQ_128B + 64 x ..._64B + 32 x ..._32B, plus
+    WRITE_SIZE; profiles/<kernel>_c1_bf16_pmc.txt) when present, else null.
   * ``device``: CU count, architecture, the shader clock amd-smi reports while
     the step runs back to back, and how the settle phase ended.
   * ``cpu_baseline``: the CPU oracle (numpy restatement of the reference CPU
