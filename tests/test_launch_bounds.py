@@ -1,0 +1,179 @@
+"""Host-side bounds of the library launches the model harness makes at the C2, C5 and C3 shapes.
+
+CPU only: the launch plans and index formulas of the kernels the harness's
+HIP legs run (csrc/syrk.hip: k_sy_scores work items, their x loads and
+partial-tile stores, k_sy_sv's partial, V and output accesses;
+csrc/decode.hip: k_decode_bf16's key, q and partial accesses) are restated
+here and evaluated over every work item, with the strides of the views the
+harness passes (x_sparse as the permuted (B, T, nh, N) encoder output, the
+packed KV cache's capacity-strided past views).  Each access must fall
+inside its buffer and every score tile must be computed exactly once.
+"""
+
+import pytest
+
+TILE, TILE_ELEMS = 256, 256 * 256
+FULL, DIAG2, DIAG1 = 0, 1, 2
+
+# (name, B, nh, T, N, D): the harness legs' attention shapes (bench.py C2, C5;
+# C3's prompt prefill)
+PREFILL = [("C2", 32, 4, 512, 8192, 256), ("C5", 4, 8, 2048, 8192, 512), ("C3 prompt", 64, 4, 256, 8192, 256)]
+
+
+def sy_plan(nslab, T, N, self_=True, max_split=8):
+    """csrc/syrk.hip sy_plan (s0 = 0): tiles, items per split, splits."""
+    nt = (T + TILE - 1) // TILE
+    ntl = nt * (nt + 1) // 2
+    nchunk = N // 64
+    nfull = ntl - nt if self_ else ntl
+    per_split = nfull + (nt + 1) // 2 if self_ else ntl
+    S = max(1, min(max_split, 256 // (nslab * per_split)))
+    S = min(S, nchunk)
+    return dict(nt=nt, ntl=ntl, nchunk=nchunk, nfull=nfull, per_split=per_split, nsplit=S, ips=per_split * S)
+
+
+def sy_item(p, T, itx, self_=True):
+    """csrc/syrk.hip sy_item: (ta, tb, split, kind) of work item itx of a slab."""
+    r, split = itx, 0
+    while r >= p["per_split"]:
+        r -= p["per_split"]
+        split += 1
+    if not self_ or r < p["nfull"]:
+        t = 0
+        while r >= (t if self_ else t + 1):
+            r -= t if self_ else t + 1
+            t += 1
+        return t, r, split, FULL
+    ta = 2 * (r - p["nfull"])
+    tb = ta + 1 if ta + 1 < p["nt"] else ta
+    return ta, tb, split, DIAG1 if tb == ta else DIAG2
+
+
+def check_scores(B, nh, T, N, strides, numel):
+    """Every k_sy_scores workgroup: its item, x rows and columns, partial tiles."""
+    nslab = B * nh
+    p = sy_plan(nslab, T, N)
+    S, ntl = p["nsplit"], p["ntl"]
+    grid = 8 * ((nslab + 7) // 8) * p["ips"]
+    seen = set()
+    for bid in range(grid):
+        xcd, kk = bid & 7, bid >> 3
+        grp = kk // p["ips"]
+        slab = grp * 8 + xcd
+        if slab >= nslab:
+            continue
+        ta, tb, split, kind = sy_item(p, T, kk - grp * p["ips"])
+        assert split < S
+        if kind == FULL:
+            assert 0 <= tb < ta < p["nt"]
+        else:  # diagonal tiles ta and tb = ta + 1 (or ta alone)
+            assert 0 <= ta < p["nt"] and tb == (ta + 1 if kind == DIAG2 else ta) < p["nt"]
+        # tiles stored by the item's waves (sy_scores_body: tile_out)
+        tiles = [ta * (ta + 1) // 2 + tb] if kind == FULL else [ta * (ta + 1) // 2 + ta] + (
+            [tb * (tb + 1) // 2 + tb] if kind == DIAG2 else [])
+        for t in tiles:
+            assert 0 <= t < ntl
+            key = (slab, t, split)
+            assert key not in seen, f"tile {key} computed twice"
+            seen.add(key)
+        # x loads: rows min(tile * 256 + r, T - 1) of both row blocks; stage
+        # columns kofs(s) + 8 c + [0, 8) for stages s < 2 nch (later stages
+        # re-load the last one)
+        nch = (p["nchunk"] - split + S - 1) // S
+        last = split + S * (nch - 1)
+        assert 0 <= last < p["nchunk"]
+        max_col = last * 64 + 32 + 8 * 3 + 8
+        assert max_col <= N
+        b, h = divmod(slab, nh)
+        max_row = min(max(ta, tb) * TILE + TILE - 1, T - 1)
+        hi = b * strides[0] + h * strides[1] + max_row * strides[2] + max_col
+        assert hi <= numel
+        # partial stores: ((slab ntl + tile) S + split) 65536 + ws NM 1024 + m 1024 + {0, 512} + 8 l + [0, 8)
+        for t in tiles:
+            nm, nws = (8, 8) if kind == FULL else (9, 4)
+            top = ((slab * ntl + t) * S + split) * TILE_ELEMS + (nws - 1) * nm * 1024 + (nm - 1) * 1024 + 512 + 63 * 8 + 8
+            assert top <= (slab * ntl + t + 1) * S * TILE_ELEMS
+    assert len(seen) == nslab * ntl * S
+    return p
+
+
+def check_sv(B, nh, T, D, p, v_strides, v_numel):
+    """k_sy_sv: every (row block, slab) workgroup, each 256-column launch."""
+    nslab = B * nh
+    nrb = (T + 63) // 64
+    S, ntl = p["nsplit"], p["ntl"]
+    part_elems = nslab * ntl * S * TILE_ELEMS
+    for d0 in range(0, D, 256):
+        Dc = min(256, D - d0)
+        assert Dc % 8 == 0
+        for rb in range(nrb):
+            r0 = rb * 64
+            nch = (min(T, r0 + 64) + 63) // 64
+            ti = r0 >> 8
+            for ck in range(nch):
+                tj = (ck * 64) >> 8
+                assert tj <= ti
+                tile = ti * (ti + 1) // 2 + tj
+                # the piece read for split sp: slot (< 64 full, < 36 diagonal) * 1024 + half * 512 + 8 l + [0, 8)
+                top = ((nslab - 1) * ntl + tile) * S * TILE_ELEMS + (S - 1) * TILE_ELEMS + 63 * 1024 + 512 + 63 * 8 + 8
+                assert top <= part_elems
+            # V rows min(j, T - 1) of chunks < nch, columns 8 min(vc, Dc / 8 - 1) + [0, 8) of the launch's slice
+            max_v = (B - 1) * v_strides[0] + (T - 1) * v_strides[2] + d0 + 8 * (Dc // 8 - 1) + 8
+            assert max_v <= v_numel
+
+
+def check_decode(B, nh, S, N, D, cap):
+    """k_decode_bf16 over capacity-strided past views (KVCache.past: rows [0, S) of (B, nh, cap, N))."""
+    assert N % 2048 == 0  # the kernel's 16-byte pieces: nc = N / 512, c += 4
+    k_strides = (nh * cap * N, cap * N, N)
+    v_strides = (cap * D, 0, D)
+    nred = (S + 63) // 64
+    rows = B * nh
+    for chunk in range(nred):
+        s0, s1 = chunk * 64, min(S, chunk * 64 + 64)
+        assert s0 < s1
+        # keys s0 + wave + 8 j (and + 4 when < s1): all < s1 <= S
+        keys = [s for wave in range(4) for s in range(s0 + wave, s1, 8)]
+        keys += [s + 4 for s in keys if s + 4 < s1]
+        assert max(keys) < S and min(keys) >= 0
+        nc = N // 512
+        max_col = 63 * 8 + (nc - 1) * 512 + 8
+        assert max_col <= N
+        hi = (B - 1) * k_strides[0] + (nh - 1) * k_strides[1] + (S - 1) * k_strides[2] + max_col
+        assert hi <= B * nh * cap * N  # inside the layer's cache block
+        assert (B - 1) * v_strides[0] + (S - 1) * v_strides[2] + D <= B * cap * D
+    assert nred * rows * D > 0
+
+
+@pytest.mark.parametrize("name,B,nh,T,N,D", PREFILL, ids=[c[0] for c in PREFILL])
+def test_prefill_launches_stay_in_bounds(name, B, nh, T, N, D):
+    # x_sparse: the permuted (B, T, nh, N) encoder output viewed as (B, nh, T, N)
+    x_strides = (T * nh * N, N, nh * N)
+    p = check_scores(B, nh, T, N, x_strides, B * T * nh * N)
+    # V: the layer input (B, 1, T, D), contiguous
+    check_sv(B, nh, T, D, p, (T * D, 0, D), B * T * D)
+
+
+@pytest.mark.parametrize("S", [256, 257, 300, 383, 384, 448, 511])
+def test_decode_launches_stay_in_bounds(S):
+    # C3 generate: B = 64, nh = 4, N = 8192, D = 256, cache capacity prompt + new = 512
+    check_decode(64, 4, S, 8192, 256, 512)
+
+
+def test_restated_plan_matches_the_documented_c1_split():
+    # C1: 32 slabs, one full tile + one diagonal pair per split, 4 splits = 256 items
+    p = sy_plan(32, 512, 8192)
+    assert (p["per_split"], p["nsplit"], p["ips"]) == (2, 4, 8)
+    assert 8 * ((32 + 7) // 8) * p["ips"] == 256
+    # every item kind appears, pairs cover both diagonal tiles
+    kinds = {sy_item(p, 512, i)[3] for i in range(p["ips"])}
+    assert kinds == {FULL, DIAG2}
+    assert {sy_item(p, 512, i)[:2] for i in range(p["ips"])} == {(1, 0), (0, 1)}
+
+
+def test_a_planted_overrun_is_caught():
+    # the checker itself: a row stride one element too long overruns the buffer
+    B, nh, T, N = 2, 4, 300, 512
+    with pytest.raises(AssertionError):
+        check_scores(B, nh, T, N, (T * nh * N, N, nh * N + 1), B * T * nh * N)
+    check_scores(B, nh, T, N, (T * nh * N, N, nh * N), B * T * nh * N)
