@@ -231,9 +231,8 @@ struct BwdPlan {
   FwdPlan f;
   int64_t tpad;
   size_t g_off, ws_bytes;
-  // bf16 with RoPE on the MFMA path: [table + score tiles | R(x) bf16 |
-  // G bf16 | R^T-bound dQ fp32]
-  size_t r_sy = 0, r_qr = 0, r_g = 0, r_dq = 0, r_end = 0;
+  // bf16 with RoPE on the MFMA path: [table + score tiles | R(x) bf16 | G bf16]
+  size_t r_sy = 0, r_qr = 0, r_g = 0, r_end = 0;
 };
 
 // saved: the score tiles come from the forward's workspace, so the first
@@ -252,8 +251,7 @@ BwdPlan plan_bwd(int64_t B, int64_t H, int64_t T, int64_t K, bool bf, bool saved
       const size_t x_elems = size_t(B * H) * size_t(T) * size_t(K);
       p.r_qr = align_up(p.r_sy, 256);
       p.r_g = align_up(p.r_qr + x_elems * 2, 256);
-      p.r_dq = align_up(p.r_g + size_t(B * H) * size_t(p.tpad) * size_t(p.tpad) * 2, 256);
-      p.r_end = p.r_dq + x_elems * 4;
+      p.r_end = p.r_g + size_t(B * H) * size_t(p.tpad) * size_t(p.tpad) * 2;
       p.ws_bytes = std::max(p.ws_bytes, p.r_end);
     }
   }
@@ -269,9 +267,9 @@ bool rows16b(const bdh_tensor4* t) {
 
 // bf16 self attention with RoPE on the MFMA path: one absolute-position score
 // kernel recomputes M's tiles and writes R(x) into the workspace; dV from the
-// tiles, G from dO and V, dR = G R(x) in fp32, then dx = R^T(dR) with the
-// score kernel's (cos, sin) table.  kNotEligible (nothing launched) outside
-// its shapes.
+// tiles, G from dO and V, then dx = R^T(G R(x)) from the dQ kernel, whose
+// epilogue applies R^T to its fp32 sums.  kNotEligible (nothing launched)
+// outside its shapes.
 int rope_fast_bwd(const bdh_tensor4* x, const bdh_tensor4* v, const bdh_tensor4* dout, const bdh_tensor4* dx,
                   const bdh_tensor4* dv, const float* freqs, int64_t rope_start, void* ws, size_t ws_bytes,
                   const BwdPlan& p, hipStream_t s) {
@@ -296,9 +294,6 @@ int rope_fast_bwd(const bdh_tensor4* x, const bdh_tensor4* v, const bdh_tensor4*
   qr.stride[1] = T * N;
   qr.stride[0] = H * T * N;
   qr.dtype = BDH_BF16;
-  bdh_tensor4 gq = qr;
-  gq.data = w + p.r_dq;
-  gq.dtype = BDH_F32;
   const void* tiles = nullptr;
   int rc = sy_rope_scores(x, v, freqs, rope_start, &qr, ws, p.r_sy, s, &tiles);
   if (rc != BDH_OK) return rc;  // kNotEligible before anything ran
@@ -308,8 +303,7 @@ int rope_fast_bwd(const bdh_tensor4* x, const bdh_tensor4* v, const bdh_tensor4*
   if (numel4(dv) > 0) BDH_TRY(step(sy_bwd_dv(&qr, v, dout, dv, nullptr, 0, s, tiles)));
   if (numel4(dx) == 0) return BDH_OK;
   BDH_TRY(step(sy_bwd_g(dout, v, w + p.r_g, p.tpad, s)));
-  BDH_TRY(step(sy_dq(w + p.r_g, p.tpad, &qr, &gq, s)));
-  return step(sy_rope_unrotate(static_cast<const float*>(gq.data), ws, B, H, T, N, dx, s));
+  return step(sy_dq(w + p.r_g, p.tpad, &qr, dx, s, freqs, rope_start));
 }
 
 bool vec4_rows(const bdh_tensor4* t) {

@@ -77,17 +77,16 @@ bool sy_keeps_scores(const bdh_tensor4* q, const bdh_tensor4* v, size_t* scores_
 // Backward G = dS + dS^T (bf16, [B*H][tpad][tpad]) on the MFMA score kernel
 // (syrk.hip): bf16 dO and V, D a multiple of 64.
 int sy_bwd_g(const bdh_tensor4* dout, const bdh_tensor4* v, void* g, int64_t tpad, hipStream_t s);
-// Backward dQ = G X on the MFMA path (syrk.hip): bf16 X, self attention, no RoPE.
-int sy_dq(const void* g, int64_t tpad, const bdh_tensor4* x, const bdh_tensor4* out, hipStream_t s);
+// Backward dQ = G X on the MFMA path (syrk.hip): bf16 X, self attention.
+// With freqs, out = R^T(G X) at positions rope_start + t (X = R(x)).
+int sy_dq(const void* g, int64_t tpad, const bdh_tensor4* x, const bdh_tensor4* out, hipStream_t s,
+          const float* freqs = nullptr, int64_t rope_start = 0);
 // Backward of the fused RoPE op on the MFMA path (syrk.hip): the score tiles
 // of R(x) R(x)^T with R(x) written to qr (absolute positions; ws starts with
-// their (cos, sin) table, *tiles points at the tiles), then dx = R^T(g) from
-// that table.
+// their (cos, sin) table, *tiles points at the tiles).
 size_t sy_rope_scores_workspace(int64_t B, int64_t H, int64_t T, int64_t N);
 int sy_rope_scores(const bdh_tensor4* x, const bdh_tensor4* v, const float* freqs, int64_t rope_start,
                    const bdh_tensor4* qr, void* ws, size_t ws_bytes, hipStream_t s, const void** tiles);
-int sy_rope_unrotate(const float* g, const void* ws, int64_t B, int64_t H, int64_t T, int64_t N,
-                     const bdh_tensor4* dx, hipStream_t s);
 
 FwdPlan plan_fwd(int64_t B, int64_t H, int64_t T, int64_t K, bool bf, int64_t past = 0);
 int run_scores(const ScoresArgs& a, const FwdPlan& p, int64_t BH, bool bf, bool rope, bool trans,

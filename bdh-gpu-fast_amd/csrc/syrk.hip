@@ -242,43 +242,6 @@ __global__ __launch_bounds__(256) void k_rope_table(const float* __restrict__ fr
   cs[(int64_t(m >> 4) * T + t) * 16 + (m & 15)] = rope_cs(float(rope_start + t), freqs[2 * m]);
 }
 
-// The transpose rotation RoPE^T (the backward of RoPE) with the table's
-// (cos, sin): dx[2m] = g[2m] c + g[2m+1] s, dx[2m+1] = g[2m+1] c - g[2m] s,
-// fp32 arithmetic, one rounding to TO.  g is fp32, contiguous (B*H, T, N);
-// dx any (B, H, T) strides with 16-byte rows.  Thread: 8 elements (4 pairs)
-// of row t of slab z; grid (N / 2048 rounded up, T, B*H).
-template <typename TO>
-__global__ __launch_bounds__(256) void k_rope_unrotate(const float* __restrict__ g, const uint32_t* __restrict__ cs,
-                                                       int H, int T, int N, TO* __restrict__ dx, int64_t o0,
-                                                       int64_t o1, int64_t o2) {
-  const int t = blockIdx.y, z = blockIdx.z;
-  const int e = (blockIdx.x * 256 + threadIdx.x) * 8;
-  if (e >= N) return;
-  const int m = e >> 1;  // first pair; m % 4 == 0, so its four entries are one 16-byte run
-  const float* gp = g + (int64_t(z) * T + t) * N + e;
-  const float4 g0 = *reinterpret_cast<const float4*>(gp);
-  const float4 g1 = *reinterpret_cast<const float4*>(gp + 4);
-  const u32x4 c4 = *reinterpret_cast<const u32x4*>(cs + (int64_t(m >> 4) * T + t) * 16 + (m & 15));
-  const float gv[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
-  const uint32_t cw[4] = {c4.x, c4.y, c4.z, c4.w};
-  float y[8];
-#pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const float c = __uint_as_float(cw[q] << 16), sn = __uint_as_float(cw[q] & 0xffff0000u);
-    y[2 * q] = fmaf(gv[2 * q], c, gv[2 * q + 1] * sn);
-    y[2 * q + 1] = fmaf(gv[2 * q + 1], c, -(gv[2 * q] * sn));
-  }
-  const int b = z / H, h = z - b * H;
-  TO* op = dx + b * o0 + h * o1 + int64_t(t) * o2 + e;
-  if constexpr (sizeof(TO) == 2) {
-    *reinterpret_cast<u32x4*>(op) =
-        u32x4{pack_bf2(y[0], y[1]), pack_bf2(y[2], y[3]), pack_bf2(y[4], y[5]), pack_bf2(y[6], y[7])};
-  } else {
-    *reinterpret_cast<float4*>(op) = make_float4(y[0], y[1], y[2], y[3]);
-    *reinterpret_cast<float4*>(op + 4) = make_float4(y[4], y[5], y[6], y[7]);
-  }
-}
-
 // Diagonal tiles (Q = K) in pairs: the 36 lower 32x32 blocks of one diagonal
 // tile are split into four wave programs of 9 blocks; waves 0-3 run them on
 // the first tile of the pair and waves 4-7 on the second, so each SIMD issues
@@ -870,13 +833,15 @@ struct DqsArgs {
   void* o;
   int64_t o0, o1, o2;
   int H, T, N, tpad, nslab, nti, ntn;
+  const float* freqs = nullptr;  // RoPE: the output is R^T(G X), positions rope_start + t
+  int64_t rope_start = 0;
 };
 
 __device__ __forceinline__ bf16x4 lds_tr4(const uint8_t* p) {
   return __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(p));
 }
 
-template <typename TO>
+template <typename TO, bool ROPE = false>
 __global__ __launch_bounds__(kSyThreads, 1) void k_dq_sy(const DqsArgs a) {
   const int bid = blockIdx.x;
   const int xcd = bid & 7, kk = bid >> 3;
@@ -1017,6 +982,40 @@ __global__ __launch_bounds__(kSyThreads, 1) void k_dq_sy(const DqsArgs a) {
   sy_wait<0>();  // the re-loads past the end land before the LDS is freed
 
   TO* o = static_cast<TO*>(a.o) + b * a.o0 + h * a.o1;
+  if constexpr (ROPE) {
+    // R^T of the RoPE pair (2p, 2p + 1) = columns of lanes l and l ^ 1:
+    // dx[2p] = g[2p] c + g[2p+1] s, dx[2p+1] = g[2p+1] c - g[2p] s, with the
+    // (cos, sin) dword of rope_cs (the table kernel's bits) at position
+    // rope_start + row, fp32 arithmetic, one rounding to TO
+    // Lanes l and l ^ 1 share every (row, pair): each makes the dwords of the
+    // values r with r % 2 == l % 2 and takes the others from its partner, and
+    // partners swap values with a DPP quad permute (1, 0, 3, 2).
+    const bool odd = (lane & 1) != 0;
+    auto swap1 = [](uint32_t u) { return uint32_t(__builtin_amdgcn_mov_dpp(int(u), 0xB1, 0xF, 0xF, false)); };
+    float fq[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) fq[u] = a.freqs[(n0 + 64 * wn + 32 * u + (lane & 31)) & ~1];
+#pragma unroll
+    for (int m = 0; m < 8; ++m)
+#pragma unroll
+      for (int r = 0; r < 16; r += 2) {
+        const int row0 = i0 + 128 * wm + 32 * (m >> 1) + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        const int col = n0 + 64 * wn + 32 * (m & 1) + (lane & 31);
+        // this lane makes the dword of value r + (lane & 1); the partner the other
+        const uint32_t mine = rope_cs(float(a.rope_start + row0 + (odd ? 1 : 0)), fq[m & 1]);
+        const uint32_t theirs = swap1(mine);
+        const uint32_t cws[2] = {odd ? theirs : mine, odd ? mine : theirs};
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          const float v = acc[m][r + e];
+          const float pv = __uint_as_float(swap1(__float_as_uint(v)));
+          const float c = __uint_as_float(cws[e] << 16), sn = __uint_as_float(cws[e] & 0xffff0000u);
+          const float y = odd ? fmaf(v, c, -(pv * sn)) : fmaf(v, c, pv * sn);
+          if (row0 + e < a.T) o[int64_t(row0 + e) * a.o2 + col] = from_f<TO>(y);
+        }
+      }
+    return;
+  }
 #pragma unroll
   for (int m = 0; m < 8; ++m)
 #pragma unroll
@@ -1666,22 +1665,6 @@ int sy_rope_scores(const bdh_tensor4* x, const bdh_tensor4* v, const float* freq
   return rc;
 }
 
-// dx = RoPE^T(g) with the table sy_rope_scores left at the start of ws.
-int sy_rope_unrotate(const float* g, const void* ws, int64_t B, int64_t H, int64_t T, int64_t N,
-                     const bdh_tensor4* dx, hipStream_t s) {
-  if (N % 8 != 0 || T > 65535 || B * H > 65535 || !rows16(dx)) return kNotEligible;
-  if (dx->dtype != BDH_BF16 && dx->dtype != BDH_F32) return kNotEligible;
-  const dim3 grid(unsigned((N / 8 + 255) / 256), unsigned(T), unsigned(B * H));
-  const uint32_t* cs = static_cast<const uint32_t*>(ws);
-  if (dx->dtype == BDH_BF16)
-    BDH_LAUNCH("k_rope_unrotate", k_rope_unrotate<bf16_t>, grid, dim3(256), 0, s, g, cs, int(H), int(T), int(N),
-               static_cast<bf16_t*>(dx->data), dx->stride[0], dx->stride[1], dx->stride[2]);
-  else
-    BDH_LAUNCH("k_rope_unrotate", k_rope_unrotate<float>, grid, dim3(256), 0, s, g, cs, int(H), int(T), int(N),
-               static_cast<float*>(dx->data), dx->stride[0], dx->stride[1], dx->stride[2]);
-  return BDH_OK;
-}
-
 size_t sy_past_workspace(int64_t B, int64_t H, int64_t Tk, int64_t past, int64_t N, int64_t Dv) {
   if (past <= 0 || past >= Tk) return 0;
   const SyPlan p = sy_plan(B * H, Tk, N, true, false, Dv, 8, int(past / kSyTile));
@@ -1700,9 +1683,11 @@ int sy_past(const bdh_tensor4* q, const bdh_tensor4* k, const bdh_tensor4* v, co
 }
 
 
-// dQ = G X (self attention, bf16 X, no RoPE) on the MFMA path; kNotEligible
-// when the shapes fall outside it.
-int sy_dq(const void* g, int64_t tpad, const bdh_tensor4* x, const bdh_tensor4* out, hipStream_t s) {
+// dQ = G X (self attention, bf16 X) on the MFMA path; with freqs, out =
+// R^T(G X) at positions rope_start + t (x is then R(x)).  kNotEligible when
+// the shapes fall outside it.
+int sy_dq(const void* g, int64_t tpad, const bdh_tensor4* x, const bdh_tensor4* out, hipStream_t s,
+          const float* freqs, int64_t rope_start) {
   const int64_t B = x->size[0], H = x->size[1], T = x->size[2], N = x->size[3];
   if (x->dtype != BDH_BF16 || N % kSyTile != 0 || T < 1 || !rows16(x)) return kNotEligible;
   if (out->size[0] != B || out->size[1] != H || out->size[2] != T || out->size[3] != N) return kNotEligible;
@@ -1729,11 +1714,19 @@ int sy_dq(const void* g, int64_t tpad, const bdh_tensor4* x, const bdh_tensor4* 
   a.nslab = int(nslab);
   a.nti = int(nti);
   a.ntn = int(ntn);
+  a.freqs = freqs;
+  a.rope_start = rope_start;
   const dim3 gs{unsigned(grid)};
-  if (out->dtype == BDH_BF16)
+  if (freqs != nullptr) {
+    if (out->dtype == BDH_BF16)
+      BDH_LAUNCH("k_dq_sy", (k_dq_sy<bf16_t, true>), gs, dim3(kSyThreads), 0, s, a);
+    else
+      BDH_LAUNCH("k_dq_sy", (k_dq_sy<float, true>), gs, dim3(kSyThreads), 0, s, a);
+  } else if (out->dtype == BDH_BF16) {
     BDH_LAUNCH("k_dq_sy", k_dq_sy<bf16_t>, gs, dim3(kSyThreads), 0, s, a);
-  else
+  } else {
     BDH_LAUNCH("k_dq_sy", k_dq_sy<float>, gs, dim3(kSyThreads), 0, s, a);
+  }
   return BDH_OK;
 }
 

@@ -3,13 +3,13 @@
 bf16 self attention with RoPE (``tril_rope_score_v_bwd``, the backward of
 ``TrilRopeSelfAttnFn`` that ``bdh_attn_rope`` uses under autograd): one
 absolute-position score kernel recomputes M's tiles and writes R(x), dV comes
-from the tiles, G from dO and V, dR = G R(x) in fp32, and dx = R^T(dR) from
-the score kernel's (cos, sin) table.  Checked against the oracle's gradients
+from the tiles, G from dO and V, and the dQ kernel forms dx = R^T(G R(x)),
+applying R^T to its fp32 sums in the epilogue.  Checked against the oracle's gradients
 (oracle/tril_attn_oracle.py ``tril_rope_score_v_backward``, the reference's
 attention_bwd.py:45-83 composed with rope.py:543-556) at the bf16 tolerance
 (2e-2, relative Frobenius), against the generic kernels on the same inputs,
 and through autograd with an fp32 V (the AMP case: V is the LayerNorm output).
-Each case checks that the route ran (its RoPE^T kernel in the launch log).
+Each case checks that the route ran (its dQ kernel in the launch log).
 """
 
 from __future__ import annotations
@@ -67,7 +67,7 @@ def test_rope_backward_mfma_route_matches_oracle(shape):
     xd, vd, dd = to_dev(x, BF), to_dev(v, BF), to_dev(dO, BF)
     fd = torch.from_numpy(f).to(DEV)
     (dx, dv), names = _names(lambda: ext.tril_rope_score_v_bwd(xd, vd, dd, fd, start))
-    assert "k_rope_unrotate" in names and "k_dq_sy" in names, names
+    assert "k_dq_sy" in names and "k_dv_sy" in names, names
     wx, wv = O.tril_rope_score_v_backward(x, v, dO, f, start)
     ex, ev = rel_fro(np_of(dx), wx), rel_fro(np_of(dv), wv)
     print(f"  dx rel {ex:.3e}, dv rel {ev:.3e}", flush=True)
@@ -75,7 +75,7 @@ def test_rope_backward_mfma_route_matches_oracle(shape):
     assert ev <= TOL
     # the generic kernels on the same values (fp32 V takes them): same gradients within bf16
     (gx, gv), gnames = _names(lambda: ext.tril_rope_score_v_bwd(xd, vd.float(), dd, fd, start))
-    assert "k_rope_unrotate" not in gnames
+    assert "k_dq_sy" not in gnames
     assert rel_fro(np_of(dx), np_of(gx)) <= TOL
     assert rel_fro(np_of(dv), np_of(gv)) <= TOL
 
@@ -114,7 +114,7 @@ def test_rope_autograd_with_fp32_v_takes_the_mfma_route():
         return out
 
     out, names = _names(run)
-    assert "k_rope_unrotate" in names, names
+    assert "k_dq_sy" in names, names
     assert xd.grad.dtype == BF and vd.grad.dtype == torch.float32
     wx, wv = O.tril_rope_score_v_backward(x, O.bf16_round(v), dO, f, start)
     assert rel_fro(np_of(xd.grad), wx) <= TOL
