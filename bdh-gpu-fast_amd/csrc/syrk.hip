@@ -1204,6 +1204,8 @@ struct SvArgs {
   int past = 0;        // rows below past are not stored; row i is stored at i - past
   int rel = 0;         // the tiles came from the relative-RoPE score kernel (fragment slot order)
   int self = 1;        // Q = K: diagonal tiles hold their 36 lower blocks (else every tile is full)
+  int nrbk = 1;        // row blocks per slab in this launch
+  int nslab = 0;
 };
 
 template <typename TO, typename TV, int NS>
@@ -1215,13 +1217,16 @@ __global__ __launch_bounds__(512, 1) void k_sy_sv(const SvArgs a) {
   uint8_t* const vblk = sv_lds + 64 * 128;   // 64 x 512 bytes
   float* const red = reinterpret_cast<float*>(sv_lds);
   constexpr int VL = sizeof(TV) == 2 ? 1 : 2;  // 16-byte loads per 8 V elements
-  // Row blocks have 1..nrb key chunks and workgroups go to the XCDs round
-  // robin by linear id, so the block index is rotated by the slab: with the
-  // plain order an XCD would get one block length only (C1: one XCD every
-  // 8-chunk block, another every 1-chunk block), and the longest ones would
-  // share one XCD's bandwidth.
-  const int slab = blockIdx.y;
-  const int rb = int((blockIdx.x + blockIdx.y) % gridDim.x) + a.rb0;
+  // Workgroups go to the XCDs round robin by linear id L.  The row blocks of
+  // slab s run on XCD s % 8, the XCD whose L2 took the slab's partial tiles
+  // in the score kernel (L = 8 (nrbk (s / 8) + k) + s % 8 for the k-th block
+  // of the slab).  Row blocks have 1..nrb key chunks, so the block index is
+  // rotated by the slab: every XCD gets every block length.
+  const int nrbk = a.nrbk;
+  const int L = blockIdx.x, xcdv = L & 7, kk = L >> 3;
+  const int slab = (kk / nrbk) * 8 + xcdv;
+  if (slab >= a.nslab) return;
+  const int rb = (kk % nrbk + slab) % nrbk + a.rb0;
   const int b = slab / a.H, h = slab - b * a.H, hv = a.Hv == 1 ? 0 : h;
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   const int r0 = rb * 64;
@@ -1621,7 +1626,9 @@ int sy_run(const bdh_tensor4* q, const bdh_tensor4* k, const bdh_tensor4* v, con
   sa.past = int(past);
   sa.rel = rel ? 1 : 0;
   sa.self = self ? 1 : 0;
-  const dim3 gsv(unsigned((T + 63) / 64 - sa.rb0), unsigned(nslab));
+  sa.nrbk = int((T + 63) / 64 - sa.rb0);
+  sa.nslab = int(nslab);
+  const dim3 gsv(unsigned(8 * ((nslab + 7) / 8) * sa.nrbk));
   const bool o16 = out->dtype == BDH_BF16, v16 = v->dtype == BDH_BF16;
   // one launch per 256 columns of V (the score tiles are read again by each)
   for (int64_t d0 = 0; d0 < Dv; d0 += 256) {

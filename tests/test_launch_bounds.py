@@ -97,12 +97,27 @@ def check_scores(B, nh, T, N, strides, numel):
     return p
 
 
+def sv_grid(nslab, nrb):
+    """csrc/syrk.hip k_sy_sv: (rb, slab) of each linear workgroup id (None past the slabs)."""
+    out = []
+    for L in range(8 * ((nslab + 7) // 8) * nrb):
+        xcd, kk = L & 7, L >> 3
+        slab = (kk // nrb) * 8 + xcd
+        out.append(None if slab >= nslab else ((kk % nrb + slab) % nrb, slab))
+    return out
+
+
 def check_sv(B, nh, T, D, p, v_strides, v_numel):
     """k_sy_sv: every (row block, slab) workgroup, each 256-column launch."""
     nslab = B * nh
     nrb = (T + 63) // 64
     S, ntl = p["nsplit"], p["ntl"]
     part_elems = nslab * ntl * S * TILE_ELEMS
+    # the 1-D grid visits each (row block, slab) once; slab s sits on XCD s % 8
+    grid = sv_grid(nslab, nrb)
+    live = [g for g in grid if g is not None]
+    assert sorted(live) == sorted((rb, s) for s in range(nslab) for rb in range(nrb))
+    assert all(g[1] % 8 == L % 8 for L, g in enumerate(grid) if g is not None)
     for d0 in range(0, D, 256):
         Dc = min(256, D - d0)
         assert Dc % 8 == 0
