@@ -23,8 +23,10 @@ hipEvent_t take_event() {
     g_free.pop_back();
     return e;
   }
+  // Timing-only events: no system-scope fence when they are recorded (the
+  // records are read after the caller has synchronised the stream).
   hipEvent_t e = nullptr;
-  if (hipEventCreate(&e) != hipSuccess) return nullptr;
+  if (hipEventCreateWithFlags(&e, hipEventDisableSystemFence) != hipSuccess) return nullptr;
   return e;
 }
 }  // namespace

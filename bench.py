@@ -7,17 +7,21 @@ HIP kernels (``kernels.bdh_attn_rope(impl="hip")``), inputs resident in HBM.
 One step = one call over the whole batch.  Throughput is the algorithmic
 F = B*nh*(N+D)*T*(T-1) flops per step (strict lower triangle; RoPE's
 elementwise work is not counted) divided by the measured step time.  The step
-first runs untimed until two consecutive 20-step windows agree within 2 %
-(at least 0.2 s, at most 3 s), then W warmup steps, then exactly K timed steps
-(defaults K = 200, W = 100), synchronised on both sides.
+first runs untimed, back to back, until two consecutive windows of about 0.1 s
+agree within 1 % (at least 1 s, at most 4 s: the shader clock keeps rising for
+about a second of sustained work), then W warmup steps, then exactly K timed
+steps (defaults K = 200, W = 100), synchronised on both sides.
 
 The JSON line also carries:
   * ``roofline``: the dominant kernel (``k_sy_scores``, the score tiles QR QR^T)
-    timed over the K timed steps themselves: each launch carries HIP start/stop
-    events that the runtime stamps at the kernel's own start and end
-    (hipExtLaunchKernelGGL on the launch stream, no extra stream work);
-    achieved = its algorithmic flops B*nh*N*T*(T-1) / mean duration, against
-    the 2.5 PFLOP/s bf16 dense MFMA peak.  ``kernels_us_isolated`` and
+    timed over K more steps run right after the timed ones: each launch
+    carries HIP start/stop events that the runtime stamps at the kernel's own
+    start and end (hipExtLaunchKernelGGL on the launch stream, no extra
+    stream work); achieved = its algorithmic flops B*nh*N*T*(T-1) / mean
+    duration, against the 2.5 PFLOP/s bf16 dense MFMA peak.  The events leave
+    kernel durations as they are but make each launch wait for the previous
+    one to end, so they stay out of the K timed steps; ``ms_per_step_observed``
+    is the step time with them.  ``kernels_us_isolated`` and
     ``frac_isolated`` repeat the measurement with a synchronisation after
     every step (no kernel overlapping the previous one's tail, as under a
     profiler's kernel trace).  ``traffic`` is the HBM
@@ -81,17 +85,31 @@ def attn_flops(B, nh, T, N, D) -> float:
     return float(B * nh * (N + D) * T * (T - 1))
 
 
-def settle(fn, window: int = 20, tol: float = 0.02, max_s: float = 3.0, min_s: float = 0.2) -> dict:
-    """Run the step untimed until its rate has settled: consecutive windows of
-    ``window`` steps (HIP events) until two in a row agree within ``tol``,
-    after at least ``min_s`` seconds and at most ``max_s``.  The first ~100
-    steps of a cold process run up to 10% slower (clocks and queues settling),
-    which a short warmup would leave in the timed region.  Returns the window
-    times (ms per step) and whether they converged."""
+def settle(fn, window_s: float = 0.1, tol: float = 0.01, max_s: float = 4.0, min_s: float = 1.0) -> dict:
+    """Run the step untimed until its rate has settled: back-to-back windows
+    of about ``window_s`` seconds each (HIP events), until two in a row agree
+    within ``tol``, after at least ``min_s`` seconds and at most ``max_s``.
+    Two effects make a cold start slow.  The first ~100 steps of a process
+    run up to 10 % slower (queues and caches settling).  The shader clock then
+    keeps rising for about a second of back-to-back work: on MI355X amd-smi
+    read 2.06 GHz early in a run and 2.25 GHz after 1.5 s, and the C1 score
+    kernel went from 99.6 to 88.0 us.  Windows of a few milliseconds agree
+    with each other long before the clock has risen, so the windows here are
+    sized in time.  Returns the window times (ms per step) and whether they
+    converged."""
     import torch
 
-    t_end = time.perf_counter() + max_s
-    t_min = time.perf_counter() + min_s
+    t0 = time.perf_counter()
+    fn()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    for _ in range(8):  # warm calls size the window
+        fn()
+    torch.cuda.synchronize()
+    per_step = max((time.perf_counter() - t1) / 8, 1e-6)
+    window = max(3, int(window_s / per_step))
+    t_end = t0 + max_s
+    t_min = t0 + min_s
     hist: list = []
     converged = False
     while time.perf_counter() < t_end:
@@ -106,7 +124,8 @@ def settle(fn, window: int = 20, tol: float = 0.02, max_s: float = 3.0, min_s: f
         if len(hist) >= 2 and time.perf_counter() >= t_min and abs(hist[-1] - hist[-2]) <= tol * hist[-2]:
             converged = True
             break
-    return {"windows": len(hist), "last_ms": hist[-2:], "converged": converged}
+    return {"windows": len(hist), "steps_per_window": window, "seconds": round(time.perf_counter() - t0, 2),
+            "last_ms": hist[-2:], "converged": converged}
 
 
 def sample_sclk(fn, seconds: float = 1.5, n_samples: int = 6) -> dict:
@@ -157,14 +176,14 @@ def sample_sclk(fn, seconds: float = 1.5, n_samples: int = 6) -> dict:
     }
 
 
-def time_steps(fn, steps: int, warmup: int, settle_s: float = 0.2) -> float:
+def time_steps(fn, steps: int, warmup: int, settle_s: float = 0.5) -> float:
     """ms per step over exactly ``steps`` calls, synchronised on both sides,
-    after a short settle (at least ``settle_s`` seconds, until two 20-step
-    windows agree within 2 %) and ``warmup`` untimed calls."""
+    after a settle (at least ``settle_s`` seconds of back-to-back steps, until
+    two windows of about 0.1 s agree within 1 %) and ``warmup`` untimed calls."""
     import torch
 
     if settle_s > 0:
-        settle(fn, max_s=max(settle_s, 1.0), min_s=settle_s)
+        settle(fn, max_s=max(2 * settle_s, 2.0), min_s=settle_s)
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
@@ -443,18 +462,23 @@ def main() -> int:
     settled = settle(step)
     log(f"[bench] settle: {settled}")
     launches0 = ext.launch_count()
-    # the per-kernel events ride on the launches of the timed steps (stamped
-    # by the runtime at kernel start and end; no extra stream work)
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
+    ms = time_steps(step, args.steps, 0, settle_s=0)
+    # The per-kernel events ride on the launches of the next K steps, run
+    # right after the timed ones (stamped by the runtime at kernel start and
+    # end).  They do not change a kernel's duration, but the runtime starts
+    # each evented launch only after the previous one has ended (median gap
+    # 7.8 us in a kernel trace, 0 without events), which would slow the
+    # timed steps themselves; ms_per_step_observed shows that cost.
     ext.profile_enable(True)
     try:
-        ms = time_steps(step, args.steps, 0, settle_s=0)
+        ms_obs = time_steps(step, args.steps, 0, settle_s=0)
         live = _agg(ext.profile_collect(), args.steps)
     finally:
         ext.profile_enable(False)
-    assert ext.launch_count() - launches0 == args.steps + args.warmup, "HIP library calls missing"
+    assert ext.launch_count() - launches0 == 2 * args.steps + args.warmup, "HIP library calls missing"
     F = attn_flops(B, nh, T, N, D)
     value = F / (ms * 1e-3) / 1e12
     log(f"[bench] fused RoPE tril-attn fwd C1 bf16: {ms * 1e3:.1f} us/step, {value:.1f} TFLOP/s")
@@ -476,6 +500,7 @@ def main() -> int:
         "frac": achieved / PEAK_BF16_TFLOPS,
         "traffic": traffic,
         "kernel_us": k_ms * 1e3,
+        "ms_per_step_observed": ms_obs,
         "kernels_us": {k: round(v[0] * 1e3, 2) for k, v in means.items()},
         "kernels_us_isolated": {k: round(v[0] * 1e3, 2) for k, v in isolated.items()},
         "frac_isolated": F_scores / (isolated[kname][0] * 1e-3) / 1e12 / PEAK_BF16_TFLOPS,
