@@ -1030,11 +1030,16 @@ __global__ __launch_bounds__(kSyThreads, 1) void k_dq_sy(const DqsArgs a) {
 // dV[b, hv, j, :] = sum over heads h and rows i > j of M_h[i, j] dO_h[i, :],
 // M from the partial score tiles of k_sy_scores (split sum in fp32, one
 // rounding to bf16).  Rows j in blocks of 64 per workgroup, all D (<= 256)
-// columns: wave w owns columns [64 w, +64).  Per 64-row chunk of i the M block
-// (64 i x 64 j) and the dO block (64 i x 256 d) are staged row-major in LDS
-// and both MFMA operands (M^T as A, dO as B, both contracting over i, their
-// row index) are read with ds_read_b64_tr_b16.  The next chunk's loads are
-// issued before the current chunk's MFMAs.
+// columns.  The workgroup's items, (head, 64-row chunk of i >= j0), are
+// dealt alternately to two groups of four waves; in a group wave w owns
+// columns [64 w, +64).  Per item the M block (64 i x 64 j) and the dO block
+// (64 i x 256 d) are staged row-major in the group's LDS, and both MFMA
+// operands (M^T as A, dO as B, both contracting over i, their row index) are
+// read with ds_read_b64_tr_b16.  A group's next item is loaded while it runs
+// the current one's MFMAs.  The second group's fp32 sums are added to the
+// first's through LDS at the end.  Two groups halve the longest workgroup's
+// chain of items (the row block j0 = 0 has H * T / 64 of them) and keep two
+// items' loads in flight per CU.
 struct DvsArgs {
   const bf16_t* part;  // [slab][ntl][nsplit][256*256]
   int ntl, nsplit;
@@ -1046,25 +1051,38 @@ struct DvsArgs {
 };
 
 template <typename TO, int NS>
-__global__ __launch_bounds__(256) void k_dv_sy(const DvsArgs a) {
-  __shared__ __attribute__((aligned(16))) uint8_t mblk[64 * 128];  // M [i][j], 16-byte chunk c at c ^ 2 (i & 3)
-  __shared__ __attribute__((aligned(16))) uint8_t dblk[64 * 512];  // dO [i][d], chunk c at c ^ 4 (i & 3)
+__global__ __launch_bounds__(512) void k_dv_sy(const DvsArgs a) {
+  // two groups of four waves, each with its own staging blocks:
+  // M [i][j] (16-byte chunk c at c ^ 2 (i & 3)) and dO [i][d] (chunk c at c ^ 4 (i & 3))
+  constexpr int kBlk = 64 * 128 + 64 * 512;
+  __shared__ __attribute__((aligned(16))) uint8_t dv_lds[2 * kBlk];
   const int rb = blockIdx.x, bv = blockIdx.y;
   const int b = bv / a.Hv, hv = bv - b * a.Hv;
   const int j0 = rb * 64;
-  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  const int tid = threadIdx.x, grp = tid >> 8, gt = tid & 255, w = gt >> 6, lane = tid & 63;
+  uint8_t* const mblk = dv_lds + grp * kBlk;
+  uint8_t* const dblk = mblk + 64 * 128;
   const int h_lo = a.Hv == 1 ? 0 : hv, h_hi = a.Hv == 1 ? a.H : hv + 1;
   const int ic0 = j0 / 64, nic = (a.T + 63) / 64;  // chunks of i: i >= j0 (i > j)
   const int tj = j0 >> 8;
+  // items it = (head h_lo + it / per_h, chunk ic0 + it % per_h); group g takes
+  // items g, g + 2, ... (ng of them), both groups step together (nk steps)
+  const int per_h = nic - ic0;
+  const int total = per_h * (h_hi - h_lo);
+  const int ng = (total - grp + 1) / 2, nk = (total + 1) / 2;
 
   // builder roles: M pieces (fragment-ordered partial tiles, see sy_piece):
-  // piece e of this thread is 32 x 32 block mbi = (tid + 256 e) / 128 of the
+  // piece e of this thread is 32 x 32 block mbi = (gt + 256 e) / 128 of the
   // 64 x 64 (i, j) chunk (rows i: mbi / 2, columns j: mbi % 2), lane
-  // ((tid & 127) >> 1), half tid & 1; dO chunks e = tid + 256 u
-  const int pl = (tid & 127) >> 1, ph = tid & 1;
+  // ((gt & 127) >> 1), half gt & 1; dO chunks e = gt + 256 u
+  const int pl = (gt & 127) >> 1, ph = gt & 1;
   uint4 mp[NS][2];
   uint4 dp[8];
-  auto load_chunk = [&](int h, int ic) {
+  // Steps past a group's last item load the workgroup's last item again (an
+  // L2 hit, not used); splits past nsplit re-read the last split (not summed).
+  auto load_chunk = [&](int itq) {
+    const int it = min(itq, total - 1);
+    const int h = h_lo + it / per_h, ic = ic0 + it % per_h;
     const int i0 = ic * 64;
     const int ti = i0 >> 8;
     const int slab = b * a.H + h;
@@ -1072,25 +1090,25 @@ __global__ __launch_bounds__(256) void k_dv_sy(const DvsArgs a) {
     const bf16_t* p = a.part + ((int64_t(slab) * a.ntl + ti * (ti + 1) / 2 + tj) * a.nsplit) * kSyTileElems;
 #pragma unroll
     for (int e = 0; e < 2; ++e) {
-      const int mbi = (tid >> 7) + 2 * e;
+      const int mbi = (gt >> 7) + 2 * e;
       const int rbk = ((i0 & 255) >> 5) + (mbi >> 1), cbk = ((j0 & 255) >> 5) + (mbi & 1);
       // (no blocks above a diagonal tile's diagonal: read the diagonal block, masked below)
       const int off = sy_piece(dt, 0, rbk, dt && cbk > rbk ? rbk : cbk, pl, ph);
 #pragma unroll
       for (int sp = 0; sp < NS; ++sp)
-        mp[sp][e] = sp < a.nsplit ? *reinterpret_cast<const uint4*>(p + int64_t(sp) * kSyTileElems + off)
-                                  : uint4{0u, 0u, 0u, 0u};
+        mp[sp][e] = *reinterpret_cast<const uint4*>(p + int64_t(min(sp, a.nsplit - 1)) * kSyTileElems + off);
     }
     const bf16_t* dob = a.dO + b * a.d0 + h * a.d1;
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
-      const int e = tid + 256 * u, r = e >> 5, c = e & 31;
+      const int e = gt + 256 * u, r = e >> 5, c = e & 31;
       const int ig = i0 + r;
       dp[u] = (ig < a.T && 8 * c < a.D) ? *reinterpret_cast<const uint4*>(dob + int64_t(ig) * a.d2 + 8 * c)
                                         : uint4{0u, 0u, 0u, 0u};
     }
   };
-  auto store_chunk = [&](int ic) {
+  auto store_chunk = [&](int it, bool live) {
+    const int ic = ic0 + min(it, total - 1) % per_h;
 #pragma unroll
     for (int e = 0; e < 2; ++e) {
       float sacc[8];
@@ -1098,6 +1116,7 @@ __global__ __launch_bounds__(256) void k_dv_sy(const DvsArgs a) {
       for (int q = 0; q < 8; ++q) sacc[q] = 0.f;
 #pragma unroll
       for (int sp = 0; sp < NS; ++sp) {
+        if (sp >= a.nsplit) break;  // uniform
         const uint32_t xw[4] = {mp[sp][e].x, mp[sp][e].y, mp[sp][e].z, mp[sp][e].w};
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
@@ -1105,20 +1124,20 @@ __global__ __launch_bounds__(256) void k_dv_sy(const DvsArgs a) {
           sacc[2 * q + 1] += __uint_as_float(xw[q] & 0xffff0000u);
         }
       }
-      const int mbi = (tid >> 7) + 2 * e;
+      const int mbi = (gt >> 7) + 2 * e;
       const int lj = (mbi & 1) * 32 + (pl & 31), gj = j0 + lj;
 #pragma unroll
       for (int q = 0; q < 4; ++q)
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
           const int li = (mbi >> 1) * 32 + sy_piece_row(pl, ph, q, u), gi = ic * 64 + li;
-          const float val = (gi < a.T && gi > gj) ? sacc[2 * q + u] : 0.f;
+          const float val = (live && gi < a.T && gi > gj) ? sacc[2 * q + u] : 0.f;
           *reinterpret_cast<bf16_t*>(mblk + li * 128 + (((lj >> 3) ^ (2 * (li & 3))) * 16) + (lj & 7) * 2) = f2bf(val);
         }
     }
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
-      const int e = tid + 256 * u, r = e >> 5, c = e & 31;
+      const int e = gt + 256 * u, r = e >> 5, c = e & 31;
       *reinterpret_cast<uint4*>(dblk + r * 512 + ((c ^ (4 * (r & 3))) * 16)) = dp[u];
     }
   };
@@ -1142,14 +1161,14 @@ __global__ __launch_bounds__(256) void k_dv_sy(const DvsArgs a) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][c][r] = 0.f;
 
-  const int per_h = nic - ic0;
-  const int total = per_h * (h_hi - h_lo);
-  if (total > 0) load_chunk(h_lo, ic0);
-  for (int it = 0; it < total; ++it) {
-    const int ic = ic0 + it % per_h;
-    __syncthreads();  // the previous chunk's fragment reads are done
-    store_chunk(ic);
-    if (it + 1 < total) load_chunk(h_lo + (it + 1) / per_h, ic0 + (it + 1) % per_h);
+  load_chunk(grp);
+  // step k: the group's item grp + 2 k into its blocks, then the load of item
+  // grp + 2 (k + 1), then the MFMAs.  A group past its last item stages a
+  // zero M block (its MFMAs add zeros).
+  for (int k = 0; k < nk; ++k) {
+    __syncthreads();  // the previous step's fragment reads are done
+    store_chunk(grp + 2 * k, k < ng);
+    load_chunk(grp + 2 * (k + 1));
     __syncthreads();
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
@@ -1167,6 +1186,19 @@ __global__ __launch_bounds__(256) void k_dv_sy(const DvsArgs a) {
         for (int c = 0; c < 2; ++c) acc[i][c] = mma(fa[i], fb[c], acc[i][c]);
     }
   }
+  // group 1's sums into group 0's
+  __syncthreads();  // the blocks' last fragment reads are done
+  float* const red = reinterpret_cast<float*>(dv_lds);  // [wave][value][lane], 64 KB
+  if (grp == 1) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) red[(w * 64 + (i * 2 + c) * 16 + r) * 64 + lane] = acc[i][c][r];
+  }
+  __syncthreads();
+  if (grp == 1) return;
   TO* o = static_cast<TO*>(a.o) + b * a.o0 + hv * a.o1;
 #pragma unroll
   for (int i = 0; i < 2; ++i)
@@ -1176,7 +1208,8 @@ __global__ __launch_bounds__(256) void k_dv_sy(const DvsArgs a) {
       for (int r = 0; r < 16; ++r) {
         const int j = j0 + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
         const int d = 64 * w + 32 * c + (lane & 31);
-        if (j < a.T && d < a.D) o[int64_t(j) * a.o2 + d] = from_f<TO>(acc[i][c][r]);
+        const float val = acc[i][c][r] + red[(w * 64 + (i * 2 + c) * 16 + r) * 64 + lane];
+        if (j < a.T && d < a.D) o[int64_t(j) * a.o2 + d] = from_f<TO>(val);
       }
 }
 
@@ -1860,14 +1893,14 @@ int sy_bwd_dv(const bdh_tensor4* q, const bdh_tensor4* v, const bdh_tensor4* dou
   const dim3 gd(unsigned((T + 63) / 64), unsigned(B * Hv));
   const bool o16 = dv->dtype == BDH_BF16;
   if (p.nsplit <= 2) {
-    if (o16) BDH_LAUNCH("k_dv_sy", (k_dv_sy<bf16_t, 2>), gd, dim3(256), 0, s, d);
-    else BDH_LAUNCH("k_dv_sy", (k_dv_sy<float, 2>), gd, dim3(256), 0, s, d);
+    if (o16) BDH_LAUNCH("k_dv_sy", (k_dv_sy<bf16_t, 2>), gd, dim3(512), 0, s, d);
+    else BDH_LAUNCH("k_dv_sy", (k_dv_sy<float, 2>), gd, dim3(512), 0, s, d);
   } else if (p.nsplit <= 4) {
-    if (o16) BDH_LAUNCH("k_dv_sy", (k_dv_sy<bf16_t, 4>), gd, dim3(256), 0, s, d);
-    else BDH_LAUNCH("k_dv_sy", (k_dv_sy<float, 4>), gd, dim3(256), 0, s, d);
+    if (o16) BDH_LAUNCH("k_dv_sy", (k_dv_sy<bf16_t, 4>), gd, dim3(512), 0, s, d);
+    else BDH_LAUNCH("k_dv_sy", (k_dv_sy<float, 4>), gd, dim3(512), 0, s, d);
   } else {
-    if (o16) BDH_LAUNCH("k_dv_sy", (k_dv_sy<bf16_t, 8>), gd, dim3(256), 0, s, d);
-    else BDH_LAUNCH("k_dv_sy", (k_dv_sy<float, 8>), gd, dim3(256), 0, s, d);
+    if (o16) BDH_LAUNCH("k_dv_sy", (k_dv_sy<bf16_t, 8>), gd, dim3(512), 0, s, d);
+    else BDH_LAUNCH("k_dv_sy", (k_dv_sy<float, 8>), gd, dim3(512), 0, s, d);
   }
   return BDH_OK;
 }
