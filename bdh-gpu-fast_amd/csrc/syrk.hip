@@ -1447,7 +1447,11 @@ __global__ __launch_bounds__(512, 1) void k_sy_sv(const SvArgs a) {
 template <typename TO, typename TV>
 int launch_sy_sv(const SvArgs& sa, dim3 grid, hipStream_t s) {
   const int ns = sa.nsplit;
-  if (ns <= 2)
+  // one instantiation per split bound: a wider one re-reads the last split
+  // for every split past nsplit
+  if (ns == 1)
+    BDH_LAUNCH("k_sy_sv", (k_sy_sv<TO, TV, 1>), grid, dim3(512), 0, s, sa);
+  else if (ns <= 2)
     BDH_LAUNCH("k_sy_sv", (k_sy_sv<TO, TV, 2>), grid, dim3(512), 0, s, sa);
   else if (ns <= 4)
     BDH_LAUNCH("k_sy_sv", (k_sy_sv<TO, TV, 4>), grid, dim3(512), 0, s, sa);
@@ -1892,7 +1896,10 @@ int sy_bwd_dv(const bdh_tensor4* q, const bdh_tensor4* v, const bdh_tensor4* dou
   d.D = int(D);
   const dim3 gd(unsigned((T + 63) / 64), unsigned(B * Hv));
   const bool o16 = dv->dtype == BDH_BF16;
-  if (p.nsplit <= 2) {
+  if (p.nsplit == 1) {
+    if (o16) BDH_LAUNCH("k_dv_sy", (k_dv_sy<bf16_t, 1>), gd, dim3(512), 0, s, d);
+    else BDH_LAUNCH("k_dv_sy", (k_dv_sy<float, 1>), gd, dim3(512), 0, s, d);
+  } else if (p.nsplit <= 2) {
     if (o16) BDH_LAUNCH("k_dv_sy", (k_dv_sy<bf16_t, 2>), gd, dim3(512), 0, s, d);
     else BDH_LAUNCH("k_dv_sy", (k_dv_sy<float, 2>), gd, dim3(512), 0, s, d);
   } else if (p.nsplit <= 4) {
