@@ -1252,14 +1252,15 @@ __global__ __launch_bounds__(512, 1) void k_sy_sv(const SvArgs a) {
   constexpr int VL = sizeof(TV) == 2 ? 1 : 2;  // 16-byte loads per 8 V elements
   // Workgroups go to the XCDs round robin by linear id L.  The row blocks of
   // slab s run on XCD s % 8, the XCD whose L2 took the slab's partial tiles
-  // in the score kernel (L = 8 (nrbk (s / 8) + k) + s % 8 for the k-th block
-  // of the slab).  Row blocks have 1..nrb key chunks, so the block index is
-  // rotated by the slab: every XCD gets every block length.
-  const int nrbk = a.nrbk;
+  // in the score kernel.  On each XCD the row blocks go longest first (block
+  // rb has rb + 1 key chunks): the k-th workgroup of XCD x is slab
+  // 8 (k % nsx) + x, block nrbk - 1 - k / nsx, so when the grid takes more than
+  // one round of the CUs the last workgroups to start are the short ones.
+  const int nrbk = a.nrbk, nsx = (a.nslab + 7) / 8;
   const int L = blockIdx.x, xcdv = L & 7, kk = L >> 3;
-  const int slab = (kk / nrbk) * 8 + xcdv;
+  const int slab = (kk % nsx) * 8 + xcdv;
   if (slab >= a.nslab) return;
-  const int rb = (kk % nrbk + slab) % nrbk + a.rb0;
+  const int rb = nrbk - 1 - kk / nsx + a.rb0;
   const int b = slab / a.H, h = slab - b * a.H, hv = a.Hv == 1 ? 0 : h;
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   const int r0 = rb * 64;

@@ -100,10 +100,11 @@ def check_scores(B, nh, T, N, strides, numel):
 def sv_grid(nslab, nrb):
     """csrc/syrk.hip k_sy_sv: (rb, slab) of each linear workgroup id (None past the slabs)."""
     out = []
-    for L in range(8 * ((nslab + 7) // 8) * nrb):
+    nsx = (nslab + 7) // 8
+    for L in range(8 * nsx * nrb):
         xcd, kk = L & 7, L >> 3
-        slab = (kk // nrb) * 8 + xcd
-        out.append(None if slab >= nslab else ((kk % nrb + slab) % nrb, slab))
+        slab = (kk % nsx) * 8 + xcd
+        out.append(None if slab >= nslab else (nrb - 1 - kk // nsx, slab))
     return out
 
 
@@ -118,6 +119,10 @@ def check_sv(B, nh, T, D, p, v_strides, v_numel):
     live = [g for g in grid if g is not None]
     assert sorted(live) == sorted((rb, s) for s in range(nslab) for rb in range(nrb))
     assert all(g[1] % 8 == L % 8 for L, g in enumerate(grid) if g is not None)
+    # on each XCD the row blocks (rb + 1 key chunks each) start longest first
+    for x in range(8):
+        rbs = [g[0] for L, g in enumerate(grid) if L % 8 == x and g is not None]
+        assert rbs == sorted(rbs, reverse=True)
     for d0 in range(0, D, 256):
         Dc = min(256, D - d0)
         assert Dc % 8 == 0
