@@ -268,6 +268,9 @@ int bdh_layer_norm_rows(const bdh_tensor4* x, const bdh_tensor4* y,
  * While enabled, every kernel the library launches is bracketed by HIP events
  * on its stream.  bdh_profile_collect() waits for the recorded events and
  * returns up to `max` (name, milliseconds) records, then clears the log.
+ * The events leave each kernel's duration as it is, but the runtime then
+ * starts a launch only after the previous one has ended (several
+ * microseconds between kernels), so time whole steps with profiling off.
  */
 void bdh_profile_enable(int32_t on);
 int bdh_profile_collect(char* names, int32_t name_len, float* ms, int32_t max);
