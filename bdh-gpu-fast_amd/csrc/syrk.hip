@@ -27,11 +27,13 @@
 //     * A barrier between the two k16 halves of a stage, fragments of the
 //       next half read before the current half's MFMAs.
 //     * v_mfma_f32_32x32x16_bf16 with fp32 accumulators; the epilogue stores
-//       the partial tiles [slab][tile][split][256][256] as bf16.
+//       the partial tiles [slab][tile][split] as bf16 in MFMA fragment order
+//       (whole 1 KB fragment rows per store).
 //  3. k_sy_sv: out = tril(sum over splits of S, -1) V, score blocks and V rows
 //     staged in LDS, V read as MFMA fragments with ds_read_b64_tr_b16.
-// Backward (bf16 self attention without RoPE): k_dq_sy (dQ = G X) and k_dv_sy
-// (dV from the score tiles of k_sy_scores), both with transposing LDS reads.
+// Backward (bf16 self attention): k_dq_sy (dQ = G X; with RoPE, R^T applied
+// to its fp32 sums in the epilogue) and k_dv_sy (dV from the score tiles of
+// k_sy_scores), both with transposing LDS reads.
 #include <algorithm>
 #include <type_traits>
 #include <utility>
