@@ -43,6 +43,9 @@ __all__ = [
     "tril_score_v_save",
     "tril_score_v_bwd_saved",
     "tril_rope_score_v_bwd",
+    "rope_keeps_scores",
+    "tril_rope_score_v_save",
+    "tril_rope_score_v_bwd_saved",
     "rope_rotate",
     "relu_mul",
     "gated_gemm",
@@ -76,6 +79,9 @@ EXPORTED_SYMBOLS = (
     "bdh_tril_score_v_bwd_saved",
     "bdh_tril_rope_score_v_bwd_workspace",
     "bdh_tril_rope_score_v_bwd",
+    "bdh_tril_rope_score_v_keeps_scores",
+    "bdh_tril_rope_score_v_bwd_saved_workspace",
+    "bdh_tril_rope_score_v_bwd_saved",
     "bdh_relu_mul",
     "bdh_gated_gemm",
     "bdh_small_gemm_workspace",
@@ -136,6 +142,9 @@ def _load():
         "bdh_tril_score_v_bwd_saved": (ctypes.c_int, [P, P, P, P, P, vp, sz, vp, sz, vp]),
         "bdh_tril_rope_score_v_bwd_workspace": (sz, [i64, i64, i64, i64, i64, i64, i32]),
         "bdh_tril_rope_score_v_bwd": (ctypes.c_int, [P, P, P, fp, i64, P, P, vp, sz, vp]),
+        "bdh_tril_rope_score_v_keeps_scores": (ctypes.c_int, [P, P, ctypes.POINTER(sz)]),
+        "bdh_tril_rope_score_v_bwd_saved_workspace": (sz, [i64, i64, i64, i64, i64, i64, i32]),
+        "bdh_tril_rope_score_v_bwd_saved": (ctypes.c_int, [P, P, P, fp, i64, P, P, vp, sz, vp, sz, vp]),
         "bdh_relu_mul": (ctypes.c_int, [P, P, P, vp]),
         "bdh_layer_norm_rows": (ctypes.c_int, [P, P, P, vp]),
         "bdh_gated_gemm": (ctypes.c_int, [P, P, P, P, vp]),
@@ -331,6 +340,66 @@ def tril_rope_score_v(
         )
     _check(rc, "tril_rope_score_v")
     return out
+
+
+def rope_keeps_scores(x: torch.Tensor, v: torch.Tensor) -> bool:
+    """Whether ``tril_rope_score_v(x, v, ...)`` (no ``qr_out``) leaves reusable
+    score tiles in its workspace."""
+    if not (x.is_cuda and v.is_cuda) or x.dim() != 4 or v.dim() != 4:
+        return False
+    return bool(_lib.bdh_tril_rope_score_v_keeps_scores(ctypes.byref(_t4(x)), ctypes.byref(_t4(v)), None))
+
+
+def tril_rope_score_v_save(
+    x: torch.Tensor, v: torch.Tensor, freqs: torch.Tensor, rope_start: int = 0
+) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
+    """:func:`tril_rope_score_v` that also returns its workspace when it holds
+    the score tiles (:func:`rope_keeps_scores`), for
+    :func:`tril_rope_score_v_bwd_saved`; else ``(out, None)``."""
+    dev = _require_device(x, v)
+    B, H, T, N = x.shape
+    f, fptr = _freqs_ptr(freqs, N, dev)
+    out = torch.empty(B, H, T, v.size(-1), dtype=x.dtype, device=dev)
+    with torch.cuda.device(dev):
+        need = _lib.bdh_tril_score_v_workspace(B, H, T, N, v.size(-1), _dtype_code(x))
+        ws, nb = _workspace(need, dev)
+        rc = _lib.bdh_tril_rope_score_v(
+            ctypes.byref(_t4(x)), ctypes.byref(_t4(v)), ctypes.byref(_t4(out)), fptr, int(rope_start), None,
+            ws.data_ptr() if ws is not None else None, nb, _stream(dev),
+        )
+    _check(rc, "tril_rope_score_v")
+    return out, (ws if rope_keeps_scores(x, v) else None)
+
+
+def tril_rope_score_v_bwd_saved(
+    x: torch.Tensor,
+    v: torch.Tensor,
+    dout: torch.Tensor,
+    freqs: torch.Tensor,
+    rope_start: int,
+    scores: torch.Tensor,
+    *,
+    dv: Optional[torch.Tensor] = None,
+) -> Tuple[torch.Tensor, torch.Tensor]:
+    """``(dx, dv)`` of :func:`tril_rope_score_v` from the score tiles kept by
+    :func:`tril_rope_score_v_save` on the same ``x``, ``v``, ``freqs`` and
+    ``rope_start`` (no recompute of the tiles)."""
+    dev = _require_device(x, v, dout, scores, dv)
+    B, H, T, N = x.shape
+    f, fptr = _freqs_ptr(freqs, N, dev)
+    dx = torch.empty_like(x, memory_format=torch.contiguous_format)
+    if dv is None:
+        dv = torch.empty_like(v, memory_format=torch.contiguous_format)
+    with torch.cuda.device(dev):
+        need = _lib.bdh_tril_rope_score_v_bwd_saved_workspace(B, H, v.size(1), T, N, v.size(-1), _dtype_code(x))
+        ws, nb = _workspace(need, dev)
+        rc = _lib.bdh_tril_rope_score_v_bwd_saved(
+            ctypes.byref(_t4(x)), ctypes.byref(_t4(v)), ctypes.byref(_t4(dout)), fptr, int(rope_start),
+            ctypes.byref(_t4(dx)), ctypes.byref(_t4(dv)), scores.data_ptr(), scores.numel() * scores.element_size(),
+            ws.data_ptr() if ws is not None else None, nb, _stream(dev),
+        )
+    _check(rc, "tril_rope_score_v_bwd_saved")
+    return dx, dv
 
 
 # ------------------------------------------------------------ CPU entries

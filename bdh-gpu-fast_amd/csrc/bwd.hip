@@ -306,6 +306,61 @@ int rope_fast_bwd(const bdh_tensor4* x, const bdh_tensor4* v, const bdh_tensor4*
   return step(sy_dq(w + p.r_g, p.tpad, &qr, dx, s, freqs, rope_start));
 }
 
+// The fused RoPE op's backward from the score tiles its forward kept
+// (relative layout when the forward rotated about the tile centres): R(x) at
+// absolute positions by one streaming pass, dV from the kept tiles, G from dO
+// and V, then dx = R^T(G R(x)) as in rope_fast_bwd.  Workspace: [R(x) bf16 |
+// G bf16].
+size_t rope_saved_bwd_bytes(int64_t B, int64_t H, int64_t T, int64_t N, size_t* g_off, int64_t* tpad) {
+  const BwdPlan p = plan_bwd(B, H, T, N, true, true, false);
+  const size_t off = align_up(size_t(B * H) * size_t(T) * size_t(N) * 2, 256);
+  if (g_off) *g_off = off;
+  if (tpad) *tpad = p.tpad;
+  return off + size_t(B * H) * size_t(p.tpad) * size_t(p.tpad) * 2;
+}
+
+int rope_saved_bwd(const bdh_tensor4* x, const bdh_tensor4* v, const bdh_tensor4* dout, const bdh_tensor4* dx,
+                   const bdh_tensor4* dv, const float* freqs, int64_t rope_start, const void* scores,
+                   size_t scores_bytes, void* ws, size_t ws_bytes, hipStream_t s) {
+  const int64_t B = x->size[0], H = x->size[1], T = x->size[2], N = x->size[3];
+  const int64_t D = v->size[3];
+  size_t off = 0, kept = 0;
+  int rel = 0;
+  if (scores == nullptr || !sy_rope_keeps_scores(x, v, &off, &kept, &rel)) return BDH_ERR_ARG;
+  if (scores_bytes < kept) return BDH_ERR_WORKSPACE;
+  size_t g_off = 0;
+  int64_t tpad = 0;
+  const size_t need = rope_saved_bwd_bytes(B, H, T, N, &g_off, &tpad);
+  if (ws == nullptr || ws_bytes < need) return BDH_ERR_WORKSPACE;
+  // the shapes every step below takes (checked here, so no step declines
+  // after another has run)
+  if (dout->dtype != BDH_BF16 || v->dtype != BDH_BF16) return BDH_ERR_DTYPE;
+  if (D < 64 || D > 256 || D % 64 != 0 || N % 256 != 0 || T > 65535) return BDH_ERR_SHAPE;
+  if (!rows16b(dout) || !rows16b(v) || !rows16b(dx) || !rows16b(dv)) return BDH_ERR_STRIDE;
+  if (dx->dtype != BDH_BF16 && dx->dtype != BDH_F32) return BDH_ERR_DTYPE;
+  if (tpad % 32 != 0 || tpad * tpad * 2 >= (int64_t(1) << 31)) return BDH_ERR_SHAPE;
+  if (((T - 1) * std::max(dout->stride[2], v->stride[2]) + D) * 2 >= (int64_t(1) << 31)) return BDH_ERR_SHAPE;
+  char* w = static_cast<char*>(ws);
+  bdh_tensor4 qr{};
+  qr.data = w;
+  qr.size[0] = B;
+  qr.size[1] = H;
+  qr.size[2] = T;
+  qr.size[3] = N;
+  qr.stride[3] = 1;
+  qr.stride[2] = N;
+  qr.stride[1] = T * N;
+  qr.stride[0] = H * T * N;
+  qr.dtype = BDH_BF16;
+  auto step = [](int r) { return r == kNotEligible ? int(BDH_ERR_SHAPE) : r; };
+  BDH_TRY(step(sy_rope_abs(x, freqs, rope_start, &qr, s)));
+  const void* tiles = static_cast<const char*>(scores) + off;
+  if (numel4(dv) > 0) BDH_TRY(step(sy_bwd_dv(&qr, v, dout, dv, nullptr, 0, s, tiles, rel)));
+  if (numel4(dx) == 0) return BDH_OK;
+  BDH_TRY(step(sy_bwd_g(dout, v, w + g_off, tpad, s)));
+  return step(sy_dq(w + g_off, tpad, &qr, dx, s, freqs, rope_start));
+}
+
 bool vec4_rows(const bdh_tensor4* t) {
   const int64_t es = esize(t->dtype);
   if ((reinterpret_cast<uintptr_t>(t->data) % (4 * es)) != 0) return false;
@@ -585,6 +640,37 @@ extern "C" size_t bdh_tril_rope_score_v_bwd_workspace(int64_t B, int64_t H, int6
   (void)Hv;
   (void)Dv;
   return plan_bwd(B, H, T, N, x_dtype == BDH_BF16, false, true).ws_bytes;
+}
+
+extern "C" int bdh_tril_rope_score_v_keeps_scores(const bdh_tensor4* x, const bdh_tensor4* v, size_t* scores_bytes) {
+  size_t off = 0, kept = 0;
+  int rel = 0;
+  const bool keep = check_view(x) == BDH_OK && check_view(v) == BDH_OK && v->size[0] == x->size[0] &&
+                    v->size[2] == x->size[2] && (v->size[1] == 1 || v->size[1] == x->size[1]) &&
+                    x->size[3] % 256 == 0 && v->size[3] % 64 == 0 && sy_rope_keeps_scores(x, v, &off, &kept, &rel);
+  if (scores_bytes) *scores_bytes = keep ? kept : 0;
+  return keep ? 1 : 0;
+}
+
+extern "C" size_t bdh_tril_rope_score_v_bwd_saved_workspace(int64_t B, int64_t H, int64_t Hv, int64_t T,
+                                                            int64_t N, int64_t Dv, int32_t x_dtype) {
+  (void)Hv;
+  (void)Dv;
+  if (x_dtype != BDH_BF16) return 0;
+  return rope_saved_bwd_bytes(B, H, T, N, nullptr, nullptr);
+}
+
+extern "C" int bdh_tril_rope_score_v_bwd_saved(const bdh_tensor4* x, const bdh_tensor4* v, const bdh_tensor4* dout,
+                                               const float* freqs, int64_t rope_start, const bdh_tensor4* dx,
+                                               const bdh_tensor4* dv, const void* scores, size_t scores_bytes,
+                                               void* workspace, size_t workspace_bytes, bdh_stream stream) {
+  BDH_TRY(check_bwd(x, nullptr, v, dout, dx, nullptr, dv));
+  if (freqs == nullptr && x->size[3] > 0) return BDH_ERR_ARG;
+  if (x->size[3] % 2 != 0) return BDH_ERR_SHAPE;
+  if (rope_start < 0 || rope_start + x->size[2] > (int64_t(1) << 24)) return BDH_ERR_ARG;
+  if (numel4(dx) == 0 && numel4(dv) == 0) return BDH_OK;
+  return rope_saved_bwd(x, v, dout, dx, dv, freqs, rope_start, scores, scores_bytes, workspace, workspace_bytes,
+                        static_cast<hipStream_t>(stream));
 }
 
 extern "C" int bdh_tril_rope_score_v_bwd(const bdh_tensor4* x, const bdh_tensor4* v, const bdh_tensor4* dout,

@@ -69,8 +69,20 @@ int sy_past(const bdh_tensor4* q, const bdh_tensor4* k, const bdh_tensor4* v, co
 size_t sy_bwd_workspace(int64_t B, int64_t H, int64_t T, int64_t N);
 // saved: the score tiles left by the forward on the same q (its workspace), used
 // instead of recomputing them (then ws may be NULL).
+// rel: the saved tiles came from the relative-RoPE forward (their fragment
+// slot order).
 int sy_bwd_dv(const bdh_tensor4* q, const bdh_tensor4* v, const bdh_tensor4* dout, const bdh_tensor4* dv, void* ws,
-              size_t ws_bytes, hipStream_t s, const void* saved = nullptr);
+              size_t ws_bytes, hipStream_t s, const void* saved = nullptr, int rel = 0);
+// Whether bdh_tril_rope_score_v(x, x, v) without the R(x) copy runs the MFMA
+// path: its score tiles then sit at *tiles_offset of its workspace, whose
+// first *kept_bytes the backward from saved tiles needs, in the relative
+// layout when *rel.
+bool sy_rope_keeps_scores(const bdh_tensor4* x, const bdh_tensor4* v, size_t* tiles_offset, size_t* kept_bytes,
+                          int* rel);
+// R(x) at positions rope_start + t into a contiguous bf16 out (the bits of
+// the absolute score pass's R(x) copy).
+int sy_rope_abs(const bdh_tensor4* x, const float* freqs, int64_t rope_start, const bdh_tensor4* out,
+                hipStream_t s);
 // Whether bdh_tril_score_v(q, q, v) runs the MFMA path; its workspace then
 // starts with the score tiles (*scores_bytes of them) that sy_bwd_dv can reuse.
 bool sy_keeps_scores(const bdh_tensor4* q, const bdh_tensor4* v, size_t* scores_bytes);

@@ -244,6 +244,46 @@ __global__ __launch_bounds__(256) void k_rope_table(const float* __restrict__ fr
   cs[(int64_t(m >> 4) * T + t) * 16 + (m & 15)] = rope_cs(float(rope_start + t), freqs[2 * m]);
 }
 
+// R(x) at absolute positions (rope_start + t), bf16, with the table kernel's
+// (cos, sin) entries and the score kernel's rotation, so the bits equal the
+// R(x) copy the absolute score pass writes.  A thread takes one 16-byte chunk
+// (four pairs) of row t, makes its four entries once and rotates that chunk
+// in every (b, h) slab, four slabs at a time.  out is contiguous (B, H, T, N).
+struct RopeAbsArgs {
+  const bf16_t* x;
+  int64_t x0, x1, x2;
+  bf16_t* out;
+  const float* freqs;
+  int64_t rope_start;
+  int H, T, N, nslab, cpr;  // cpr: 16-byte chunks per row (N / 8)
+};
+
+__global__ __launch_bounds__(256) void k_rope_abs(const RopeAbsArgs a) {
+  const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= int64_t(a.T) * a.cpr) return;
+  const int c = int(i % a.cpr), t = int(i / a.cpr);
+  const float pos = float(a.rope_start + t);
+  const float* f = a.freqs + 8 * c;
+  const u32x4 cs{rope_cs(pos, f[0]), rope_cs(pos, f[2]), rope_cs(pos, f[4]), rope_cs(pos, f[6])};
+  const int64_t xo = int64_t(t) * a.x2 + 8 * c, oo = int64_t(t) * a.N + 8 * c;
+  const int64_t ostep = int64_t(a.T) * a.N;
+  auto xrow = [&](int sl) {
+    const int b = sl / a.H, h = sl - b * a.H;
+    return a.x + b * a.x0 + h * a.x1 + xo;
+  };
+  int sl = 0;
+  for (; sl + 4 <= a.nslab; sl += 4) {
+    u32x4 xv[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) xv[k] = *reinterpret_cast<const u32x4*>(xrow(sl + k));
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      *reinterpret_cast<u32x4*>(a.out + (sl + k) * ostep + oo) = rot_chunk<false>(xv[k], cs);
+  }
+  for (; sl < a.nslab; ++sl)
+    *reinterpret_cast<u32x4*>(a.out + sl * ostep + oo) = rot_chunk<false>(*reinterpret_cast<const u32x4*>(xrow(sl)), cs);
+}
+
 // Diagonal tiles (Q = K) in pairs: the 36 lower 32x32 blocks of one diagonal
 // tile are split into four wave programs of 9 blocks; waves 0-3 run them on
 // the first tile of the pair and waves 4-7 on the second, so each SIMD issues
@@ -1050,6 +1090,7 @@ struct DvsArgs {
   void* o;
   int64_t o0, o1, o2;
   int H, Hv, T, D;
+  int rel = 0;  // the tiles came from the relative-RoPE score kernel (fragment slot order)
 };
 
 template <typename TO, int NS>
@@ -1095,7 +1136,7 @@ __global__ __launch_bounds__(512) void k_dv_sy(const DvsArgs a) {
       const int mbi = (gt >> 7) + 2 * e;
       const int rbk = ((i0 & 255) >> 5) + (mbi >> 1), cbk = ((j0 & 255) >> 5) + (mbi & 1);
       // (no blocks above a diagonal tile's diagonal: read the diagonal block, masked below)
-      const int off = sy_piece(dt, 0, rbk, dt && cbk > rbk ? rbk : cbk, pl, ph);
+      const int off = sy_piece(dt, a.rel, rbk, dt && cbk > rbk ? rbk : cbk, pl, ph);
 #pragma unroll
       for (int sp = 0; sp < NS; ++sp)
         mp[sp][e] = *reinterpret_cast<const uint4*>(p + int64_t(min(sp, a.nsplit - 1)) * kSyTileElems + off);
@@ -1561,6 +1602,49 @@ bool sy_cold_check(const bdh_tensor4* q, const bdh_tensor4* k, const bdh_tensor4
 
 }  // namespace
 
+bool sy_rope_keeps_scores(const bdh_tensor4* x, const bdh_tensor4* v, size_t* tiles_offset, size_t* kept_bytes,
+                          int* rel) {
+  SyPlan p;
+  bool self = false;
+  // what sy_run does for the fused RoPE forward without the R(x) copy: the
+  // tiles follow the table region of the workspace, in the relative layout
+  // when a workgroup has at most 512 stages
+  if (v->size[3] < 1 || v->size[3] > 256 || !sy_cold_check(x, x, v, true, nullptr, p, self) || !self) return false;
+  const int max_stages = 2 * ((p.nchunk + p.nsplit - 1) / p.nsplit);
+  if (tiles_offset) *tiles_offset = p.table_bytes;
+  if (kept_bytes) *kept_bytes = p.table_bytes + p.part_bytes;
+  if (rel) *rel = max_stages <= 512 ? 1 : 0;
+  return true;
+}
+
+int sy_rope_abs(const bdh_tensor4* x, const float* freqs, int64_t rope_start, const bdh_tensor4* out,
+                hipStream_t s) {
+  const int64_t B = x->size[0], H = x->size[1], T = x->size[2], N = x->size[3];
+  if (x->dtype != BDH_BF16 || out->dtype != BDH_BF16 || N % 8 != 0 || !rows16(x)) return kNotEligible;
+  for (int i = 0; i < 4; ++i)
+    if (out->size[i] != x->size[i]) return kNotEligible;
+  if (out->stride[3] != 1 || out->stride[2] != N || out->stride[1] != T * N || out->stride[0] != H * T * N)
+    return kNotEligible;
+  const int64_t nthreads = T * (N / 8);
+  if (nthreads == 0 || B * H == 0) return BDH_OK;
+  if (B * H > (int64_t(1) << 24) || T > 65535 || H > 65535) return kNotEligible;
+  RopeAbsArgs a;
+  a.x = static_cast<const bf16_t*>(x->data);
+  a.x0 = x->stride[0];
+  a.x1 = x->stride[1];
+  a.x2 = x->stride[2];
+  a.out = static_cast<bf16_t*>(out->data);
+  a.freqs = freqs;
+  a.rope_start = rope_start;
+  a.H = int(H);
+  a.T = int(T);
+  a.N = int(N);
+  a.nslab = int(B * H);
+  a.cpr = int(N / 8);
+  BDH_LAUNCH("k_rope_abs", k_rope_abs, dim3(unsigned((nthreads + 255) / 256)), dim3(256), 0, s, a);
+  return BDH_OK;
+}
+
 bool sy_keeps_scores(const bdh_tensor4* q, const bdh_tensor4* v, size_t* scores_bytes) {
   SyPlan p;
   bool self = false;
@@ -1837,7 +1921,7 @@ size_t sy_bwd_workspace(int64_t B, int64_t H, int64_t T, int64_t N) {
 // into ws (or saved by the forward), then k_dv_sy.  kNotEligible when the
 // shapes fall outside it.
 int sy_bwd_dv(const bdh_tensor4* q, const bdh_tensor4* v, const bdh_tensor4* dout, const bdh_tensor4* dv, void* ws,
-              size_t ws_bytes, hipStream_t s, const void* saved) {
+              size_t ws_bytes, hipStream_t s, const void* saved, int rel) {
   const int64_t B = q->size[0], H = q->size[1], T = q->size[2], N = q->size[3];
   const int64_t Hv = v->size[1], D = v->size[3];
   if (q->dtype != BDH_BF16 || dout->dtype != BDH_BF16) return kNotEligible;
@@ -1897,6 +1981,7 @@ int sy_bwd_dv(const bdh_tensor4* q, const bdh_tensor4* v, const bdh_tensor4* dou
   d.Hv = int(Hv);
   d.T = int(T);
   d.D = int(D);
+  d.rel = saved != nullptr ? rel : 0;
   const dim3 gd(unsigned((T + 63) / 64), unsigned(B * Hv));
   const bool o16 = dv->dtype == BDH_BF16;
   if (p.nsplit == 1) {

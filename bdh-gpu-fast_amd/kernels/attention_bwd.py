@@ -141,24 +141,43 @@ class TrilRopeSelfAttnFn(torch.autograd.Function):
 
     The backward returns dx (RoPE^T of the merged dQR) and dV; ``freqs`` is a
     constant buffer (no gradient), like the reference's detached cos/sin.
+    Without ``qr_out`` the forward's bf16 score tiles are kept for the
+    backward when the shapes allow it (``BDH_ATTN_SAVE_SCORES=0`` turns this
+    off), so the backward recomputes none of them.
     """
 
     @staticmethod
     def forward(ctx, x, V, freqs, rope_start: int, qr_out=None):  # type: ignore[override]
         ctx.rope_start = int(rope_start)
-        ctx.save_for_backward(x, V, freqs)
+        scores = None
         with torch.no_grad():
-            return hip_attn.tril_rope_score_v(x, V, freqs, rope_start, qr_out=qr_out)
+            if qr_out is None and x.dtype == torch.bfloat16 and _save_scores():
+                out, scores = hip_attn.tril_rope_score_v_save(x, V, freqs, rope_start)
+            else:
+                out = hip_attn.tril_rope_score_v(x, V, freqs, rope_start, qr_out=qr_out)
+        ctx.has_scores = scores is not None
+        if scores is not None:
+            ctx.save_for_backward(x, V, freqs, scores)
+        else:
+            ctx.save_for_backward(x, V, freqs)
+        return out
 
     @staticmethod
     def backward(ctx, dO):  # type: ignore[override]
-        x, V, freqs = ctx.saved_tensors
+        if ctx.has_scores:
+            x, V, freqs, scores = ctx.saved_tensors
+        else:
+            x, V, freqs = ctx.saved_tensors
         # bf16 x: V enters the products as bf16, as in the forward (and as the
         # reference's autocast matmul casts it), which lets the backward run on
         # the MFMA kernels; dV comes back in V's own dtype
         Vc = V.to(x.dtype) if x.dtype == torch.bfloat16 else V
         dV = torch.empty_like(V, memory_format=torch.contiguous_format)
-        dx, dV = hip_attn.tril_rope_score_v_bwd(x, Vc, dO.to(x.dtype), freqs, ctx.rope_start, dv=dV)
+        if ctx.has_scores:
+            dx, dV = hip_attn.tril_rope_score_v_bwd_saved(x, Vc, dO.to(x.dtype), freqs, ctx.rope_start, scores,
+                                                          dv=dV)
+        else:
+            dx, dV = hip_attn.tril_rope_score_v_bwd(x, Vc, dO.to(x.dtype), freqs, ctx.rope_start, dv=dV)
         return dx, dV, None, None, None
 
 

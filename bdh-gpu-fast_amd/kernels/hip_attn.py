@@ -201,6 +201,26 @@ def tril_score_v_bwd_saved(x, v, dout, scores):
     return ext.tril_score_v_bwd_saved(_last_dim_unit(x), _last_dim_unit(v), _last_dim_unit(dout), scores)
 
 
+def tril_rope_score_v_save(x: torch.Tensor, v: torch.Tensor, freqs: torch.Tensor, rope_start: int = 0):
+    """Fused RoPE forward that also returns its score tiles for the backward
+    (``(out, scores)``; ``scores`` is None when the shapes take another path)."""
+    _check_cold_shapes(x, x, v)
+    if x.size(-1) % 2 != 0:
+        raise ValueError(f"RoPE last dim must be even, got {x.size(-1)}")
+    ext = _require(x, v)
+    check_pair_freqs(freqs)
+    return ext.tril_rope_score_v_save(_last_dim_unit(x), _last_dim_unit(v), freqs, int(rope_start))
+
+
+def tril_rope_score_v_bwd_saved(x, v, dout, freqs, rope_start: int, scores, *, dv=None):
+    """dx and dv of the fused RoPE op from the score tiles saved by
+    :func:`tril_rope_score_v_save`."""
+    ext = _require(x, v, dout, scores)
+    return ext.tril_rope_score_v_bwd_saved(
+        _last_dim_unit(x), _last_dim_unit(v), _last_dim_unit(dout), freqs, int(rope_start), scores, dv=dv
+    )
+
+
 def tril_rope_score_v_bwd(x, v, dout, freqs, rope_start: int = 0, *, dv=None):
     ext = _require(x, v, dout)
     return ext.tril_rope_score_v_bwd(

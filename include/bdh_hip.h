@@ -214,6 +214,31 @@ int bdh_tril_rope_score_v_bwd(const bdh_tensor4* x, const bdh_tensor4* v,
                               size_t workspace_bytes, bdh_stream stream);
 
 /*
+ * The same gradients from the score tiles the forward kept (the save-S side
+ * of the reference's choice, as bdh_tril_score_v_bwd_saved; the reference's
+ * default autograd keeps S, attention_bwd.py:259-291).
+ * bdh_tril_rope_score_v_keeps_scores returns 1 when bdh_tril_rope_score_v(x, v,
+ * out, freqs, rope_start, NULL, ...) on these views runs the bf16 MFMA path
+ * and leaves its score tiles in its workspace, of which the backward needs
+ * the first *scores_bytes; else 0.  bdh_tril_rope_score_v_bwd_saved takes
+ * that workspace as `scores` (x, v, freqs and rope_start those of the
+ * forward, x unchanged since) and recomputes no score tile: R(x) at absolute
+ * positions in one pass, dv from the kept tiles, dx as above.  Other views
+ * give BDH_ERR_ARG.  bf16 x, dout and v; D a multiple of 64 up to 256.
+ */
+int bdh_tril_rope_score_v_keeps_scores(const bdh_tensor4* x, const bdh_tensor4* v,
+                                       size_t* scores_bytes);
+size_t bdh_tril_rope_score_v_bwd_saved_workspace(int64_t B, int64_t H, int64_t Hv,
+                                                 int64_t T, int64_t N, int64_t Dv,
+                                                 int32_t x_dtype);
+int bdh_tril_rope_score_v_bwd_saved(const bdh_tensor4* x, const bdh_tensor4* v,
+                                    const bdh_tensor4* dout, const float* freqs,
+                                    int64_t rope_start, const bdh_tensor4* dx,
+                                    const bdh_tensor4* dv, const void* scores,
+                                    size_t scores_bytes, void* workspace,
+                                    size_t workspace_bytes, bdh_stream stream);
+
+/*
  * Consumer of the attention in the BDH layer: out = x * max(y, 0), elementwise.
  * Replaces the ReLU of encoder_v's output (bdh.py:914-925, `_bias_relu_`) and
  * the sparse product of _mlp_merge (bdh.py:927-945, `x_bthn * y_bthn`) in one

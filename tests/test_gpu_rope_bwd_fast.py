@@ -9,7 +9,9 @@ applying R^T to its fp32 sums in the epilogue.  Checked against the oracle's gra
 attention_bwd.py:45-83 composed with rope.py:543-556) at the bf16 tolerance
 (2e-2, relative Frobenius), against the generic kernels on the same inputs,
 and through autograd with an fp32 V (the AMP case: V is the LayerNorm output).
-Each case checks that the route ran (its dQ kernel in the launch log).
+Each case checks that the route ran (its dQ kernel in the launch log).  The
+route from the score tiles the forward kept (no recompute) is checked against
+the recompute route and the oracle.
 """
 
 from __future__ import annotations
@@ -137,3 +139,60 @@ def test_rope_backward_c2_width_batch0():
     ex, ev = rel_fro(np_of(dx[:1]), wx), rel_fro(np_of(dv[:1]), wv)
     print(f"C2 width batch 0: dx rel {ex:.3e}, dv rel {ev:.3e}", flush=True)
     assert ex <= TOL and ev <= TOL
+
+
+@pytest.mark.parametrize("shape", SHAPES)
+def test_rope_backward_from_saved_tiles(shape):
+    """The forward keeps its score tiles (relative layout) and the backward
+    recomputes none: R(x) from one pass, dV from the kept tiles.  dx equals the
+    recompute route's bit for bit (the same R(x) and G); dV is within the bf16
+    tolerance of it and of the oracle (the kept tiles rotate about the tile
+    centres, the recomputed ones by absolute positions)."""
+    B, H, T, N, D, Hv, start = shape
+    print(f"rope bwd saved tiles {shape}", flush=True)
+    x = O.bf16_round(latent((B, H, T, N), 10))
+    v = O.bf16_round(normal((B, Hv, T, D), 11))
+    dO = O.bf16_round(normal((B, H, T, D), 12))
+    f = O.get_freqs(N)
+    xd, vd, dd = to_dev(x, BF), to_dev(v, BF), to_dev(dO, BF)
+    fd = torch.from_numpy(f).to(DEV)
+    out, scores = ext.tril_rope_score_v_save(xd, vd, fd, start)
+    assert scores is not None
+    assert torch.equal(out, ext.tril_rope_score_v(xd, vd, fd, start))
+    (sx, sv), names = _names(lambda: ext.tril_rope_score_v_bwd_saved(xd, vd, dd, fd, start, scores))
+    assert "k_rope_abs" in names and "k_dq_sy" in names and "k_dv_sy" in names, names
+    assert not any(n.startswith("k_sy_scores") and n != "k_sy_scores_g" for n in names), names
+    rx, rv = ext.tril_rope_score_v_bwd(xd, vd, dd, fd, start)
+    assert torch.equal(sx, rx)
+    assert rel_fro(np_of(sv), np_of(rv)) <= TOL
+    wx, wv = O.tril_rope_score_v_backward(x, v, dO, f, start)
+    ex, ev = rel_fro(np_of(sx), wx), rel_fro(np_of(sv), wv)
+    print(f"  dx rel {ex:.3e}, dv rel {ev:.3e}", flush=True)
+    assert ex <= TOL and ev <= TOL
+
+
+def test_rope_autograd_saved_tiles_switch(monkeypatch):
+    """bdh_attn_rope under autograd keeps the forward's tiles by default and
+    recomputes them with BDH_ATTN_SAVE_SCORES=0: same dx bits, dV within the
+    bf16 tolerance."""
+    B, H, T, N, D, start = 2, 4, 300, 512, 128, 4
+    x = O.bf16_round(latent((B, H, T, N), 13))
+    v = normal((B, 1, T, D), 14)
+    dO = O.bf16_round(normal((B, H, T, D), 15))
+    fd = torch.from_numpy(O.get_freqs(N)).to(DEV)
+    grads = {}
+    for save in ("1", "0"):
+        monkeypatch.setenv("BDH_ATTN_SAVE_SCORES", save)
+        xd = to_dev(x, BF).requires_grad_(True)
+        vd = to_dev(v, torch.float32).requires_grad_(True)
+
+        def run():
+            out = kernels.bdh_attn_rope(xd, vd, fd, start, impl="hip")
+            out.backward(to_dev(dO, BF))
+            return out
+
+        _, names = _names(run)
+        assert ("k_rope_abs" in names) == (save == "1"), names
+        grads[save] = (xd.grad.clone(), vd.grad.clone())
+    assert torch.equal(grads["1"][0], grads["0"][0])
+    assert rel_fro(np_of(grads["1"][1]), np_of(grads["0"][1])) <= TOL
