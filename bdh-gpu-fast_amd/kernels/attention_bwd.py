@@ -6,11 +6,13 @@ Mirrors the reference surface kernels/attention_bwd.py:
 ``strict_tril_attn`` (:294-320) and ``_env_autograd_enabled`` (:323-325).
 
 For ``impl="hip"`` the forward is the HIP kernel and the backward is the HIP
-analytic backward (one library call: recomputed scores, G = dS + dS^T, merged
-dQ, head-summed dV).  ``eager`` keeps the reference's dense PyTorch math.
+analytic backward (one library call: the score tiles the forward kept, or
+recomputed ones, G = dS + dS^T, merged dQ, head-summed dV).  ``eager`` keeps
+the reference's dense PyTorch math.
 
 :class:`TrilRopeSelfAttnFn` covers the fused RoPE entry (Q = K = RoPE(x)):
-its backward returns dx directly (RoPE and its transpose fused in-kernel).
+its backward returns dx directly (RoPE and its transpose fused in-kernel),
+from the forward's kept score tiles when the shapes allow it.
 """
 
 from __future__ import annotations
