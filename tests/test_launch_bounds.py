@@ -3,11 +3,12 @@
 CPU only: the launch plans and index formulas of the kernels the harness's
 HIP legs run (csrc/syrk.hip: k_sy_scores work items, their x loads and
 partial-tile stores, k_sy_sv's partial, V and output accesses;
-csrc/decode.hip: k_decode_bf16's key, q and partial accesses) are restated
-here and evaluated over every work item, with the strides of the views the
-harness passes (x_sparse as the permuted (B, T, nh, N) encoder output, the
-packed KV cache's capacity-strided past views).  Each access must fall
-inside its buffer and every score tile must be computed exactly once.
+csrc/decode.hip: k_decode_bf16's key, q and partial accesses; the training
+backward's k_rope_abs and k_dv_sy) are restated here and evaluated over every
+work item, with the strides of the views the harness passes (x_sparse as the
+permuted (B, T, nh, N) encoder output, the packed KV cache's
+capacity-strided past views).  Each access must fall inside its buffer and
+every score tile must be computed exactly once.
 """
 
 import pytest
@@ -197,3 +198,59 @@ def test_a_planted_overrun_is_caught():
     with pytest.raises(AssertionError):
         check_scores(B, nh, T, N, (T * nh * N, N, nh * N + 1), B * T * nh * N)
     check_scores(B, nh, T, N, (T * nh * N, N, nh * N), B * T * nh * N)
+
+
+def check_rope_abs(B, nh, T, N, x_strides, x_numel):
+    """csrc/syrk.hip k_rope_abs: thread i < T * N / 8 takes chunk c = i % (N / 8) of row
+    t = i / (N / 8) in every slab: x at b x0 + h x1 + t x2 + 8 c + [0, 8), out
+    (contiguous (B, nh, T, N)) at (slab T + t) N + 8 c + [0, 8)."""
+    cpr, nslab = N // 8, B * nh
+    nthreads = T * cpr
+    grid = (nthreads + 255) // 256
+    for i in (0, 1, cpr - 1, cpr, nthreads - cpr, nthreads - 1, grid * 256 - 1):
+        if i >= nthreads:
+            continue  # the kernel returns
+        c, t = i % cpr, i // cpr
+        for sl in (0, 1, nslab - 1):
+            b, h = divmod(sl, nh)
+            assert b * x_strides[0] + h * x_strides[1] + t * x_strides[2] + 8 * c + 8 <= x_numel
+            assert (sl * T + t) * N + 8 * c + 8 <= nslab * T * N
+    # every output chunk has exactly one writer: (t, c) from the thread, the slab from its loop
+    assert nthreads * nslab * 8 == nslab * T * N
+
+
+def check_dv(B, nh, Hv, T, N, D, p):
+    """csrc/syrk.hip k_dv_sy: grid (T / 64, B Hv), two groups taking items g, g + 2, ...
+    of (head, 64-row chunk ic >= rb); loads of item min(it, total - 1); M pieces of tile
+    (ti, tj), ti >= tj, splits < nsplit; dO rows < T (others zero); dV rows < T."""
+    nrb = (T + 63) // 64
+    S, ntl = p["nsplit"], p["ntl"]
+    part_elems = B * nh * ntl * S * TILE_ELEMS
+    for rb in range(nrb):
+        for bv in range(B * Hv):
+            b, hv = divmod(bv, Hv)
+            h_lo, h_hi = (0, nh) if Hv == 1 else (hv, hv + 1)
+            per_h = nrb - rb
+            total = per_h * (h_hi - h_lo)
+            assert total >= 1
+            for grp in (0, 1):
+                nk = (total + 1) // 2
+                for k in range(nk + 1):  # steps plus the load issued after the last one
+                    it = min(grp + 2 * k, total - 1)
+                    h, ic = h_lo + it // per_h, rb + it % per_h
+                    assert h_lo <= h < h_hi and rb <= ic < nrb
+                    ti, tj = (ic * 64) >> 8, (rb * 64) >> 8
+                    assert tj <= ti
+                    slab = b * nh + h
+                    tile = ti * (ti + 1) // 2 + tj
+                    top = ((slab * ntl + tile) * S + S - 1) * TILE_ELEMS + 63 * 1024 + 512 + 63 * 8 + 8
+                    assert top <= part_elems
+
+
+@pytest.mark.parametrize("B,nh,T,N,D", [(32, 4, 512, 8192, 256), (3, 2, 300, 512, 64), (1, 3, 700, 768, 256)])
+def test_rope_backward_launches_stay_in_bounds(B, nh, T, N, D):
+    # the training backward from kept tiles: x_sparse as the permuted (B, T, nh, N) view
+    check_rope_abs(B, nh, T, N, (T * nh * N, N, nh * N), B * T * nh * N)
+    p = sy_plan(B * nh, T, N)
+    check_dv(B, nh, 1, T, N, D, p)
+    check_dv(B, nh, nh, T, N, D, p)
