@@ -307,16 +307,15 @@ int rope_fast_bwd(const bdh_tensor4* x, const bdh_tensor4* v, const bdh_tensor4*
 }
 
 // The fused RoPE op's backward from the score tiles its forward kept
-// (relative layout when the forward rotated about the tile centres): R(x) at
-// absolute positions by one streaming pass, dV from the kept tiles, G from dO
-// and V, then dx = R^T(G R(x)) as in rope_fast_bwd.  Workspace: [R(x) bf16 |
-// G bf16].
+// (relative layout when the forward rotated about the tile centres): dV from
+// the kept tiles, G from dO and V, then dx = R^T(G R(x)) with the dQ kernel
+// rotating x at absolute positions as it stages it, so R(x) is never
+// written.  Workspace: G bf16.
 size_t rope_saved_bwd_bytes(int64_t B, int64_t H, int64_t T, int64_t N, size_t* g_off, int64_t* tpad) {
   const BwdPlan p = plan_bwd(B, H, T, N, true, true, false);
-  const size_t off = align_up(size_t(B * H) * size_t(T) * size_t(N) * 2, 256);
-  if (g_off) *g_off = off;
+  if (g_off) *g_off = 0;
   if (tpad) *tpad = p.tpad;
-  return off + size_t(B * H) * size_t(p.tpad) * size_t(p.tpad) * 2;
+  return size_t(B * H) * size_t(p.tpad) * size_t(p.tpad) * 2;
 }
 
 int rope_saved_bwd(const bdh_tensor4* x, const bdh_tensor4* v, const bdh_tensor4* dout, const bdh_tensor4* dx,
@@ -341,24 +340,12 @@ int rope_saved_bwd(const bdh_tensor4* x, const bdh_tensor4* v, const bdh_tensor4
   if (tpad % 32 != 0 || tpad * tpad * 2 >= (int64_t(1) << 31)) return BDH_ERR_SHAPE;
   if (((T - 1) * std::max(dout->stride[2], v->stride[2]) + D) * 2 >= (int64_t(1) << 31)) return BDH_ERR_SHAPE;
   char* w = static_cast<char*>(ws);
-  bdh_tensor4 qr{};
-  qr.data = w;
-  qr.size[0] = B;
-  qr.size[1] = H;
-  qr.size[2] = T;
-  qr.size[3] = N;
-  qr.stride[3] = 1;
-  qr.stride[2] = N;
-  qr.stride[1] = T * N;
-  qr.stride[0] = H * T * N;
-  qr.dtype = BDH_BF16;
   auto step = [](int r) { return r == kNotEligible ? int(BDH_ERR_SHAPE) : r; };
-  BDH_TRY(step(sy_rope_abs(x, freqs, rope_start, &qr, s)));
   const void* tiles = static_cast<const char*>(scores) + off;
-  if (numel4(dv) > 0) BDH_TRY(step(sy_bwd_dv(&qr, v, dout, dv, nullptr, 0, s, tiles, rel)));
+  if (numel4(dv) > 0) BDH_TRY(step(sy_bwd_dv(x, v, dout, dv, nullptr, 0, s, tiles, rel)));
   if (numel4(dx) == 0) return BDH_OK;
   BDH_TRY(step(sy_bwd_g(dout, v, w + g_off, tpad, s)));
-  return step(sy_dq(w + g_off, tpad, &qr, dx, s, freqs, rope_start));
+  return step(sy_dq(w + g_off, tpad, x, dx, s, freqs, rope_start, true));
 }
 
 bool vec4_rows(const bdh_tensor4* t) {

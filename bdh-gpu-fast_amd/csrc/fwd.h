@@ -79,10 +79,6 @@ int sy_bwd_dv(const bdh_tensor4* q, const bdh_tensor4* v, const bdh_tensor4* dou
 // layout when *rel.
 bool sy_rope_keeps_scores(const bdh_tensor4* x, const bdh_tensor4* v, size_t* tiles_offset, size_t* kept_bytes,
                           int* rel);
-// R(x) at positions rope_start + t into a contiguous bf16 out (the bits of
-// the absolute score pass's R(x) copy).
-int sy_rope_abs(const bdh_tensor4* x, const float* freqs, int64_t rope_start, const bdh_tensor4* out,
-                hipStream_t s);
 // Whether bdh_tril_score_v(q, q, v) runs the MFMA path; its workspace then
 // starts with the score tiles (*scores_bytes of them) that sy_bwd_dv can reuse.
 bool sy_keeps_scores(const bdh_tensor4* q, const bdh_tensor4* v, size_t* scores_bytes);
@@ -91,8 +87,9 @@ bool sy_keeps_scores(const bdh_tensor4* q, const bdh_tensor4* v, size_t* scores_
 int sy_bwd_g(const bdh_tensor4* dout, const bdh_tensor4* v, void* g, int64_t tpad, hipStream_t s);
 // Backward dQ = G X on the MFMA path (syrk.hip): bf16 X, self attention.
 // With freqs, out = R^T(G X) at positions rope_start + t (X = R(x)).
+// rot_b (with freqs): x is x itself, rotated in the kernel as it is staged.
 int sy_dq(const void* g, int64_t tpad, const bdh_tensor4* x, const bdh_tensor4* out, hipStream_t s,
-          const float* freqs = nullptr, int64_t rope_start = 0);
+          const float* freqs = nullptr, int64_t rope_start = 0, bool rot_b = false);
 // Backward of the fused RoPE op on the MFMA path (syrk.hip): the score tiles
 // of R(x) R(x)^T with R(x) written to qr (absolute positions; ws starts with
 // their (cos, sin) table, *tiles points at the tiles).

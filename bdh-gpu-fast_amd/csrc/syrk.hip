@@ -244,46 +244,6 @@ __global__ __launch_bounds__(256) void k_rope_table(const float* __restrict__ fr
   cs[(int64_t(m >> 4) * T + t) * 16 + (m & 15)] = rope_cs(float(rope_start + t), freqs[2 * m]);
 }
 
-// R(x) at absolute positions (rope_start + t), bf16, with the table kernel's
-// (cos, sin) entries and the score kernel's rotation, so the bits equal the
-// R(x) copy the absolute score pass writes.  A thread takes one 16-byte chunk
-// (four pairs) of row t, makes its four entries once and rotates that chunk
-// in every (b, h) slab, four slabs at a time.  out is contiguous (B, H, T, N).
-struct RopeAbsArgs {
-  const bf16_t* x;
-  int64_t x0, x1, x2;
-  bf16_t* out;
-  const float* freqs;
-  int64_t rope_start;
-  int H, T, N, nslab, cpr;  // cpr: 16-byte chunks per row (N / 8)
-};
-
-__global__ __launch_bounds__(256) void k_rope_abs(const RopeAbsArgs a) {
-  const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
-  if (i >= int64_t(a.T) * a.cpr) return;
-  const int c = int(i % a.cpr), t = int(i / a.cpr);
-  const float pos = float(a.rope_start + t);
-  const float* f = a.freqs + 8 * c;
-  const u32x4 cs{rope_cs(pos, f[0]), rope_cs(pos, f[2]), rope_cs(pos, f[4]), rope_cs(pos, f[6])};
-  const int64_t xo = int64_t(t) * a.x2 + 8 * c, oo = int64_t(t) * a.N + 8 * c;
-  const int64_t ostep = int64_t(a.T) * a.N;
-  auto xrow = [&](int sl) {
-    const int b = sl / a.H, h = sl - b * a.H;
-    return a.x + b * a.x0 + h * a.x1 + xo;
-  };
-  int sl = 0;
-  for (; sl + 4 <= a.nslab; sl += 4) {
-    u32x4 xv[4];
-#pragma unroll
-    for (int k = 0; k < 4; ++k) xv[k] = *reinterpret_cast<const u32x4*>(xrow(sl + k));
-#pragma unroll
-    for (int k = 0; k < 4; ++k)
-      *reinterpret_cast<u32x4*>(a.out + (sl + k) * ostep + oo) = rot_chunk<false>(xv[k], cs);
-  }
-  for (; sl < a.nslab; ++sl)
-    *reinterpret_cast<u32x4*>(a.out + sl * ostep + oo) = rot_chunk<false>(*reinterpret_cast<const u32x4*>(xrow(sl)), cs);
-}
-
 // Diagonal tiles (Q = K) in pairs: the 36 lower 32x32 blocks of one diagonal
 // tile are split into four wave programs of 9 blocks; waves 0-3 run them on
 // the first tile of the pair and waves 4-7 on the second, so each SIMD issues
@@ -883,8 +843,14 @@ __device__ __forceinline__ bf16x4 lds_tr4(const uint8_t* p) {
   return __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(p));
 }
 
-template <typename TO, bool ROPE = false>
+// ROTB (with ROPE): X is x itself and each lane rotates the B chunks it
+// loaded (positions rope_start + row) in LDS after they land and before the
+// barrier that hands the stage to the fragment reads, with the table
+// kernel's (cos, sin) entries and the score kernel's rotation, so the
+// product sees the bits of the R(x) copy the absolute score pass writes.
+template <typename TO, bool ROPE = false, bool ROTB = false>
 __global__ __launch_bounds__(kSyThreads, 1) void k_dq_sy(const DqsArgs a) {
+  static_assert(!ROTB || ROPE, "B rotation: RoPE output");
   const int bid = blockIdx.x;
   const int xcd = bid & 7, kk = bid >> 3;
   const int tiles = a.nti * a.ntn;
@@ -961,6 +927,28 @@ __global__ __launch_bounds__(kSyThreads, 1) void k_dq_sy(const DqsArgs a) {
   for (int i = 0; i < 8; ++i)
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[i][r] = 0.f;
+  // B rotation: this lane's two chunks of each stage (rows brow[u], pairs
+  // from element bcol[u] / 2) and their frequencies
+  float bfq[2][4];
+  if constexpr (ROTB) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) bfq[u][j] = a.freqs[(bcol[u] >> 1) + 2 * j];
+  }
+  auto rotate_b = [&](int st) __attribute__((always_inline)) {
+    if constexpr (ROTB) {
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        uint8_t* const pc = slot(st) + kSyBlk + u * 8192 + w * 1024 + lane * 16;
+        const u32x4 xv = *reinterpret_cast<const u32x4*>(pc);
+        const float pos = float(a.rope_start + st * 32 + brow[u]);
+        const u32x4 cs{rope_cs(pos, bfq[u][0]), rope_cs(pos, bfq[u][1]), rope_cs(pos, bfq[u][2]),
+                       rope_cs(pos, bfq[u][3])};
+        *reinterpret_cast<u32x4*>(pc) = rot_chunk<false>(xv, cs);
+      }
+    }
+  };
   bf16x8 f0[6], f1[6];
   auto read_frags = [&](bf16x8(&f)[6], int st, int hf) {
     const uint8_t* sl = slot(st);
@@ -985,6 +973,7 @@ __global__ __launch_bounds__(kSyThreads, 1) void k_dq_sy(const DqsArgs a) {
     dma_b(d, I1());
   }
   sy_wait<(lead - 1) * 4>();
+  rotate_b(0);
   sy_barrier();
   read_frags(f0, 0, 0);
   // stage s: second-half fragment reads; first-half MFMAs with the A chunks of
@@ -1002,6 +991,7 @@ __global__ __launch_bounds__(kSyThreads, 1) void k_dq_sy(const DqsArgs a) {
       if constexpr (m == 3) sy_wait<(lead - 2) * 4 + 2>();  // stage s+1 landed
     });
     __builtin_amdgcn_sched_barrier(0);
+    rotate_b(s + 1);
     sy_barrier();
     read_frags(f0, s + 1, 0);
     __builtin_amdgcn_sched_barrier(0);
@@ -1617,34 +1607,6 @@ bool sy_rope_keeps_scores(const bdh_tensor4* x, const bdh_tensor4* v, size_t* ti
   return true;
 }
 
-int sy_rope_abs(const bdh_tensor4* x, const float* freqs, int64_t rope_start, const bdh_tensor4* out,
-                hipStream_t s) {
-  const int64_t B = x->size[0], H = x->size[1], T = x->size[2], N = x->size[3];
-  if (x->dtype != BDH_BF16 || out->dtype != BDH_BF16 || N % 8 != 0 || !rows16(x)) return kNotEligible;
-  for (int i = 0; i < 4; ++i)
-    if (out->size[i] != x->size[i]) return kNotEligible;
-  if (out->stride[3] != 1 || out->stride[2] != N || out->stride[1] != T * N || out->stride[0] != H * T * N)
-    return kNotEligible;
-  const int64_t nthreads = T * (N / 8);
-  if (nthreads == 0 || B * H == 0) return BDH_OK;
-  if (B * H > (int64_t(1) << 24) || T > 65535 || H > 65535) return kNotEligible;
-  RopeAbsArgs a;
-  a.x = static_cast<const bf16_t*>(x->data);
-  a.x0 = x->stride[0];
-  a.x1 = x->stride[1];
-  a.x2 = x->stride[2];
-  a.out = static_cast<bf16_t*>(out->data);
-  a.freqs = freqs;
-  a.rope_start = rope_start;
-  a.H = int(H);
-  a.T = int(T);
-  a.N = int(N);
-  a.nslab = int(B * H);
-  a.cpr = int(N / 8);
-  BDH_LAUNCH("k_rope_abs", k_rope_abs, dim3(unsigned((nthreads + 255) / 256)), dim3(256), 0, s, a);
-  return BDH_OK;
-}
-
 bool sy_keeps_scores(const bdh_tensor4* q, const bdh_tensor4* v, size_t* scores_bytes) {
   SyPlan p;
   bool self = false;
@@ -1818,7 +1780,7 @@ int sy_past(const bdh_tensor4* q, const bdh_tensor4* k, const bdh_tensor4* v, co
 // R^T(G X) at positions rope_start + t (x is then R(x)).  kNotEligible when
 // the shapes fall outside it.
 int sy_dq(const void* g, int64_t tpad, const bdh_tensor4* x, const bdh_tensor4* out, hipStream_t s,
-          const float* freqs, int64_t rope_start) {
+          const float* freqs, int64_t rope_start, bool rot_b) {
   const int64_t B = x->size[0], H = x->size[1], T = x->size[2], N = x->size[3];
   if (x->dtype != BDH_BF16 || N % kSyTile != 0 || T < 1 || !rows16(x)) return kNotEligible;
   if (out->size[0] != B || out->size[1] != H || out->size[2] != T || out->size[3] != N) return kNotEligible;
@@ -1848,7 +1810,12 @@ int sy_dq(const void* g, int64_t tpad, const bdh_tensor4* x, const bdh_tensor4* 
   a.freqs = freqs;
   a.rope_start = rope_start;
   const dim3 gs{unsigned(grid)};
-  if (freqs != nullptr) {
+  if (freqs != nullptr && rot_b) {
+    if (out->dtype == BDH_BF16)
+      BDH_LAUNCH("k_dq_sy", (k_dq_sy<bf16_t, true, true>), gs, dim3(kSyThreads), 0, s, a);
+    else
+      BDH_LAUNCH("k_dq_sy", (k_dq_sy<float, true, true>), gs, dim3(kSyThreads), 0, s, a);
+  } else if (freqs != nullptr) {
     if (out->dtype == BDH_BF16)
       BDH_LAUNCH("k_dq_sy", (k_dq_sy<bf16_t, true>), gs, dim3(kSyThreads), 0, s, a);
     else

@@ -222,8 +222,9 @@ int bdh_tril_rope_score_v_bwd(const bdh_tensor4* x, const bdh_tensor4* v,
  * and leaves its score tiles in its workspace, of which the backward needs
  * the first *scores_bytes; else 0.  bdh_tril_rope_score_v_bwd_saved takes
  * that workspace as `scores` (x, v, freqs and rope_start those of the
- * forward, x unchanged since) and recomputes no score tile: R(x) at absolute
- * positions in one pass, dv from the kept tiles, dx as above.  Other views
+ * forward, x unchanged since) and recomputes no score tile: dv from the kept
+ * tiles, dx as above with x rotated (absolute positions) as the dQ product
+ * stages it, so R(x) is never written.  Other views
  * give BDH_ERR_ARG.  bf16 x, dout and v; D a multiple of 64 up to 256.
  */
 int bdh_tril_rope_score_v_keeps_scores(const bdh_tensor4* x, const bdh_tensor4* v,

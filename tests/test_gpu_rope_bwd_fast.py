@@ -144,10 +144,11 @@ def test_rope_backward_c2_width_batch0():
 @pytest.mark.parametrize("shape", SHAPES)
 def test_rope_backward_from_saved_tiles(shape):
     """The forward keeps its score tiles (relative layout) and the backward
-    recomputes none: R(x) from one pass, dV from the kept tiles.  dx equals the
-    recompute route's bit for bit (the same R(x) and G); dV is within the bf16
-    tolerance of it and of the oracle (the kept tiles rotate about the tile
-    centres, the recomputed ones by absolute positions)."""
+    recomputes none: dV from the kept tiles, dx with x rotated as the dQ
+    kernel stages it.  dx equals the recompute route's bit for bit (the same
+    R(x) bits and G); dV is within the bf16 tolerance of it and of the oracle
+    (the kept tiles rotate about the tile centres, the recomputed ones by
+    absolute positions)."""
     B, H, T, N, D, Hv, start = shape
     print(f"rope bwd saved tiles {shape}", flush=True)
     x = O.bf16_round(latent((B, H, T, N), 10))
@@ -160,7 +161,8 @@ def test_rope_backward_from_saved_tiles(shape):
     assert scores is not None
     assert torch.equal(out, ext.tril_rope_score_v(xd, vd, fd, start))
     (sx, sv), names = _names(lambda: ext.tril_rope_score_v_bwd_saved(xd, vd, dd, fd, start, scores))
-    assert "k_rope_abs" in names and "k_dq_sy" in names and "k_dv_sy" in names, names
+    assert "k_dq_sy" in names and "k_dv_sy" in names, names
+    assert "k_rope_table" not in names, names
     assert not any(n.startswith("k_sy_scores") and n != "k_sy_scores_g" for n in names), names
     rx, rv = ext.tril_rope_score_v_bwd(xd, vd, dd, fd, start)
     assert torch.equal(sx, rx)
@@ -192,7 +194,7 @@ def test_rope_autograd_saved_tiles_switch(monkeypatch):
             return out
 
         _, names = _names(run)
-        assert ("k_rope_abs" in names) == (save == "1"), names
+        assert ("k_rope_table" in names) == (save == "0"), names
         grads[save] = (xd.grad.clone(), vd.grad.clone())
     assert torch.equal(grads["1"][0], grads["0"][0])
     assert rel_fro(np_of(grads["1"][1]), np_of(grads["0"][1])) <= TOL

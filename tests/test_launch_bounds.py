@@ -4,7 +4,7 @@ CPU only: the launch plans and index formulas of the kernels the harness's
 HIP legs run (csrc/syrk.hip: k_sy_scores work items, their x loads and
 partial-tile stores, k_sy_sv's partial, V and output accesses;
 csrc/decode.hip: k_decode_bf16's key, q and partial accesses; the training
-backward's k_rope_abs and k_dv_sy) are restated here and evaluated over every
+backward's k_dq_sy B loads on x and k_dv_sy) are restated here and evaluated over every
 work item, with the strides of the views the harness passes (x_sparse as the
 permuted (B, T, nh, N) encoder output, the packed KV cache's
 capacity-strided past views).  Each access must fall inside its buffer and
@@ -200,23 +200,26 @@ def test_a_planted_overrun_is_caught():
     check_scores(B, nh, T, N, (T * nh * N, N, nh * N), B * T * nh * N)
 
 
-def check_rope_abs(B, nh, T, N, x_strides, x_numel):
-    """csrc/syrk.hip k_rope_abs: thread i < T * N / 8 takes chunk c = i % (N / 8) of row
-    t = i / (N / 8) in every slab: x at b x0 + h x1 + t x2 + 8 c + [0, 8), out
-    (contiguous (B, nh, T, N)) at (slab T + t) N + 8 c + [0, 8)."""
-    cpr, nslab = N // 8, B * nh
-    nthreads = T * cpr
-    grid = (nthreads + 255) // 256
-    for i in (0, 1, cpr - 1, cpr, nthreads - cpr, nthreads - 1, grid * 256 - 1):
-        if i >= nthreads:
-            continue  # the kernel returns
-        c, t = i % cpr, i // cpr
-        for sl in (0, 1, nslab - 1):
-            b, h = divmod(sl, nh)
-            assert b * x_strides[0] + h * x_strides[1] + t * x_strides[2] + 8 * c + 8 <= x_numel
-            assert (sl * T + t) * N + 8 * c + 8 <= nslab * T * N
-    # every output chunk has exactly one writer: (t, c) from the thread, the slab from its loop
-    assert nthreads * nslab * 8 == nslab * T * N
+def check_dq_rot(B, nh, T, N, x_strides, x_numel, tpad):
+    """csrc/syrk.hip k_dq_sy with the B rotation, on x itself: B chunk u of lane (w, lane)
+    is row min(32 st + brow, T - 1), brow = 2 (8 u + w) + lane / 32, columns n0 + 8 (pb ^ 4 (brow & 3))
+    + [0, 8), pb = lane % 32; its frequencies at element (n0 + 8 (...)) + 2 j + [0, 1], j < 4."""
+    ntn = N // TILE
+    nst = tpad // 32
+    for b, h in ((0, 0), (B - 1, nh - 1)):
+        for tn in (0, ntn - 1):
+            n0 = tn * TILE
+            for st in (0, nst - 1):
+                for u in (0, 1):
+                    for w in (0, 7):
+                        for lane in (0, 31, 32, 63):
+                            brow = 2 * (8 * u + w) + lane // 32
+                            row = min(32 * st + brow, T - 1)
+                            col = n0 + 8 * ((lane % 32) ^ (4 * (brow & 3)))
+                            assert col + 8 <= N and col + 2 * 3 + 1 < N
+                            assert b * x_strides[0] + h * x_strides[1] + row * x_strides[2] + col + 8 <= x_numel
+                            # the byte offset within the slab fits the DMA's 32-bit voffset
+                            assert (row * x_strides[2] + col) * 2 < 2 ** 32
 
 
 def check_dv(B, nh, Hv, T, N, D, p):
@@ -250,7 +253,8 @@ def check_dv(B, nh, Hv, T, N, D, p):
 @pytest.mark.parametrize("B,nh,T,N,D", [(32, 4, 512, 8192, 256), (3, 2, 300, 512, 64), (1, 3, 700, 768, 256)])
 def test_rope_backward_launches_stay_in_bounds(B, nh, T, N, D):
     # the training backward from kept tiles: x_sparse as the permuted (B, T, nh, N) view
-    check_rope_abs(B, nh, T, N, (T * nh * N, N, nh * N), B * T * nh * N)
+    tpad = ((T + 63) // 64) * 64
+    check_dq_rot(B, nh, T, N, (T * nh * N, N, nh * N), B * T * nh * N, tpad)
     p = sy_plan(B * nh, T, N)
     check_dv(B, nh, 1, T, N, D, p)
     check_dv(B, nh, nh, T, N, D, p)
