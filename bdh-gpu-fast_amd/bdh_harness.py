@@ -149,14 +149,16 @@ def _encode_relu_epilogue(x: torch.Tensor, wc: torch.Tensor, zero: torch.Tensor,
 def _gated_product(x_bthn: torch.Tensor, y_ln: torch.Tensor, w: torch.Tensor, wt=None) -> torch.Tensor:
     """x_bthn * relu(encoder_v GEMM), token-major (B, T, nh, N).
 
-    bf16 (K a multiple of 32, N of 8): one HIP kernel, the GEMM with the gated
-    product as its epilogue (its output never reaches HBM).  Otherwise one
+    bf16 (K a multiple of 32, N of 8, one head's y and wt under 4 GiB): one HIP
+    kernel, the GEMM with the gated product as its epilogue (its output never
+    reaches HBM).  Otherwise one
     batched GEMM (nh, B*T, D) @ (nh, D, N) on contiguous operands into
     head-major rows, then one HIP pass for the ReLU and the product."""
     B, T, nh, N = x_bthn.shape
     D = y_ln.size(-1)
     dt = _compute_dtype(x_bthn)
-    if dt == torch.bfloat16 and x_bthn.dtype == torch.bfloat16 and D % 32 == 0 and N % 8 == 0:
+    fits = B * nh * T * D * 2 <= 2**32 and N * D * 2 <= 2**32  # the kernel's 32-bit DMA offsets
+    if dt == torch.bfloat16 and x_bthn.dtype == torch.bfloat16 and D % 32 == 0 and N % 8 == 0 and fits:
         if wt is None:
             wt = w.transpose(1, 2).to(dt).contiguous()  # (nh, N, D)
         return kernels.gated_gemm(y_ln.to(dt).contiguous(), wt, x_bthn)

@@ -11,7 +11,10 @@
 // product is formed in fp32 and rounded once to the output dtype, the same
 // value torch's bf16 / fp32 elementwise product gives.
 #include "common.h"
+#include "lds_dma.h"
 #include "tile_gemm.h"
+
+#pragma clang diagnostic ignored "-Winline-asm"
 
 namespace bdh {
 
@@ -89,9 +92,9 @@ __global__ __launch_bounds__(256) void k_relu_mul(ReluMulArgs a) {
 //
 // Tiles of 256 rows (tokens) x 128 columns of one head, 8 waves of 64 x 64
 // (2 x 2 MFMA 32x32x16 blocks), K in stages of 32 through a ring of three LDS
-// buffers, the global loads issued two stages ahead (16-byte chunk c of row r
-// at c ^ ((r >> 2) & 3), conflict-free fragment reads).  Two workgroups per
-// CU, so one tile's epilogue overlaps another's main loop.  Tiles run column
+// buffers filled by LDS DMA two stages ahead (16-byte chunk c of row r at
+// c ^ ((r >> 2) & 3), conflict-free fragment reads; no register staging).
+// Two workgroups per CU, so one tile's epilogue overlaps another's main loop.  Tiles run column
 // blocks fastest (the tiles in flight on an XCD share their A block and cover
 // whole rows of one head), each XCD a contiguous range.
 // Epilogue: relu(acc) rounded to bf16 (the value the unfused GEMM would
@@ -121,7 +124,7 @@ __device__ __forceinline__ f32x16 mma_bf16(bf16x8 a, bf16x8 b, f32x16 c) {
 __device__ __forceinline__ int g_sw(int row, int c) { return row * 64 + ((c ^ ((row >> 2) & 3)) * 16); }
 
 __global__ __launch_bounds__(512, 2) void k_gated_gemm(const GatedArgs a) {
-  __shared__ __attribute__((aligned(16))) uint8_t g_lds[kGLds];
+  __shared__ __attribute__((aligned(1024))) uint8_t g_lds[kGLds];
   const int bid = blockIdx.x, xcd = bid & 7, kk = bid >> 3;
   if (kk >= a.per_xcd) return;
   const int64_t t = int64_t(xcd) * a.per_xcd + kk;
@@ -132,42 +135,32 @@ __global__ __launch_bounds__(512, 2) void k_gated_gemm(const GatedArgs a) {
   const int g = int(t - int64_t(h) * per_head);
   const int mbi = g / a.nnb, nbi = g - mbi * a.nnb;
   const int m0 = mbi * kGM, n0 = nbi * kGN;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
 
-  // loader: A rows lr and lr + 128, B row lr; 16-byte chunk lc of the 64-byte stage row
-  const int lr = tid >> 2, lc = tid & 3;
-  const bf16_t* ap[2];
+  // LDS DMA: instruction u of wave w fills bytes [(8u + w) KB, +1 KB) of a
+  // stage: u = 0, 1 the A rows 16 (8u + w) + lane / 4, u = 2 the B rows
+  // 16 w + lane / 4; the lane's 16-byte slot lane & 3 of the row holds chunk
+  // (lane & 3) ^ ((row >> 2) & 3)
+  const int dc = (lane & 3) ^ ((lane >> 4) & 3);
+  uint32_t aoffd[2];
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int m = min(m0 + lr + 128 * i, a.M - 1);
+  for (int u = 0; u < 2; ++u) {
+    const int m = min(m0 + 16 * (8 * u + w) + (lane >> 2), a.M - 1);
     const int b = m / a.T, tt = m - b * a.T;
-    ap[i] = a.y + b * a.y0 + h * a.y1 + tt * a.y2 + lc * 8;
+    aoffd[u] = uint32_t((b * a.y0 + tt * a.y2 + dc * 8) * 2);
   }
-  const bf16_t* bp = a.w + h * a.w1 + int64_t(min(n0 + lr, a.N - 1)) * a.w2 + lc * 8;
-  const int aoff0 = g_sw(lr, lc), aoff1 = g_sw(lr + 128, lc), boff = kGStageA + g_sw(lr, lc);
-  // two stages in flight in named registers (slot 0: q0*, slot 1: q1*), so none
-  // of them is addressed through memory
-  uint4 q0a, q0b, q0c, q1a, q1b, q1c;
-  auto gload = [&](int s, auto slotc) __attribute__((always_inline)) {
-    const int k = s * kGK;
-    const uint4 va = *reinterpret_cast<const uint4*>(ap[0] + k);
-    const uint4 vb = *reinterpret_cast<const uint4*>(ap[1] + k);
-    const uint4 vc = *reinterpret_cast<const uint4*>(bp + k);
-    if constexpr (decltype(slotc)::value == 0) {
-      q0a = va; q0b = vb; q0c = vc;
-    } else {
-      q1a = va; q1b = vb; q1c = vc;
-    }
+  const uint32_t boffd = uint32_t((int64_t(min(n0 + 16 * w + (lane >> 2), a.N - 1)) * a.w2 + dc * 8) * 2);
+  const void* ybase = sgpr_ptr(a.y + h * a.y1);
+  const void* wbase = sgpr_ptr(a.w + h * a.w1);
+  const uint32_t lds0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_u8*)g_lds);
+  auto issue = [&](int s) __attribute__((always_inline)) {
+    const uint32_t m0b = lds0 + uint32_t((s % kGRing) * kGStage) + uint32_t(w) * 1024u;
+    const uint32_t kb = uint32_t(s * kGK * 2);
+    dma16<0>(m0b, ybase, aoffd[0] + kb);
+    dma16<8192>(m0b, ybase, aoffd[1] + kb);
+    dma16<kGStageA>(m0b, wbase, boffd + kb);
   };
-  auto lstore = [&](int buf, auto slotc) __attribute__((always_inline)) {
-    uint8_t* base = g_lds + buf * kGStage;
-    constexpr bool z = decltype(slotc)::value == 0;
-    *reinterpret_cast<uint4*>(base + aoff0) = z ? q0a : q1a;
-    *reinterpret_cast<uint4*>(base + aoff1) = z ? q0b : q1b;
-    *reinterpret_cast<uint4*>(base + boff) = z ? q0c : q1c;
-  };
-  using S0 = std::integral_constant<int, 0>;
-  using S1 = std::integral_constant<int, 1>;
 
   // fragments: wave (wm, wn) owns rows 64 wm.., columns 64 wn..; lane row / column fr, k half fh
   const int wm = w >> 1, wn = w & 1, fr = lane & 31, fh = lane >> 5;
@@ -188,17 +181,33 @@ __global__ __launch_bounds__(512, 2) void k_gated_gemm(const GatedArgs a) {
       for (int r = 0; r < 16; ++r) acc[i][c][r] = 0.f;
 
   const int nst = a.K / kGK;
-  gload(0, S0());
-  if (nst > 1) gload(1, S1());
-  lstore(0, S0());
+  issue(0);
+  if (nst > 1) {
+    issue(1);
+    sy_wait<3>();
+  } else {
+    sy_wait<0>();
+  }
   __syncthreads();
-  int buf = 0;
-  // stage s keeps its registers in slot s & 1; the loop is unrolled by two so
-  // the slots are compile-time register indices
-  auto stage = [&](int s, auto slotc) __attribute__((always_inline)) {
-    constexpr int SL = decltype(slotc)::value;
-    if (s + 2 < nst) gload(s + 2, slotc);
-    const uint8_t* base = g_lds + buf * kGStage;
+  constexpr int kEp = (kGM * kGN / 8) / 512;
+  const int cc = tid & 15, n = n0 + cc * 8;
+  uint4 xr[kEp];
+  auto load_x = [&](int e) __attribute__((always_inline)) {
+    const int m = min(m0 + (tid >> 4) + 32 * e, a.M - 1);
+    const int b = m / a.T, tt = m - b * a.T;
+    xr[e] = *reinterpret_cast<const uint4*>(a.x + b * a.x0 + tt * a.x1 + h * a.x2 + min(n, a.N - 8));
+  };
+  for (int s = 0; s < nst; ++s) {
+    // stage s + 2 goes to the slot of stage s - 1, which every wave finished
+    // before the barrier that ended stage s - 1
+    if (s + 2 < nst) issue(s + 2);
+    // the epilogue's x chunks go out with the last stage, so their latency
+    // runs under its MFMAs
+    if (s == nst - 1) {
+#pragma unroll
+      for (int e = 0; e < kEp; ++e) load_x(e);
+    }
+    const uint8_t* base = g_lds + (s % kGRing) * kGStage;
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       bf16x8 va[2], vb[2];
@@ -212,31 +221,20 @@ __global__ __launch_bounds__(512, 2) void k_gated_gemm(const GatedArgs a) {
 #pragma unroll
         for (int c = 0; c < 2; ++c) acc[i][c] = mma_bf16(va[i], vb[c], acc[i][c]);
     }
-    // the next ring buffer was last read in stage s - 2, which every wave
-    // finished before the barrier that ended it
-    const int nbuf = buf == kGRing - 1 ? 0 : buf + 1;
-    if (s + 1 < nst) lstore(nbuf, std::integral_constant<int, SL ^ 1>());
-    __syncthreads();
-    buf = nbuf;
-  };
-  for (int s = 0; s < nst; s += 2) {
-    stage(s, S0());
-    if (s + 1 < nst) stage(s + 1, S1());
+    if (s + 1 < nst) {
+      if (s + 2 < nst)
+        sy_wait<3>();  // stage s + 1 landed (only s + 2 outstanding)
+      else
+        sy_wait<0>();
+      __syncthreads();
+    }
   }
+  __syncthreads();  // every wave's last fragment reads done before the output tile reuses the LDS
 
-  // epilogue: the tile's x chunks are loaded first (all in flight at once,
-  // from clamped addresses), then relu(acc) goes as bf16 into the LDS output
-  // tile, then the gated product.  Thread tid takes 16-byte chunk tid & 15 of
-  // rows (tid >> 4) + 32 e.
-  constexpr int kEp = (kGM * kGN / 8) / 512;
-  const int cc = tid & 15, n = n0 + cc * 8;
-  uint4 xr[kEp];
-#pragma unroll
-  for (int e = 0; e < kEp; ++e) {
-    const int m = min(m0 + (tid >> 4) + 32 * e, a.M - 1);
-    const int b = m / a.T, tt = m - b * a.T;
-    xr[e] = *reinterpret_cast<const uint4*>(a.x + b * a.x0 + tt * a.x1 + h * a.x2 + min(n, a.N - 8));
-  }
+  // epilogue: relu(acc) goes as bf16 into the LDS output tile, then the gated
+  // product with the x chunks loaded during the last stage (from clamped
+  // addresses).  Thread tid takes 16-byte chunk tid & 15 of rows
+  // (tid >> 4) + 32 e.
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
@@ -611,6 +609,10 @@ extern "C" int bdh_gated_gemm(const bdh_tensor4* y, const bdh_tensor4* wt, const
   if (!rows16(y) || !rows16(wt) || !rows16(x) || !rows16(out)) return BDH_ERR_STRIDE;
   const int64_t M = B * T;
   if (M >= (int64_t(1) << 31) || T >= (int64_t(1) << 31)) return BDH_ERR_SHAPE;
+  // the DMA takes 32-bit byte offsets from the per-head bases of y and wt
+  const int64_t y_span = (B - 1) * y->stride[0] + (T - 1) * y->stride[2] + K;
+  const int64_t w_span = (N - 1) * wt->stride[2] + K;
+  if (y_span * 2 > (int64_t(1) << 32) || w_span * 2 > (int64_t(1) << 32)) return BDH_ERR_SHAPE;
   GatedArgs a;
   a.y = static_cast<const bf16_t*>(y->data);
   a.y0 = y->stride[0];

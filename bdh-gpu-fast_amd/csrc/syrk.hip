@@ -39,6 +39,7 @@
 #include <utility>
 
 #include "fwd.h"
+#include "lds_dma.h"
 
 #pragma clang diagnostic ignored "-Winline-asm"
 
@@ -51,8 +52,6 @@ constexpr int kSyBlk = kSyTile * 64;   // bytes of one row block per stage (256 
 constexpr int kSySlot = 2 * kSyBlk;    // A and B row blocks
 constexpr int kSyLdsSlots = 5;    // 160 KB: x ring of 5 (plain), or 4 x + table or frequencies (fused)
 constexpr int kSyTileElems = kSyTile * kSyTile;
-
-typedef __attribute__((address_space(3))) uint8_t lds_u8;
 
 // Work item kinds.  kSyFull: tile (ta, tb), ta > tb, or any tile when Q != K;
 // kSyDiag2: diagonal tiles ta and tb; kSyDiag1: diagonal tile ta alone (tb =
@@ -115,35 +114,7 @@ __device__ inline uint32_t sy_item(const SyArgs& a, int itx) {
 __shared__ __attribute__((aligned(1024))) uint8_t sy_lds[kSyLdsSlots * kSySlot];  // 160 KB
 
 // ---------------------------------------------------------------- asm helpers
-// The x stream and the table are moved by LDS DMA issued from inline asm, so
-// the compiler neither counts them in its own vmcnt waits nor orders LDS
-// accesses behind them; the kernel waits for them explicitly (sy_wait).
-// A wave-uniform pointer made explicitly scalar (the asm takes it in SGPRs).
-__device__ __forceinline__ const void* sgpr_ptr(const void* p) {
-  const uint64_t v = reinterpret_cast<uint64_t>(p);
-  const uint32_t lo = __builtin_amdgcn_readfirstlane(uint32_t(v));
-  const uint32_t hi = __builtin_amdgcn_readfirstlane(uint32_t(v >> 32));
-  return reinterpret_cast<const void*>((uint64_t(hi) << 32) | lo);
-}
-
-// 16 bytes per lane from gbase + voff to LDS address m0base + IMM + 16 * lane.
-// The immediate keeps one scalar base per stage instead of one per instruction.
-template <int IMM>
-__device__ __forceinline__ void dma16(uint32_t m0base, const void* gbase, uint32_t voff) {
-  asm volatile("s_add_u32 m0, %0, %3\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
-               :
-               : "s"(m0base), "v"(voff), "s"(gbase), "i"(IMM)
-               : "memory", "m0", "scc");
-}
-
-// Wait until at most N vector-memory operations of this wave are outstanding
-// (they complete in issue order).
-template <int N>
-__device__ __forceinline__ void sy_wait() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
-
+// (LDS DMA, its waits and scalar pointers: lds_dma.h)
 __device__ __forceinline__ void sy_barrier() {
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   __builtin_amdgcn_s_barrier();

@@ -258,7 +258,8 @@ int bdh_relu_mul(const bdh_tensor4* x, const bdh_tensor4* y, const bdh_tensor4* 
  * ReLU) followed by the `x_bthn * y_bthn` of _mlp_merge (bdh.py:927-945); the
  * GEMM's output never reaches HBM.  y: (B, nh, T, K), the LayerNorm of the
  * attention output; wt: (1, nh, N, K), encoder_v transposed; x, out:
- * (B, T, nh, N).  K a multiple of 32, N of 8, rows 16-byte aligned.  The
+ * (B, T, nh, N).  K a multiple of 32, N of 8, rows 16-byte aligned; one
+ * head's view of y and of wt spans at most 4 GiB (else BDH_ERR_SHAPE).  The
  * GEMM result is rounded to bf16 after the ReLU, then multiplied by x.
  */
 int bdh_gated_gemm(const bdh_tensor4* y, const bdh_tensor4* wt, const bdh_tensor4* x,

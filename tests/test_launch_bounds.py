@@ -4,7 +4,8 @@ CPU only: the launch plans and index formulas of the kernels the harness's
 HIP legs run (csrc/syrk.hip: k_sy_scores work items, their x loads and
 partial-tile stores, k_sy_sv's partial, V and output accesses;
 csrc/decode.hip: k_decode_bf16's key, q and partial accesses; the training
-backward's k_dq_sy B loads on x and k_dv_sy) are restated here and evaluated over every
+backward's k_dq_sy B loads on x and k_dv_sy; csrc/model.hip: k_gated_gemm's
+LDS-DMA operand loads and epilogue x loads) are restated here and evaluated over every
 work item, with the strides of the views the harness passes (x_sparse as the
 permuted (B, T, nh, N) encoder output, the packed KV cache's
 capacity-strided past views).  Each access must fall inside its buffer and
@@ -258,3 +259,47 @@ def test_rope_backward_launches_stay_in_bounds(B, nh, T, N, D):
     p = sy_plan(B * nh, T, N)
     check_dv(B, nh, 1, T, N, D, p)
     check_dv(B, nh, nh, T, N, D, p)
+
+
+def check_gated(B, T, nh, N, K):
+    """csrc/model.hip k_gated_gemm on contiguous y (B, nh, T, K), wt (nh, N, K) and x (B, T, nh, N):
+    every tile's DMA chunks (instruction u of wave w, lane l: A row 16 (8u + w) + l / 4, u < 2, or
+    B row 16 w + l / 4, u = 2; chunk (l & 3) ^ ((l >> 4) & 3); stage s adds 32 s elements) and
+    epilogue x chunks (row (tid >> 4) + 32 e, columns n0 + 8 (tid & 15), clamped) stay inside their
+    views, the DMA byte offsets fit 32 bits, and the LDS bytes a stage fills stay inside the
+    3-slot ring of 24 KB slots."""
+    GM, GN, GK, STAGE, RING = 256, 128, 32, 24 * 1024, 3
+    M = B * T
+    y0, y2 = nh * T * K, K
+    nst = K // GK
+    nmb, nnb = (M + GM - 1) // GM, (N + GN - 1) // GN
+    y_head, w_head = B * nh * T * K - (nh - 1) * T * K, N * K  # elements reachable from a head's base
+    for mbi in {0, nmb - 1}:
+        for nbi in {0, nnb - 1}:
+            m0, n0 = mbi * GM, nbi * GN
+            for w in (0, 7):
+                for lane in (0, 3, 16, 63):
+                    dc = (lane & 3) ^ ((lane >> 4) & 3)
+                    for u in (0, 1):
+                        m = min(m0 + 16 * (8 * u + w) + lane // 4, M - 1)
+                        b, tt = divmod(m, T)
+                        off = b * y0 + tt * y2 + dc * 8
+                        last = off + 32 * (nst - 1) + 8
+                        assert last <= y_head and off * 2 < 2 ** 32 and (last - 8) * 2 < 2 ** 32
+                        assert ((nst - 1) % RING) * STAGE + (8 * u + w) * 1024 + lane * 16 + 16 <= RING * STAGE
+                    n = min(n0 + 16 * w + lane // 4, N - 1)
+                    off = n * K + dc * 8
+                    assert off + 32 * (nst - 1) + 8 <= w_head and (off + 32 * (nst - 1)) * 2 < 2 ** 32
+                    assert 2 * STAGE + 16 * 1024 + w * 1024 + lane * 16 + 16 <= RING * STAGE
+            for tid in (0, 15, 496, 511):
+                for e in range(8):
+                    m = min(m0 + (tid >> 4) + 32 * e, M - 1)
+                    b, tt = divmod(m, T)
+                    col = min(n0 + 8 * (tid & 15), N - 8)
+                    assert b * T * nh * N + tt * nh * N + (nh - 1) * N + col + 8 <= B * T * nh * N
+
+
+@pytest.mark.parametrize("B,T,nh,N,K", [(32, 512, 4, 8192, 256), (4, 2048, 8, 8192, 512), (2, 300, 2, 1000, 96),
+                                       (3, 257, 3, 136, 64), (1, 1, 1, 8, 32)])
+def test_gated_gemm_launches_stay_in_bounds(B, T, nh, N, K):
+    check_gated(B, T, nh, N, K)
