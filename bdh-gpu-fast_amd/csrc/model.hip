@@ -14,7 +14,6 @@
 #include "lds_dma.h"
 #include "tile_gemm.h"
 
-#pragma clang diagnostic ignored "-Winline-asm"
 
 namespace bdh {
 

@@ -41,7 +41,6 @@
 #include "fwd.h"
 #include "lds_dma.h"
 
-#pragma clang diagnostic ignored "-Winline-asm"
 
 namespace bdh {
 namespace {

@@ -75,6 +75,7 @@ C2 = dict(n_layer=6, D=256, nh=4, mult=128, B=32, T=512)
 C5 = dict(n_layer=8, D=512, nh=8, mult=128, B=4, T=2048)
 C3_GEN = dict(n_layer=6, D=256, nh=4, mult=128, B=64, prompt=256, new=256, top_k=3, seed=5)
 CALIB_BYTES = 1 << 29  # reference elementwise pass that scales the HBM byte counters
+MARK_ELEMS = 1 << 16  # the section marker multiply of --pmc-targets (a grid no other target has)
 
 
 def log(msg: str) -> None:
@@ -402,8 +403,9 @@ def main() -> int:
         "--pmc-targets",
         action="store_true",
         help="run only the profiled kernels a few times each (for rocprofv3 counter passes): the C1 fused "
-        "forward, the C4 training op, one C2 layer's gated GEMM, the C3 decode step at S=511, the C2 "
-        "training step's RoPE backward, and the calibration multiply",
+        "forward, the C4 training op, one C2 layer's gated GEMM, one C2 layer's RoPE attention backward "
+        "on both routes (recomputed tiles; kept tiles, as the training step runs it), the C3 decode step at "
+        "S=511, and the calibration multiply",
     )
     ap.add_argument(
         "--calibrate",
@@ -810,9 +812,20 @@ def run_pmc_targets(torch, ext, kernels, dev, reps: int = 3) -> None:
     """The kernels the committed counter tables cover, ``reps`` calls each on
     synthetic inputs of their configuration (rocprofv3 --pmc runs this with
     --kernel-include-regex to pick them), then one calibration multiply over
-    CALIB_BYTES (the reference point that scales FETCH_SIZE / WRITE_SIZE)."""
+    CALIB_BYTES (the reference point that scales FETCH_SIZE / WRITE_SIZE).
+    Each section ends with a small elementwise multiply (MARK_ELEMS floats), a
+    marker in the dispatch order: some kernels run in two sections with the
+    same grid (the C1 and C2 score passes, C4's and C2's S x V and dV), and a
+    counter table tells them apart by the markers before them."""
     bf = torch.bfloat16
     g = torch.Generator(device=dev).manual_seed(0)
+    mark = torch.ones(MARK_ELEMS, dtype=torch.float32, device=dev)
+
+    def section_end():
+        torch.cuda.synchronize()
+        torch.mul(mark, 1.0, out=mark)
+        torch.cuda.synchronize()
+
     # C1 fused forward (k_sy_scores, k_sy_sv)
     B, nh, T, N, D = (C1[k] for k in ("B", "nh", "T", "N", "D"))
     x = torch.relu(0.32 * torch.randn(B, nh, T, N, generator=g, device=dev)).to(bf)
@@ -821,6 +834,7 @@ def run_pmc_targets(torch, ext, kernels, dev, reps: int = 3) -> None:
     for _ in range(reps):
         kernels.bdh_attn_rope(x, v, f, 0, impl="hip")
     del x, v
+    section_end()
     # C4 training op (k_sy_scores, k_dv_sy, G, k_dq_sy)
     B4, n4, T4, N4, D4 = (C4[k] for k in ("B", "nh", "T", "N", "D"))
     q4 = torch.relu(0.32 * torch.randn(B4, n4, T4, N4, generator=g, device=dev)).to(bf)
@@ -830,6 +844,7 @@ def run_pmc_targets(torch, ext, kernels, dev, reps: int = 3) -> None:
         _, sc = ext.tril_score_v_save(q4, v4)
         ext.tril_score_v_bwd_saved(q4, v4, d4, sc)
     del q4, v4, d4, sc
+    section_end()
     # one C2 layer's gated product (k_gated_gemm): y (B, nh, T, D), encoder_v^T (nh, N, D), x (B, T, nh, N)
     c = C2
     N2 = c["mult"] * c["D"] // c["nh"]
@@ -839,14 +854,23 @@ def run_pmc_targets(torch, ext, kernels, dev, reps: int = 3) -> None:
     for _ in range(reps):
         kernels.gated_gemm(y, wt, xb)
     del y, wt, xb
-    # the C2 training step's attention backward (fused RoPE, bf16): one layer
-    x2 = torch.relu(0.32 * torch.randn(c["B"], c["nh"], c["T"], N2, generator=g, device=dev)).to(bf)
+    section_end()
+    # one C2 layer's fused RoPE attention backward, bf16, x_sparse as the
+    # model's permuted (B, T, nh, N) view: the route that recomputes the score
+    # tiles, then the training step's route (the forward keeps its tiles, the
+    # backward recomputes none)
+    x2 = torch.relu(0.32 * torch.randn(c["B"], c["T"], c["nh"], N2, generator=g, device=dev)).to(bf).permute(0, 2, 1, 3)
     v2 = torch.randn(c["B"], 1, c["T"], c["D"], generator=g, device=dev).to(bf)
     d2 = torch.randn(c["B"], c["nh"], c["T"], c["D"], generator=g, device=dev).to(bf)
     f2 = kernels.get_freqs(N2).to(dev)
     for _ in range(reps):
         ext.tril_rope_score_v_bwd(x2, v2, d2, f2, 0)
-    del x2, v2, d2
+    section_end()
+    for _ in range(reps):
+        _, sc2 = ext.tril_rope_score_v_save(x2, v2, f2, 0)
+        ext.tril_rope_score_v_bwd_saved(x2, v2, d2, f2, 0, sc2)
+    del x2, v2, d2, sc2
+    section_end()
     # C3 decode step at the longest past (k_decode_bf16)
     Bd, nhd, Nd, Dd = (C3[k] for k in ("B", "nh", "N", "D"))
     S = max(C3["S"])
