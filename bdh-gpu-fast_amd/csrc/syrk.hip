@@ -335,10 +335,17 @@ __device__ __forceinline__ int sy_piece_row(int l, int half, int qq, int e) {
 // makes those entries from the stage's frequencies in LDS (rel_entry).
 // GOUT (with Q = dO, K = V, one split): instead of partial tiles, write the
 // backward's G = dS + dS^T, dS = tril(dO V^T, -1), into a.g.
-template <int RM, bool SELF, bool GOUT = false>
+// PAIR (relative RoPE): even stages issue the chunks of stages s + 2 and s + 3
+// back to back, odd stages none, so the two 64-byte halves of each 128-byte
+// line of a row are requested together.  For rows whose stride is a multiple
+// of 64 KB (the model's (B, T, nh, N) x_sparse): their pieces share few L2
+// sets, and a line fetched for one stage is gone before the next stage reads
+// its other half.
+template <int RM, bool SELF, bool GOUT = false, bool PAIR = false>
 __global__ __launch_bounds__(kSyThreads, 1) void k_sy_scores(const SyArgs a) {
   constexpr bool ROPE = RM != 0;
   constexpr bool REL = RM == 2;
+  static_assert(!PAIR || REL, "paired stages: relative RoPE");
   static_assert(!GOUT || (!SELF && !ROPE), "G epilogue: distinct operands, no RoPE");
   static_assert(!REL || SELF, "relative RoPE: self attention");
   const int bid = blockIdx.x;
@@ -565,7 +572,16 @@ __global__ __launch_bounds__(kSyThreads, 1) void k_sy_scores(const SyArgs a) {
         rot_store(st, wt_tag, uc, x, t);
       });
     };
-    if constexpr (REL) {
+    if constexpr (PAIR) {
+      const StageDma d0 = stage_dma(0), d1 = stage_dma(1);
+      sy_static_for<4>([&](auto uc) {
+        dma_x(d0, uc);
+        dma_x(d1, uc);
+      });
+      sy_wait<0>();  // stages 0 and 1 landed
+      rotate_all(0);
+      sy_barrier();
+    } else if constexpr (REL) {
       for (int st = 0; st < lead - 1; ++st) {
         const StageDma d = stage_dma(st);
         sy_static_for<4>([&](auto uc) { dma_x(d, uc); });
@@ -631,9 +647,22 @@ __global__ __launch_bounds__(kSyThreads, 1) void k_sy_scores(const SyArgs a) {
     for (int s = 0; s + 1 < nst; ++s) {
       read_frags(f1, s, 1);
       __builtin_amdgcn_sched_barrier(0);
-      const StageDma d = stage_dma(s + lead);
+      const StageDma d = stage_dma(PAIR ? s + 2 : s + lead);
+      // PAIR: stage s + 3 goes to the slot of stage s - 1, whose last reads
+      // came before the previous barrier
+      const StageDma d2 = stage_dma(s + 3);
+      const bool issue = !PAIR || (s & 1) == 0;
       if constexpr (ROPE) {
-        sy_wait<NWAITR>();
+        if constexpr (PAIR) {
+          // stage s+1 landed: even s, nothing issued after it (odd stages
+          // issue none); odd s, chunk 3 of stage s+2 after it
+          if (s & 1)
+            sy_wait<1>();
+          else
+            sy_wait<0>();
+        } else {
+          sy_wait<NWAITR>();
+        }
         u32x4 x[4], t[NTD];
         sy_static_for<4>([&](auto uc) {
           x[decltype(uc)::value] = *reinterpret_cast<const u32x4*>(slot(s + 1) + vrot + decltype(uc)::value * 8192);
@@ -648,8 +677,18 @@ __global__ __launch_bounds__(kSyThreads, 1) void k_sy_scores(const SyArgs a) {
         sy_static_for<NM>([&](auto mc) {
           constexpr int m = decltype(mc)::value;
           mfma_m(f0, mc);
-          if constexpr (m == 0) dma_x(d, I0());
-          if constexpr (m == 2) dma_x(d, I1());
+          if constexpr (m == 0) {
+            if (issue) {
+              dma_x(d, I0());
+              if constexpr (PAIR) dma_x(d2, I0());
+            }
+          }
+          if constexpr (m == 2) {
+            if (issue) {
+              dma_x(d, I1());
+              if constexpr (PAIR) dma_x(d2, I1());
+            }
+          }
           if constexpr (m < 8) {
             constexpr int u = m >> 1, hh = m & 1;
             constexpr bool conj = sy_rot_conj<REL>(WT, u);
@@ -693,8 +732,18 @@ __global__ __launch_bounds__(kSyThreads, 1) void k_sy_scores(const SyArgs a) {
       sy_static_for<NM>([&](auto mc) {
         constexpr int m = decltype(mc)::value;
         mfma_m(f1, mc);
-        if constexpr (m == 1) dma_x(d, I2());
-        if constexpr (m == 3) dma_x(d, I3());
+        if constexpr (m == 1) {
+          if (issue) {
+            dma_x(d, I2());
+            if constexpr (PAIR) dma_x(d2, I2());
+          }
+        }
+        if constexpr (m == 3) {
+          if (issue) {
+            dma_x(d, I3());
+            if constexpr (PAIR) dma_x(d2, I3());
+          }
+        }
       });
     }
     // last stage: nothing left to load or rotate
@@ -1655,7 +1704,12 @@ int sy_run(const bdh_tensor4* q, const bdh_tensor4* k, const bdh_tensor4* v, con
   a.per_split = p.per_split;
   a.nfull = p.nfull;
   const dim3 gs{unsigned(grid_scores)};
-  if (rel)
+  // row strides of a multiple of 64 KB: paired stages (both halves of each
+  // 128-byte line requested together)
+  const bool pair = rel && (q->stride[2] * 2) % 65536 == 0;
+  if (pair)
+    BDH_LAUNCH("k_sy_scores", (k_sy_scores<2, true, false, true>), gs, dim3(kSyThreads), 0, s, a);
+  else if (rel)
     BDH_LAUNCH("k_sy_scores", (k_sy_scores<2, true>), gs, dim3(kSyThreads), 0, s, a);
   else if (rope)
     BDH_LAUNCH("k_sy_scores", (k_sy_scores<1, true>), gs, dim3(kSyThreads), 0, s, a);

@@ -268,3 +268,30 @@ def test_score_v_matches_oracle_and_is_reproducible(shape):
         print(f"  rope={rope}: rel {err:.3e}", flush=True)
         assert err <= TOL[BF]
         assert not first[:, :, 0].any().item()
+
+
+@pytest.mark.parametrize("B,H,T,N", [(2, 4, 512, 8192), (1, 2, 300, 16384), (3, 2, 700, 16384)])
+def test_bf16_fused_rope_paired_stages_on_64k_rows(B, H, T, N):
+    """Token rows a multiple of 64 KB apart (the model's (B, T, nh, N) x_sparse with nh*N a
+    multiple of 32768) take the paired-stage score pass (both 64-byte halves of each 128-byte
+    line requested together).  It loads the same rows and k chunks in another order, so the
+    output, and the gradients the backward takes from the kept score tiles, equal those of the
+    same x stored contiguously (the unpaired pass) bit for bit; ragged T included."""
+    print(f"paired stages B={B} H={H} T={T} N={N}", flush=True)
+    g = torch.Generator(device=DEV).manual_seed(T + N)
+    xt = torch.relu(0.3 * torch.randn(B, T, H, N, generator=g, device=DEV)).to(BF)
+    assert (H * N * 2) % 65536 == 0
+    x_perm = xt.permute(0, 2, 1, 3)
+    x_cont = x_perm.contiguous()
+    assert (N * 2) % 65536 != 0  # the contiguous copy takes the unpaired pass
+    v = torch.randn(B, 1, T, 256, generator=g, device=DEV).to(BF)
+    freqs = torch.from_numpy(O.get_freqs(N)).to(DEV)
+    out_p, ws_p = ext.tril_rope_score_v_save(x_perm, v, freqs, 0)
+    out_c, ws_c = ext.tril_rope_score_v_save(x_cont, v, freqs, 0)
+    assert ws_p is not None and ws_c is not None
+    assert torch.equal(out_p, out_c)
+    d = torch.randn(B, H, T, 256, generator=g, device=DEV).to(BF)
+    dx_p, dv_p = ext.tril_rope_score_v_bwd_saved(x_perm, v, d, freqs, 0, ws_p)
+    dx_c, dv_c = ext.tril_rope_score_v_bwd_saved(x_cont, v, d, freqs, 0, ws_c)
+    assert torch.equal(dv_p, dv_c)
+    assert torch.equal(dx_p, dx_c)
