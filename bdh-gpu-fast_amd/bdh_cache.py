@@ -118,9 +118,15 @@ class CacheManager:
 
     @property
     def hands_storage_views(self) -> bool:
-        """Whether ``get_past`` / ``stage`` return storage-dtype views (no cast copy)."""
+        """Whether ``get_past`` / ``stage`` return storage-dtype views (no cast copy).
+
+        Only bf16 and fp32 storage is handed out uncast: those are the key and value
+        dtypes the HIP decode reads.  Any other storage dtype (the reference documents
+        float16, bdh.py:1096) keeps the reference's cast to the compute dtype."""
         if self.storage_matches_compute:
             return True
+        if self.storage_dtype not in (torch.bfloat16, torch.float32):
+            return False
         if self.decode_views is not None:
             return bool(self.decode_views)
         if self.device.type != "cuda" or torch.version.hip is None:

@@ -632,9 +632,18 @@ extern "C" size_t bdh_tril_rope_score_v_bwd_workspace(int64_t B, int64_t H, int6
 extern "C" int bdh_tril_rope_score_v_keeps_scores(const bdh_tensor4* x, const bdh_tensor4* v, size_t* scores_bytes) {
   size_t off = 0, kept = 0;
   int rel = 0;
+  // the limits rope_saved_bwd applies to what the forward already knows (G's
+  // padded T x T tile and V's row span), so tiles are kept only when the
+  // saved backward will take them; dO is passed with contiguous rows
+  int64_t tpad = 0;
+  const int64_t T = x->size[2], D = v->size[3];
+  rope_saved_bwd_bytes(x->size[0], x->size[1], T, x->size[3], nullptr, &tpad);
+  const bool fits = tpad % 32 == 0 && tpad * tpad * 2 < (int64_t(1) << 31) &&
+                    ((T - 1) * std::max(v->stride[2], D) + D) * 2 < (int64_t(1) << 31);
   const bool keep = check_view(x) == BDH_OK && check_view(v) == BDH_OK && v->size[0] == x->size[0] &&
                     v->size[2] == x->size[2] && (v->size[1] == 1 || v->size[1] == x->size[1]) &&
-                    x->size[3] % 256 == 0 && v->size[3] % 64 == 0 && sy_rope_keeps_scores(x, v, &off, &kept, &rel);
+                    x->size[3] % 256 == 0 && v->size[3] % 64 == 0 && fits &&
+                    sy_rope_keeps_scores(x, v, &off, &kept, &rel);
   if (scores_bytes) *scores_bytes = keep ? kept : 0;
   return keep ? 1 : 0;
 }

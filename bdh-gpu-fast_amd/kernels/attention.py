@@ -61,6 +61,57 @@ def eager_decode_attn(Q: torch.Tensor, K: torch.Tensor, V: torch.Tensor) -> torc
     return _two_gemm_decode(Q, K, V)
 
 
+# The reference's Triton backend is not part of this package (the gfx950 path
+# is hand-written HIP).  Its probes keep their names and answer "unavailable",
+# so callers that ask before choosing a backend take another one.
+
+def pick_cold_block_size(T: int, block_size: int | None = None) -> int:
+    """Cold query-tile width (kernels/attention.py:542-553): 64, or 128 from T = 256."""
+    if block_size is not None:
+        return max(1, int(block_size))
+    return min(128, 2 * DEFAULT_BLOCK_COLD) if int(T) >= 256 else DEFAULT_BLOCK_COLD
+
+
+def pick_triton_cold_tiles(
+    T: int,
+    N: int = 64,
+    D: int = 128,
+    *,
+    block_m: int | None = None,
+    block_n: int | None = None,
+) -> tuple[int, int, int, int]:
+    """``(BLOCK_M, BLOCK_N, BLOCK_D, BLOCK_K)`` of the reference's cold Triton tiles
+    (kernels/attention.py:98-164): query/key widths from :func:`pick_cold_block_size`,
+    at most 64 for wide heads (N > 64 or D > 128), and D / N widths, each rounded up
+    to a power of two within [16, 128] (D and N within [16, 64])."""
+
+    def ceil_pow2(x: int, lo: int, hi: int) -> int:
+        x = max(lo, min(int(x), hi))
+        p = 1
+        while p < x:
+            p *= 2
+        return min(p, hi)
+
+    wide = N > 64 or D > 128
+    want = pick_cold_block_size(T)
+    if wide:
+        want = min(want, DEFAULT_BLOCK_COLD)
+    bm = ceil_pow2(block_m, 16, 128) if block_m is not None else ceil_pow2(min(T, want) if T > 0 else want, 16, 128)
+    bn = ceil_pow2(block_n, 16, 128) if block_n is not None else ceil_pow2(min(max(T, 1), want), 16, 128)
+    return bm, bn, ceil_pow2(D if D > 0 else 1, 16, 64), ceil_pow2(N if N > 0 else 1, 16, 64)
+
+
+def triton_decode_available() -> bool:
+    """Always False: this package ships no Triton decode (kernels/attention.py:800-807)."""
+    return False
+
+
+def triton_cold_skip_reason() -> str | None:
+    """Why the Triton cold kernel is not used (kernels/attention.py:810-827): it is not
+    part of this package; ``BDH_ATTN_IMPL=hip`` runs the gfx950 kernels."""
+    return "Triton backend not built into this package; BDH_ATTN_IMPL=hip selects the gfx950 kernels (CPU-safe skip)"
+
+
 __all__ = [
     "DEFAULT_BLOCK_COLD",
     "DEFAULT_BLOCK_DECODE",
@@ -68,4 +119,8 @@ __all__ = [
     "eager_decode_attn",
     "eager_past_attn",
     "_two_gemm_decode",
+    "pick_cold_block_size",
+    "pick_triton_cold_tiles",
+    "triton_decode_available",
+    "triton_cold_skip_reason",
 ]

@@ -176,8 +176,10 @@ class TrilRopeSelfAttnFn(torch.autograd.Function):
         Vc = V.to(x.dtype) if x.dtype == torch.bfloat16 else V
         dV = torch.empty_like(V, memory_format=torch.contiguous_format)
         if ctx.has_scores:
-            dx, dV = hip_attn.tril_rope_score_v_bwd_saved(x, Vc, dO.to(x.dtype), freqs, ctx.rope_start, scores,
-                                                          dv=dV)
+            # contiguous dO rows keep its span inside the limits the forward
+            # checked before keeping the tiles
+            dx, dV = hip_attn.tril_rope_score_v_bwd_saved(x, Vc, dO.to(x.dtype).contiguous(), freqs,
+                                                          ctx.rope_start, scores, dv=dV)
         else:
             dx, dV = hip_attn.tril_rope_score_v_bwd(x, Vc, dO.to(x.dtype), freqs, ctx.rope_start, dv=dV)
         return dx, dV, None, None, None

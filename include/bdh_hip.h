@@ -128,9 +128,13 @@ int bdh_tril_decode(const bdh_tensor4* q, const bdh_tensor4* k_past,
  * harnesses that forbid allocation).  Same operands, kernels and results as
  * bdh_tril_decode.  The partial sums go to a library-owned device array of
  * BDH_NOALLOC_SCRATCH_BYTES per GPU (each GPU the library runs on holds one
- * until the process ends); inputs whose partials exceed it (B*H*Tq * Dv * 4
- * bytes per 64 past keys on the bf16 path, per 32 otherwise; C3's B*H = 256,
- * Dv = 256 fits S <= 4096) return BDH_ERR_SCRATCH.  The current device must be
+ * until the process ends); inputs whose partials exceed it return
+ * BDH_ERR_SCRATCH.  The partials take B*H*Tq * Dv * 4 bytes per chunk of past
+ * keys: 64-key chunks on both streaming kernels (q and key rows 16-byte
+ * aligned, and Dk a multiple of 2048 for bf16 q over bf16 keys, or of 256 /
+ * 512 for fp32 / bf16 keys under the fp32-arithmetic kernel), 32-key chunks on
+ * the generic kernel (any other operands).  C3's B*H = 256, Dv = 256 fits
+ * S <= 4096 on the streaming kernels.  The current device must be
  * the tensors' device.  Every call on one GPU shares that GPU's array: calls
  * that overlap in time on one GPU (other streams, other threads) race and must
  * be serialised by the caller.

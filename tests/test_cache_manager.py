@@ -156,6 +156,19 @@ def test_storage_views_policy(monkeypatch):
         monkeypatch.setenv("BDH_ATTN_IMPL", env)
         assert AD.resolve_attn_impl() == env
         assert dev.hands_storage_views is want
+    # float16 storage (documented by the reference, bdh.py:1096): the HIP decode
+    # reads only bf16/fp32 rows, so the past is cast to the compute dtype even
+    # with the hip impl forced or views asked for.
+    monkeypatch.setenv("BDH_ATTN_IMPL", "hip")
+    for views in (None, True):
+        half = CacheManager.from_config(CFG, 1, 8, "cpu", compute_dtype=torch.float32,
+                                        storage_dtype=torch.float16, decode_views=views)
+        half.device = torch.device("cuda")
+        assert half.hands_storage_views is False
+        half.device = torch.device("cpu")
+        assert past_dtype(half) == torch.float32
+        st, _ = half.stage(0, torch.ones(1, 2, 1, N), torch.ones(1, 1, 1, 16))
+        assert st.dtype == torch.float32
 
 
 def _model(seed=3):

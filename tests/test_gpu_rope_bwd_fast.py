@@ -198,3 +198,30 @@ def test_rope_autograd_saved_tiles_switch(monkeypatch):
         grads[save] = (xd.grad.clone(), vd.grad.clone())
     assert torch.equal(grads["1"][0], grads["0"][0])
     assert rel_fro(np_of(grads["1"][1]), np_of(grads["0"][1])) <= TOL
+
+
+def test_rope_backward_from_saved_tiles_absolute_layout():
+    """More than 512 k stages per workgroup (N = 16640, one split because 129 slabs
+    of one 256-row tile fill the chip) keeps the forward's tiles in the absolute
+    layout, with the (cos, sin) table ahead of them.  dx equals the recompute
+    route's bit for bit; batch element 0 matches the oracle at 2e-2."""
+    B, H, T, N, D, start = 43, 3, 256, 16640, 64, 9
+    print(f"rope bwd saved tiles, absolute layout {(B, H, T, N, D)}", flush=True)
+    g = torch.Generator(device=DEV).manual_seed(21)
+    xd = torch.relu(0.32 * torch.randn(B, H, T, N, generator=g, device=DEV)).to(BF)
+    vd = torch.randn(B, 1, T, D, generator=g, device=DEV).to(BF)
+    dd = torch.randn(B, H, T, D, generator=g, device=DEV).to(BF)
+    fd = kernels.get_freqs(N).to(DEV)
+    assert ext.rope_keeps_scores(xd, vd)
+    out, scores = ext.tril_rope_score_v_save(xd, vd, fd, start)
+    assert scores is not None
+    assert torch.equal(out, ext.tril_rope_score_v(xd, vd, fd, start))
+    (sx, sv), names = _names(lambda: ext.tril_rope_score_v_bwd_saved(xd, vd, dd, fd, start, scores))
+    assert "k_dq_sy" in names and "k_dv_sy" in names, names
+    rx, rv = ext.tril_rope_score_v_bwd(xd, vd, dd, fd, start)
+    assert torch.equal(sx, rx)
+    assert rel_fro(np_of(sv), np_of(rv)) <= TOL
+    wx, wv = O.tril_rope_score_v_backward(np_of(xd[:1]), np_of(vd[:1]), np_of(dd[:1]), np_of(fd), start)
+    ex, ev = rel_fro(np_of(sx[:1]), wx), rel_fro(np_of(sv[:1]), wv)
+    print(f"  dx rel {ex:.3e}, dv rel {ev:.3e}", flush=True)
+    assert ex <= TOL and ev <= TOL
