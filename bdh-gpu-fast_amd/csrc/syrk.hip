@@ -1708,7 +1708,7 @@ int sy_run(const bdh_tensor4* q, const bdh_tensor4* k, const bdh_tensor4* v, con
   // 128-byte line requested together)
   const bool pair = rel && (q->stride[2] * 2) % 65536 == 0;
   if (pair)
-    BDH_LAUNCH("k_sy_scores", (k_sy_scores<2, true, false, true>), gs, dim3(kSyThreads), 0, s, a);
+    BDH_LAUNCH("k_sy_scores_paired", (k_sy_scores<2, true, false, true>), gs, dim3(kSyThreads), 0, s, a);
   else if (rel)
     BDH_LAUNCH("k_sy_scores", (k_sy_scores<2, true>), gs, dim3(kSyThreads), 0, s, a);
   else if (rope)

@@ -11,6 +11,11 @@
   bf16 attention's effect on the gradients (against the same AMP step with
   fp32 attention) no larger than that of the reference's eager bf16
   attention measured the same way;
+* the training step's loss and gradients against the float64 model oracle;
+* the C3 decode route at its model configuration (L=6, D=256, nh=4, N=8192,
+  B=64, bf16 cache) through both caches: teacher-forced step logits against
+  the model oracle at S = 256..263 and 504..511, and ``generate``'s draws
+  against the oracle-anchored logits they were drawn from;
 * ``generate`` end to end;
 * the row LayerNorm (LN(y), LN(x + LN(y))) against F.layer_norm.
 """
@@ -80,6 +85,28 @@ def test_forward_full_c2_config_matches_oracle():
     with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
         got, _ = m(torch.from_numpy(idx).to(DEV), impl="hip")
     assert rel_fro(got.float().cpu().numpy(), M.bdh_forward(p, idx)) <= 2e-2
+
+
+def test_forward_c2_batch_paired_plan_matches_oracle():
+    """The C2 configuration at its own batch (B=32, T=512, 6 layers): 128 slabs
+    of two items each fill the chip at one split, and the model's (B, T, nh, N)
+    x_sparse rows are 64 KB apart, so the score pass runs the paired-stage
+    kernel at split 1 (checked in the launch log).  Sequences 0 and 31 against
+    the numpy model oracle within 2e-2."""
+    print("harness C2 batch forward (paired split-1 plan)", flush=True)
+    p = M.init_params(6, 256, 4, 8192, 256, seed=33)
+    m = _model(p, mult=128)
+    idx = np.random.default_rng(34).integers(0, 256, (32, 512))
+    ext.profile_enable(True)
+    try:
+        with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+            got, _ = m(torch.from_numpy(idx).to(DEV), impl="hip")
+        torch.cuda.synchronize()
+        names = {n for n, _ in ext.profile_collect()}
+    finally:
+        ext.profile_enable(False)
+    assert "k_sy_scores_paired" in names, names
+    assert rel_fro(got[[0, 31]].float().cpu().numpy(), M.bdh_forward(p, idx[[0, 31]])) <= 2e-2
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
@@ -171,6 +198,151 @@ def test_train_step_gradients(amp):
         e_hip, e_eag = rel_fro(hip[n], hip32[n]), rel_fro(eag[n], eag32[n])
         print(f"  {n}: bf16 vs fp32 attention: hip {e_hip:.3e} eager {e_eag:.3e}", flush=True)
         assert e_hip <= max(2e-2, 1.5 * e_eag), n
+
+
+@pytest.mark.parametrize("amp", [False, True])
+def test_train_step_gradients_match_oracle(amp):
+    """The training step's loss and parameter gradients (HIP attention forward
+    and backward) against the float64 oracle's (``bdh_loss_grads``, autograd of
+    bdh_baseline.py:109-151 with the mean cross entropy of train.py:997-1034).
+
+    fp32: every gradient within 1e-4.  AMP: the bf16 products of the model
+    itself (encoder, encoder_v, decoder, lm_head and their backward under
+    autocast, as in the reference) move the gradients by 3-6e-2 from the
+    float64 values whatever the attention does (measured on the CPU with
+    reference-semantics eager attention, in bf16 and in fp32).  So each
+    gradient's error against the oracle must stay within max(2e-2, 1.25x) the
+    error of the reference-semantics AMP step (eager attention, on the CPU)
+    against the same oracle, and the loss within 2e-2.
+
+    The fp32 comparison is well posed only when no ReLU input sits within fp32
+    rounding of zero: such an element takes either branch depending on the
+    GEMM's summation order, and its one gradient then moves every gradient
+    upstream by ~1e-3 (measured: one of 2e5 inputs flipped between the GPU and
+    the CPU product on another token draw).  The tokens are drawn so the
+    smallest ReLU input is 1.7e-5 of its tensor's RMS, ~30x the products'
+    rounding, and the test checks that first."""
+    print(f"harness train step vs oracle amp={amp}", flush=True)
+    p = M.init_params(2, 64, 2, 256, 256, seed=17)
+    idx_np = np.random.default_rng(47).integers(0, 256, (1, 128))
+    tgt_np = np.random.default_rng(48).integers(0, 256, (1, 128))
+    assert M.relu_margin(p, idx_np) >= 1e-5
+    idx, tgt = torch.from_numpy(idx_np), torch.from_numpy(tgt_np)
+    want_loss, want = M.bdh_loss_grads(p, idx_np, tgt_np)
+    hip = _grads(p, idx, tgt, "hip", amp)
+    names = {"embed.weight": "embed", "encoder": "encoder", "encoder_v": "encoder_v", "decoder": "decoder",
+             "lm_head": "lm_head"}
+    if not amp:
+        assert abs(hip["loss"][0] - want_loss) <= 1e-5 * abs(want_loss)
+        for n, k in names.items():
+            e = rel_fro(hip[n], want[k])
+            print(f"  {k}: fp32 step vs oracle {e:.3e}", flush=True)
+            assert e <= 1e-4, k
+        return
+    eag = _grads(p, idx, tgt, "eager", True, device="cpu")
+    assert abs(hip["loss"][0] - want_loss) <= 2e-2 * abs(want_loss)
+    for n, k in names.items():
+        e_hip, e_eag = rel_fro(hip[n], want[k]), rel_fro(eag[n], want[k])
+        print(f"  {k}: AMP step vs oracle: hip {e_hip:.3e}, reference-semantics eager {e_eag:.3e}", flush=True)
+        assert e_hip <= max(2e-2, 1.25 * e_eag), k
+
+
+# The C3 model (L=6, D=256, nh=4, N=8192, byte vocab) and batch (B=64).
+C3_BATCH = 64
+
+
+def _c3_params():
+    return M.init_params(6, 256, 4, 8192, 256, seed=41)
+
+
+def _c3_cache(m, kind, cap):
+    if kind == "kv":
+        return H.KVCache(m.config, C3_BATCH, cap, torch.bfloat16, DEV)
+    return H.CacheManager.from_config(m.config, batch_size=C3_BATCH, max_seq=cap, device=DEV,
+                                      compute_dtype=torch.float32, storage_dtype=torch.bfloat16,
+                                      decode_views=True)
+
+
+def _teacher_forced(m, tokens, prompt, steps, cache):
+    """generate's loop (bdh.py:1074-1193) with the next tokens given instead of
+    sampled: the prompt prefill into the cache, then one cached step per token,
+    under bf16 autocast.  Returns (B, steps + 1, V) fp32 logits: those after the
+    prompt, then those after each forced token."""
+    out = []
+    with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+        lg, _ = m(tokens[:, :prompt], cache=cache, impl="hip", last_only=True)
+        out.append(lg[:, -1].float())
+        for t in range(prompt, prompt + steps):
+            lg, _ = m(tokens[:, t:t + 1], cache=cache, impl="hip", last_only=True)
+            out.append(lg[:, -1].float())
+    return torch.stack(out, 1)
+
+
+_ORACLE_LOGITS: dict = {}
+
+
+def _oracle_logits(p, tokens_np, key):
+    if key not in _ORACLE_LOGITS:
+        _ORACLE_LOGITS[key] = M.bdh_forward(p, tokens_np)
+    return _ORACLE_LOGITS[key]
+
+
+@pytest.mark.parametrize("kind", ["kv", "manager"])
+@pytest.mark.parametrize("prompt", [256, 504])
+def test_decode_teacher_forced_c3_matches_oracle(kind, prompt):
+    """The C3 decode route at its model configuration and batch: a prompt
+    prefill (fused kernel writing RoPE(x) into the bf16 cache), then 8 cached
+    one-token steps over capacity-strided bf16 past views, through the
+    harness's packed cache (``kv``) and through ``CacheManager`` as bdh.py's
+    generate builds it (fp32 compute, bf16 storage handed out uncast).  Each
+    step's logits for sequences 0 and 1 of 64 against one oracle forward over
+    the same tokens, within 2e-2.  Prompt 256 covers S = 256..263 (C3's first
+    steps); prompt 504 covers S = 504..511 (C3's last)."""
+    steps = 8
+    print(f"C3 teacher-forced decode, {kind} cache, prompt {prompt}", flush=True)
+    p = _c3_params()
+    m = _model(p, mult=128)
+    tokens_np = np.random.default_rng(42).integers(0, 256, (C3_BATCH, prompt + steps))
+    tokens = torch.from_numpy(tokens_np).to(DEV)
+    cache = _c3_cache(m, kind, prompt + steps)
+    got = _teacher_forced(m, tokens, prompt, steps, cache).cpu().numpy()
+    want = _oracle_logits(p, tokens_np[:2], ("tf", prompt))[:, prompt - 1:]
+    for j in range(steps + 1):
+        e = rel_fro(got[:2, j], want[:, j])
+        print(f"  position {prompt - 1 + j}: logits rel {e:.3e}", flush=True)
+        assert e <= 2e-2, j
+    del cache
+    torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("kind", ["kv", "manager"])
+def test_generate_c3_samples_from_oracle_anchored_logits(kind):
+    """``generate`` at the C3 configuration (B=64, 256-token prompt, top_k=3,
+    temperature 1, seeded sampler), 8 new tokens.  Replaying the generated
+    stream through the same cached route gives the logits generate sampled
+    from (the kernels are deterministic): every new token is among their top 3,
+    and for sequences 0 and 1 they match one oracle forward over the generated
+    stream within 2e-2."""
+    prompt, steps = 256, 8
+    print(f"C3 generate, {kind} cache", flush=True)
+    p = _c3_params()
+    m = _model(p, mult=128)
+    idx = torch.from_numpy(np.random.default_rng(43).integers(0, 256, (C3_BATCH, prompt))).to(DEV)
+    out = m.generate(idx, steps, temperature=1.0, top_k=3, amp_dtype=torch.bfloat16, cache_dtype=torch.bfloat16,
+                     impl="hip", generator=torch.Generator(device=DEV).manual_seed(5),
+                     cache_manager=kind == "manager")
+    assert out.shape == (C3_BATCH, prompt + steps) and torch.equal(out[:, :prompt], idx)
+    cache = _c3_cache(m, kind, prompt + steps)
+    logits = _teacher_forced(m, out, prompt, steps - 1, cache)  # (B, steps, V): the logits of each draw
+    top3 = torch.topk(logits, 3, dim=-1).indices
+    drawn = out[:, prompt:]
+    assert bool((top3 == drawn.unsqueeze(-1)).any(-1).all()), "a generated token is outside the top 3"
+    want = M.bdh_forward(p, out[:2].cpu().numpy())[:, prompt - 1:prompt - 1 + steps]
+    e = rel_fro(logits[:2].cpu().numpy(), want)
+    print(f"  generated-stream logits vs oracle: rel {e:.3e}", flush=True)
+    assert e <= 2e-2
+    del cache
+    torch.cuda.empty_cache()
 
 
 def test_generate_end_to_end_bf16():

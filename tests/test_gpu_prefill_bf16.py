@@ -148,7 +148,7 @@ def _ran_score_tiles(fn):
     finally:
         ext.profile_enable(False)
     # the score-tile kernel, alone or with score x V fused into its tail
-    assert names & {"k_sy_scores", "k_sy_scores_sv"}, names
+    assert names & {"k_sy_scores", "k_sy_scores_paired", "k_sy_scores_sv"}, names
     return out
 
 
@@ -226,7 +226,7 @@ def test_bf16_fused_rope_stage_limit(N, table):
         names = {n for n, _ in ext.profile_collect()}
     finally:
         ext.profile_enable(False)
-    assert names & {"k_sy_scores", "k_sy_scores_sv"} and ("k_rope_table" in names) == table, names
+    assert names & {"k_sy_scores", "k_sy_scores_paired", "k_sy_scores_sv"} and ("k_rope_table" in names) == table, names
     assert rel_fro(got, want) <= TOL[BF]
     assert not got[:, :, 0].any()
 

@@ -106,3 +106,56 @@ def test_sampler_and_generate_on_cpu():
     assert torch.equal(out, again)
     with pytest.raises(ValueError):
         H.KVCache(m.config, 1, 2, torch.float32, "cpu").slot(0, 3)
+
+
+def test_loss_grads_oracle_pinned_by_forward_and_finite_differences():
+    """``bdh_loss_grads`` (float64 autograd of the model formula): its logits
+    equal the numpy oracle's, and every parameter's gradient matches central
+    finite differences of its own loss on sampled entries."""
+    p = M.init_params(2, 4, 2, 8, 7, seed=23)
+    for k in ("encoder", "encoder_v", "decoder"):
+        p[k] = p[k] * 25.0  # O(1) activations so every term matters
+    rng = np.random.default_rng(24)
+    idx, tgt = rng.integers(0, 7, (2, 6)), rng.integers(0, 7, (2, 6))
+    loss, g, logits = M.bdh_loss_grads(p, idx, tgt, return_logits=True)
+    assert rel_fro(logits, M.bdh_forward(p, idx)) <= 1e-5
+    h = 1e-6
+    for name in M.PARAM_NAMES:
+        assert g[name].shape == p[name].shape
+        for flat in rng.choice(p[name].size, 4, replace=False):
+            up = {k: (np.array(v, np.float64) if k in M.PARAM_NAMES else v) for k, v in p.items()}
+            dn = {k: (np.array(v, np.float64) if k in M.PARAM_NAMES else v) for k, v in p.items()}
+            up[name].flat[flat] += h
+            dn[name].flat[flat] -= h
+            fd = (M.bdh_loss_grads(up, idx, tgt)[0] - M.bdh_loss_grads(dn, idx, tgt)[0]) / (2 * h)
+            assert abs(fd - g[name].flat[flat]) <= 1e-6 + 1e-4 * abs(fd), (name, flat, fd, g[name].flat[flat])
+
+
+def test_harness_eager_train_step_matches_oracle_gradients():
+    """The harness's training step (eager attention, fp32 on the CPU): loss and
+    every parameter gradient against the float64 oracle at 1e-4."""
+    p = M.init_params(2, 32, 2, 64, 11, seed=25)
+    m = _model(p, mult=4)
+    rng = np.random.default_rng(26)
+    idx, tgt = rng.integers(0, 11, (2, 40)), rng.integers(0, 11, (2, 40))
+    _, loss = m(torch.from_numpy(idx), torch.from_numpy(tgt), impl="eager")
+    loss.backward()
+    want_loss, want = M.bdh_loss_grads(p, idx, tgt)
+    assert abs(loss.item() - want_loss) <= 1e-5 * abs(want_loss)
+    got = {"embed": m.embed.weight.grad, **{k: getattr(m, k).grad for k in M.PARAM_NAMES if k != "embed"}}
+    for k in M.PARAM_NAMES:
+        assert rel_fro(got[k].numpy(), want[k]) <= 1e-4, k
+
+
+def test_relu_margin_detects_inputs_near_zero():
+    """``relu_margin`` is the smallest |ReLU input| / RMS of the forward: zero when
+    an encoder product is exactly 0 (an embedding row orthogonal to an encoder
+    column), positive otherwise, and equal for a prefix of a longer draw (causal)."""
+    p = M.init_params(1, 8, 2, 8, 5, seed=27)
+    idx = np.array([[1, 3, 2, 4]])
+    m = M.relu_margin(p, idx)
+    assert 0 < m < 1
+    assert M.relu_margin(p, np.array([[1, 3, 2, 4, 0, 1]])) <= m
+    q = dict(p, encoder=p["encoder"].copy())
+    q["encoder"][0, :, 3] = 0.0  # one latent column of head 0 is identically zero
+    assert M.relu_margin(q, idx) == 0.0
