@@ -26,8 +26,14 @@ __device__ __forceinline__ bf16_t f2bf(float x) {
   return __builtin_bit_cast(bf16_t, b);
 }
 __device__ __forceinline__ float bf_round(float x) { return to_f(f2bf(x)); }
+// Two floats to a bf16 pair (lo in bits 0-15), both rounded to nearest even:
+// one v_cvt_pk_bf16_f32 (the scalar conversions above, packed by shifts and
+// an or, took four instructions).
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint32_t pack_bf2(float lo, float hi) {
-  return uint32_t(f2bf(lo)) | (uint32_t(f2bf(hi)) << 16);
+  const bf16x2_t b = __builtin_convertvector((f32x2_t{lo, hi}), bf16x2_t);
+  return __builtin_bit_cast(uint32_t, b);
 }
 
 template <typename T> __device__ __forceinline__ T from_f(float x);

@@ -35,6 +35,8 @@
 // to its fp32 sums in the epilogue) and k_dv_sy (dV from the score tiles of
 // k_sy_scores), both with transposing LDS reads.
 #include <algorithm>
+#include <cstdlib>
+#include <cstring>
 #include <type_traits>
 #include <utility>
 
@@ -118,69 +120,78 @@ __device__ __forceinline__ void sy_barrier() {
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   __builtin_amdgcn_s_barrier();
 }
+// The same barrier as one asm statement: the compiler moves no memory access
+// across it in either direction (the ping-pong schedule relies on that).
+__device__ __forceinline__ void sy_barrier_asm() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 // RoPE of the four adjacent pairs of one 16-byte chunk: pair m is
-// x.lo = x[2m], x.hi = x[2m+1] with cs = (cos, sin) as bf16 halves, giving
-// (x0 c - x1 s, x1 c + x0 s) rounded to bf16 once (products exact in fp32).
-// One asm block so the hazard spacing is explicit: a v_dot2 result is read
-// no sooner than three wait states after it is written (s_nop 2).  The
-// results overwrite the swapped copies, which are dead by then.
-// CONJ rotates by the negated angle, (x0 c + x1 s, x1 c - x0 s): the sign
-// modifier moves from the first pair of dot products to the second.
+// x.lo = x[2m], x.hi = x[2m+1] with cs = (cos, sin) and sw = (sin, cos) as bf16
+// halves, giving (x0 c - x1 s, x0 s + x1 c) = (dot2(x, cs) with s negated,
+// dot2(x, sw)), rounded to bf16 once (products exact in fp32).  The swapped
+// entry sw serves every chunk that shares cs, so the rows' data are never
+// swapped.  One asm block so the hazard spacing is explicit: a v_dot2 result
+// is read no sooner than three wait states after it is written (s_nop 2).
+// CONJ rotates by the negated angle, (x0 c + x1 s, -x0 s + x1 c): the sign
+// modifier moves from the first dot product to the second.
 #define SY_ROT_ASM(NA, NB)                                                                                   \
-  asm("v_alignbit_b32 %[s0], %[x0], %[x0], 16\n\t"                                                          \
-      "v_alignbit_b32 %[s1], %[x1], %[x1], 16\n\t"                                                          \
-      "v_alignbit_b32 %[s2], %[x2], %[x2], 16\n\t"                                                          \
-      "v_alignbit_b32 %[s3], %[x3], %[x3], 16\n\t"                                                          \
-      "v_dot2_f32_bf16 %[a0], %[x0], %[c0], 0" NA "\n\t"                                                    \
+  asm("v_dot2_f32_bf16 %[a0], %[x0], %[c0], 0" NA "\n\t"                                                    \
       "v_dot2_f32_bf16 %[a1], %[x1], %[c1], 0" NA "\n\t"                                                    \
       "v_dot2_f32_bf16 %[a2], %[x2], %[c2], 0" NA "\n\t"                                                    \
       "v_dot2_f32_bf16 %[a3], %[x3], %[c3], 0" NA "\n\t"                                                    \
-      "v_dot2_f32_bf16 %[b0], %[s0], %[c0], 0" NB "\n\t"                                                    \
-      "v_dot2_f32_bf16 %[b1], %[s1], %[c1], 0" NB "\n\t"                                                    \
-      "v_dot2_f32_bf16 %[b2], %[s2], %[c2], 0" NB "\n\t"                                                    \
-      "v_dot2_f32_bf16 %[b3], %[s3], %[c3], 0" NB "\n\t"                                                    \
+      "v_dot2_f32_bf16 %[b0], %[x0], %[w0], 0" NB "\n\t"                                                    \
+      "v_dot2_f32_bf16 %[b1], %[x1], %[w1], 0" NB "\n\t"                                                    \
+      "v_dot2_f32_bf16 %[b2], %[x2], %[w2], 0" NB "\n\t"                                                    \
+      "v_dot2_f32_bf16 %[b3], %[x3], %[w3], 0" NB "\n\t"                                                    \
       "s_nop 2\n\t"                                                                                         \
-      "v_cvt_pk_bf16_f32 %[s0], %[a0], %[b0]\n\t"                                                           \
-      "v_cvt_pk_bf16_f32 %[s1], %[a1], %[b1]\n\t"                                                           \
-      "v_cvt_pk_bf16_f32 %[s2], %[a2], %[b2]\n\t"                                                           \
-      "v_cvt_pk_bf16_f32 %[s3], %[a3], %[b3]"                                                                 \
-      : [s0] "=&v"(s0), [s1] "=&v"(s1), [s2] "=&v"(s2), [s3] "=&v"(s3), [a0] "=&v"(a0), [a1] "=&v"(a1),       \
+      "v_cvt_pk_bf16_f32 %[y0], %[a0], %[b0]\n\t"                                                           \
+      "v_cvt_pk_bf16_f32 %[y1], %[a1], %[b1]\n\t"                                                           \
+      "v_cvt_pk_bf16_f32 %[y2], %[a2], %[b2]\n\t"                                                           \
+      "v_cvt_pk_bf16_f32 %[y3], %[a3], %[b3]"                                                                 \
+      : [y0] "=&v"(y0), [y1] "=&v"(y1), [y2] "=&v"(y2), [y3] "=&v"(y3), [a0] "=&v"(a0), [a1] "=&v"(a1),       \
         [a2] "=&v"(a2), [a3] "=&v"(a3), [b0] "=&v"(b0), [b1] "=&v"(b1), [b2] "=&v"(b2), [b3] "=&v"(b3)         \
       : [x0] "v"(x.x), [x1] "v"(x.y), [x2] "v"(x.z), [x3] "v"(x.w), [c0] "v"(cs.x), [c1] "v"(cs.y),           \
-        [c2] "v"(cs.z), [c3] "v"(cs.w))
+        [c2] "v"(cs.z), [c3] "v"(cs.w), [w0] "v"(sw.x), [w1] "v"(sw.y), [w2] "v"(sw.z), [w3] "v"(sw.w))
 template <bool CONJ = false>
-__device__ __forceinline__ u32x4 rot_chunk(u32x4 x, u32x4 cs) {
-  uint32_t s0, s1, s2, s3;
+__device__ __forceinline__ u32x4 rot_chunk_w(u32x4 x, u32x4 cs, u32x4 sw) {
+  uint32_t y0, y1, y2, y3;
   float a0, a1, a2, a3, b0, b1, b2, b3;
   if constexpr (CONJ)
-    SY_ROT_ASM("", " neg_hi:[0,1,0]");
+    SY_ROT_ASM("", " neg_lo:[0,1,0]");
   else
     SY_ROT_ASM(" neg_hi:[0,1,0]", "");
-  return u32x4{s0, s1, s2, s3};
+  return u32x4{y0, y1, y2, y3};
 }
 #undef SY_ROT_ASM
 
-// Two pairs of the rotation above (dwords x0, x1 with table dwords c0, c1),
-// so a chunk's rotation can be split between two MFMAs.
-#define SY_ROT2_ASM(NA, NB)                                                                          \
-  asm("v_alignbit_b32 %[s0], %[x0], %[x0], 16\n\t"                                                  \
-      "v_alignbit_b32 %[s1], %[x1], %[x1], 16\n\t"                                                  \
-      "v_dot2_f32_bf16 %[a0], %[x0], %[c0], 0" NA "\n\t"                                            \
-      "v_dot2_f32_bf16 %[a1], %[x1], %[c1], 0" NA "\n\t"                                            \
-      "v_dot2_f32_bf16 %[b0], %[s0], %[c0], 0" NB "\n\t"                                            \
-      "v_dot2_f32_bf16 %[b1], %[s1], %[c1], 0" NB "\n\t"                                            \
-      "s_nop 2\n\t"                                                                                 \
-      "v_cvt_pk_bf16_f32 %[s0], %[a0], %[b0]\n\t"                                                   \
-      "v_cvt_pk_bf16_f32 %[s1], %[a1], %[b1]"                                                         \
-      : [s0] "=&v"(y0), [s1] "=&v"(y1), [a0] "=&v"(a0), [a1] "=&v"(a1), [b0] "=&v"(b0), [b1] "=&v"(b1) \
-      : [x0] "v"(x0), [x1] "v"(x1), [c0] "v"(c0), [c1] "v"(c1))
+// (sin, cos) from (cos, sin): the halves of each dword swapped
+__device__ __forceinline__ u32x4 swap_halves(u32x4 t) {
+  const uint32_t t0 = t.x, t1 = t.y, t2 = t.z, t3 = t.w;
+  return u32x4{__builtin_amdgcn_alignbit(t0, t0, 16), __builtin_amdgcn_alignbit(t1, t1, 16),
+               __builtin_amdgcn_alignbit(t2, t2, 16), __builtin_amdgcn_alignbit(t3, t3, 16)};
+}
 template <bool CONJ = false>
-__device__ __forceinline__ void rot_pairs(uint32_t x0, uint32_t x1, uint32_t c0, uint32_t c1, uint32_t& y0,
-                                          uint32_t& y1) {
+__device__ __forceinline__ u32x4 rot_chunk(u32x4 x, u32x4 cs) {
+  return rot_chunk_w<CONJ>(x, cs, swap_halves(cs));
+}
+
+// Two pairs of the rotation above (dwords x0, x1 with entries c0, c1 and their
+// swaps w0, w1), so a chunk's rotation can be split between two MFMAs.
+#define SY_ROT2_ASM(NA, NB)                                                                          \
+  asm("v_dot2_f32_bf16 %[a0], %[x0], %[c0], 0" NA "\n\t"                                            \
+      "v_dot2_f32_bf16 %[a1], %[x1], %[c1], 0" NA "\n\t"                                            \
+      "v_dot2_f32_bf16 %[b0], %[x0], %[w0], 0" NB "\n\t"                                            \
+      "v_dot2_f32_bf16 %[b1], %[x1], %[w1], 0" NB "\n\t"                                            \
+      "s_nop 2\n\t"                                                                                 \
+      "v_cvt_pk_bf16_f32 %[y0], %[a0], %[b0]\n\t"                                                   \
+      "v_cvt_pk_bf16_f32 %[y1], %[a1], %[b1]"                                                         \
+      : [y0] "=&v"(y0), [y1] "=&v"(y1), [a0] "=&v"(a0), [a1] "=&v"(a1), [b0] "=&v"(b0), [b1] "=&v"(b1) \
+      : [x0] "v"(x0), [x1] "v"(x1), [c0] "v"(c0), [c1] "v"(c1), [w0] "v"(w0), [w1] "v"(w1))
+template <bool CONJ = false>
+__device__ __forceinline__ void rot_pairs_w(uint32_t x0, uint32_t x1, uint32_t c0, uint32_t c1, uint32_t w0,
+                                            uint32_t w1, uint32_t& y0, uint32_t& y1) {
   float a0, a1, b0, b1;
   if constexpr (CONJ)
-    SY_ROT2_ASM("", " neg_hi:[0,1,0]");
+    SY_ROT2_ASM("", " neg_lo:[0,1,0]");
   else
     SY_ROT2_ASM(" neg_hi:[0,1,0]", "");
 }
@@ -341,11 +352,15 @@ __device__ __forceinline__ int sy_piece_row(int l, int half, int qq, int e) {
 // of 64 KB (the model's (B, T, nh, N) x_sparse): their pieces share few L2
 // sets, and a line fetched for one stage is gone before the next stage reads
 // its other half.
-template <int RM, bool SELF, bool GOUT = false, bool PAIR = false>
+// SCH (relative RoPE): 0 the lockstep schedule; 1 the ping-pong schedule of
+// the two wave groups (see the main loop).  Both give the same bits.
+template <int RM, bool SELF, bool GOUT = false, bool PAIR = false, int SCH = 0>
 __global__ __launch_bounds__(kSyThreads, 1) void k_sy_scores(const SyArgs a) {
   constexpr bool ROPE = RM != 0;
   constexpr bool REL = RM == 2;
   static_assert(!PAIR || REL, "paired stages: relative RoPE");
+  static_assert(SCH == 0 || REL, "ping-pong schedule: relative RoPE");
+  constexpr bool PP = SCH == 1;
   static_assert(!GOUT || (!SELF && !ROPE), "G epilogue: distinct operands, no RoPE");
   static_assert(!REL || SELF, "relative RoPE: self attention");
   const int bid = blockIdx.x;
@@ -572,186 +587,287 @@ __global__ __launch_bounds__(kSyThreads, 1) void k_sy_scores(const SyArgs a) {
         rot_store(st, wt_tag, uc, x, t);
       });
     };
-    if constexpr (PAIR) {
-      const StageDma d0 = stage_dma(0), d1 = stage_dma(1);
-      sy_static_for<4>([&](auto uc) {
-        dma_x(d0, uc);
-        dma_x(d1, uc);
-      });
-      sy_wait<0>();  // stages 0 and 1 landed
-      rotate_all(0);
-      sy_barrier();
-    } else if constexpr (REL) {
-      for (int st = 0; st < lead - 1; ++st) {
-        const StageDma d = stage_dma(st);
-        sy_static_for<4>([&](auto uc) { dma_x(d, uc); });
+    if constexpr (PP) {
+      // Ping-pong.  Waves 0-3 (group 0) and 4-7 (group 1) hold one wave per
+      // SIMD each and run the same program one barrier apart.  Per group and
+      // stage j:
+      //   MEM(j): read the fragments of stage j (both k16 halves); issue the
+      //           DMA of stage j + 3 (PAIR: of j + 2 and j + 3 on even j);
+      //           once this wave's chunks of stage j + 1 landed, make their
+      //           cos/sin entries and rotate them in LDS
+      //   barrier
+      //   MMA(j): the MFMAs of stage j
+      //   barrier
+      // Group 1 passes one extra barrier first, so its MEM(j) runs beside
+      // group 0's MMA(j) and its MMA(j) beside group 0's MEM(j + 1): on each
+      // SIMD one wave's MFMAs cover the other's waits, VALU and LDS work.
+      // Chunks are DMA'd and rotated as in the lockstep schedule (each wave
+      // its own four), and every chunk of stage j + 1 is rotated one barrier
+      // or more before either group reads fragments of it (group 0 rotates
+      // it two intervals ahead, group 1 one).  The DMA of stage j + 3 goes to
+      // the slot of stage j - 1, which group 1 last read in its MEM(j - 1),
+      // the interval before group 0's MEM(j).
+      const bool g1 = w >= 4;
+      auto rotate_stage = [&](int st) {
+        u32x4 x[4], t[NT];
+        sy_static_for<4>([&](auto uc) {
+          x[decltype(uc)::value] = *reinterpret_cast<const u32x4*>(slot(st) + vrot + decltype(uc)::value * 8192);
+        });
+        sy_static_for<NT>([&](auto ic) { t[decltype(ic)::value] = rel_entry(st, qpos[decltype(ic)::value]); });
+        u32x4 tw[NT];
+        sy_static_for<NT>([&](auto ic) { tw[decltype(ic)::value] = swap_halves(t[decltype(ic)::value]); });
+        sy_static_for<4>([&](auto uc) {
+          constexpr int u = decltype(uc)::value;
+          constexpr int ti = sy_rot_tidx<REL>(WT, u);
+          put_rot(st, uc, rot_chunk_w<sy_rot_conj<REL>(WT, u)>(x[u], t[ti], tw[ti]));
+        });
+      };
+      if constexpr (PAIR) {
+        const StageDma d0 = stage_dma(0), d1 = stage_dma(1);
+        sy_static_for<4>([&](auto uc) {
+          dma_x(d0, uc);
+          dma_x(d1, uc);
+        });
+        sy_wait<1>();  // stage 0 landed (chunk 3 of stage 1 issued after it)
+      } else {
+        sy_static_for<3>([&](auto sc) {
+          const StageDma d = stage_dma(decltype(sc)::value);
+          sy_static_for<4>([&](auto uc) { dma_x(d, uc); });
+        });
+        sy_wait<8>();  // stage 0 landed (stages 1 and 2 issued after it)
       }
-      const StageDma d = stage_dma(lead - 1);
-      dma_x(d, I0());
-      dma_x(d, I1());
-      sy_wait<(lead - 2) * 4 + 2>();  // stage 0 landed
-      rotate_all(0);
-      sy_barrier();
-      dma_x(d, I2());
-      dma_x(d, I3());
+      rotate_stage(0);
+      __builtin_amdgcn_sched_barrier(0);
+      sy_barrier_asm();
+      if (g1) sy_barrier_asm();
+      __builtin_amdgcn_sched_barrier(0);
+      for (int j = 0; j < nst; ++j) {
+        bf16x8 fa[NF], fb[NF];
+        read_frags(fa, j, 0);
+        read_frags(fb, j, 1);
+        if (j + 1 < nst) {
+          // operations issued after this wave's chunks of stage j + 1: PAIR
+          // even j, the eight of j + 2 and j + 3 just issued; PAIR odd j, chunk
+          // 3 of j + 2; otherwise stages j + 2 and j + 3
+          if constexpr (PAIR) {
+            if ((j & 1) == 0) {
+              const StageDma d = stage_dma(j + 2), d2 = stage_dma(j + 3);
+              sy_static_for<4>([&](auto uc) {
+                dma_x(d, uc);
+                dma_x(d2, uc);
+              });
+              sy_wait<8>();
+            } else {
+              sy_wait<1>();
+            }
+          } else {
+            const StageDma d = stage_dma(j + 3);
+            sy_static_for<4>([&](auto uc) { dma_x(d, uc); });
+            sy_wait<8>();
+          }
+          rotate_stage(j + 1);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        sy_barrier_asm();
+        __builtin_amdgcn_sched_barrier(0);
+        sy_static_for<NM>([&](auto mc) { mfma_m(fa, mc); });
+        sy_static_for<NM>([&](auto mc) { mfma_m(fb, mc); });
+        __builtin_amdgcn_sched_barrier(0);
+        sy_barrier_asm();
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      if (!g1) sy_barrier_asm();
+      // the re-loads past the end must land before the workgroup's LDS is freed
+      sy_wait<0>();
     } else {
-      for (int st = 0; st < lead - 1; ++st) {
-        const StageDma d = stage_dma(st);
-        sy_static_for<4>([&](auto uc) { dma_x(d, uc); });
-      }
-      const StageDma d = stage_dma(lead - 1);
-      dma_x(d, I0());
-      dma_x(d, I1());
-      if constexpr (ROPE) {
-        sy_static_for<4>([&](auto ic) { dma_t(stage_dma(0), ic); });
-        sy_wait<0>();  // stage 0 and its table landed
+      if constexpr (PAIR) {
+        const StageDma d0 = stage_dma(0), d1 = stage_dma(1);
+        sy_static_for<4>([&](auto uc) {
+          dma_x(d0, uc);
+          dma_x(d1, uc);
+        });
+        sy_wait<0>();  // stages 0 and 1 landed
         rotate_all(0);
         sy_barrier();
-        sy_static_for<4>([&](auto ic) { dma_t(stage_dma(1), ic); });
+      } else if constexpr (REL) {
+        for (int st = 0; st < lead - 1; ++st) {
+          const StageDma d = stage_dma(st);
+          sy_static_for<4>([&](auto uc) { dma_x(d, uc); });
+        }
+        const StageDma d = stage_dma(lead - 1);
+        dma_x(d, I0());
+        dma_x(d, I1());
+        sy_wait<(lead - 2) * 4 + 2>();  // stage 0 landed
+        rotate_all(0);
+        sy_barrier();
         dma_x(d, I2());
         dma_x(d, I3());
       } else {
-        dma_x(d, I2());
-        dma_x(d, I3());
-        sy_wait<(lead - 1) * 4>();  // stage 0 landed
-        sy_barrier();
-      }
-    }
-    read_frags(f0, 0, 0);
-
-    // ------------------------------------------------------------ main loop
-    // Stage s, per wave:
-    //  A. read the second-half fragments of s; first-half MFMAs of s with x
-    //     chunks 0-1 of stage s + lead issued between them; once this lane's
-    //     part of stage s+1 (and its table) landed, the rotation of stage s+1
-    //  B. barrier: stage s+1 is complete (loaded and rotated) in LDS
-    //  C. read the first-half fragments of s+1; (absolute RoPE) issue the
-    //     table of stage s+2; second-half MFMAs of s with x chunks 2-3 of
-    //     stage s + lead.
-    // The barrier sits between the halves, so after it the MFMA pipe runs the
-    // second half while the next fragments load.  Stage s + lead goes to x
-    // slot (s-1) % NX, last read before the previous barrier; the table slot
-    // is rewritten after the barrier that follows its rotation.
-    constexpr int KW = NM / 2 - 1;  // wait for stage s+1 after first-half MFMA KW
-    // (without RoPE) operations issued after the awaited ones at that wait:
-    // after x of s+1, x of s+2 .. s+lead-1 and chunks 0-1 of s + lead
-    constexpr int NWAIT = (lead - 2) * 4 + 2;
-    // RoPE: the wait for stage s+1 comes first, all four chunks and their
-    // table entries are read at once, and half a chunk is rotated after each
-    // of the first eight MFMAs (scheduling barriers keep that order, so the
-    // rotation's VALU work runs under the MFMAs).  Operations issued after
-    // the awaited ones: REL, stages s+2 .. s+lead-1 with their tables;
-    // absolute, x chunks 2-3 of s+2 after the table of s+1.
-    constexpr int NWAITR = REL ? (lead - 2) * 4 : 2;
-    constexpr int NTD = REL ? NT : 4;  // distinct table entries per lane and stage
-    for (int s = 0; s + 1 < nst; ++s) {
-      read_frags(f1, s, 1);
-      __builtin_amdgcn_sched_barrier(0);
-      const StageDma d = stage_dma(PAIR ? s + 2 : s + lead);
-      // PAIR: stage s + 3 goes to the slot of stage s - 1, whose last reads
-      // came before the previous barrier
-      const StageDma d2 = stage_dma(s + 3);
-      const bool issue = !PAIR || (s & 1) == 0;
-      if constexpr (ROPE) {
-        if constexpr (PAIR) {
-          // stage s+1 landed: even s, nothing issued after it (odd stages
-          // issue none); odd s, chunk 3 of stage s+2 after it
-          if (s & 1)
-            sy_wait<1>();
-          else
-            sy_wait<0>();
-        } else {
-          sy_wait<NWAITR>();
+        for (int st = 0; st < lead - 1; ++st) {
+          const StageDma d = stage_dma(st);
+          sy_static_for<4>([&](auto uc) { dma_x(d, uc); });
         }
-        u32x4 x[4], t[NTD];
-        sy_static_for<4>([&](auto uc) {
-          x[decltype(uc)::value] = *reinterpret_cast<const u32x4*>(slot(s + 1) + vrot + decltype(uc)::value * 8192);
-        });
-        sy_static_for<NTD>([&](auto ic) {
+        const StageDma d = stage_dma(lead - 1);
+        dma_x(d, I0());
+        dma_x(d, I1());
+        if constexpr (ROPE) {
+          sy_static_for<4>([&](auto ic) { dma_t(stage_dma(0), ic); });
+          sy_wait<0>();  // stage 0 and its table landed
+          rotate_all(0);
+          sy_barrier();
+          sy_static_for<4>([&](auto ic) { dma_t(stage_dma(1), ic); });
+          dma_x(d, I2());
+          dma_x(d, I3());
+        } else {
+          dma_x(d, I2());
+          dma_x(d, I3());
+          sy_wait<(lead - 1) * 4>();  // stage 0 landed
+          sy_barrier();
+        }
+      }
+      read_frags(f0, 0, 0);
+
+      // ------------------------------------------------------------ main loop
+      // Stage s, per wave:
+      //  A. read the second-half fragments of s; first-half MFMAs of s with x
+      //     chunks 0-1 of stage s + lead issued between them; once this lane's
+      //     part of stage s+1 (and its table) landed, the rotation of stage s+1
+      //  B. barrier: stage s+1 is complete (loaded and rotated) in LDS
+      //  C. read the first-half fragments of s+1; (absolute RoPE) issue the
+      //     table of stage s+2; second-half MFMAs of s with x chunks 2-3 of
+      //     stage s + lead.
+      // The barrier sits between the halves, so after it the MFMA pipe runs the
+      // second half while the next fragments load.  Stage s + lead goes to x
+      // slot (s-1) % NX, last read before the previous barrier; the table slot
+      // is rewritten after the barrier that follows its rotation.
+      constexpr int KW = NM / 2 - 1;  // wait for stage s+1 after first-half MFMA KW
+      // (without RoPE) operations issued after the awaited ones at that wait:
+      // after x of s+1, x of s+2 .. s+lead-1 and chunks 0-1 of s + lead
+      constexpr int NWAIT = (lead - 2) * 4 + 2;
+      // RoPE: the wait for stage s+1 comes first, all four chunks and their
+      // table entries are read at once, and half a chunk is rotated after each
+      // of the first eight MFMAs (scheduling barriers keep that order, so the
+      // rotation's VALU work runs under the MFMAs).  Operations issued after
+      // the awaited ones: REL, stages s+2 .. s+lead-1 with their tables;
+      // absolute, x chunks 2-3 of s+2 after the table of s+1.
+      constexpr int NWAITR = REL ? (lead - 2) * 4 : 2;
+      constexpr int NTD = REL ? NT : 4;  // distinct table entries per lane and stage
+      for (int s = 0; s + 1 < nst; ++s) {
+        read_frags(f1, s, 1);
+        __builtin_amdgcn_sched_barrier(0);
+        const StageDma d = stage_dma(PAIR ? s + 2 : s + lead);
+        // PAIR: stage s + 3 goes to the slot of stage s - 1, whose last reads
+        // came before the previous barrier
+        const StageDma d2 = stage_dma(s + 3);
+        const bool issue = !PAIR || (s & 1) == 0;
+        if constexpr (ROPE) {
+          if constexpr (PAIR) {
+            // stage s+1 landed: even s, nothing issued after it (odd stages
+            // issue none); odd s, chunk 3 of stage s+2 after it
+            if (s & 1)
+              sy_wait<1>();
+            else
+              sy_wait<0>();
+          } else {
+            sy_wait<NWAITR>();
+          }
+          u32x4 x[4], t[NTD];
+          sy_static_for<4>([&](auto uc) {
+            x[decltype(uc)::value] = *reinterpret_cast<const u32x4*>(slot(s + 1) + vrot + decltype(uc)::value * 8192);
+          });
+          sy_static_for<NTD>([&](auto ic) {
+            constexpr int i = decltype(ic)::value;
+            if constexpr (REL)
+              t[i] = rel_entry(s + 1, qpos[i]);
+            else
+              t[i] = *reinterpret_cast<const u32x4*>(tslot(s + 1) + vrot + i * 8192);
+          });
+          // relative: the entries with their halves swapped, once per entry
+          // (shared by two or four chunks); absolute: per chunk, below
+          u32x4 tw[REL ? NTD : 1];
           if constexpr (REL)
-            t[decltype(ic)::value] = rel_entry(s + 1, qpos[decltype(ic)::value]);
-          else
-            t[decltype(ic)::value] = *reinterpret_cast<const u32x4*>(tslot(s + 1) + vrot + decltype(ic)::value * 8192);
-        });
+            sy_static_for<NTD>([&](auto ic) { tw[decltype(ic)::value] = swap_halves(t[decltype(ic)::value]); });
+          __builtin_amdgcn_sched_barrier(0);
+          sy_static_for<NM>([&](auto mc) {
+            constexpr int m = decltype(mc)::value;
+            mfma_m(f0, mc);
+            if constexpr (m == 0) {
+              if (issue) {
+                dma_x(d, I0());
+                if constexpr (PAIR) dma_x(d2, I0());
+              }
+            }
+            if constexpr (m == 2) {
+              if (issue) {
+                dma_x(d, I1());
+                if constexpr (PAIR) dma_x(d2, I1());
+              }
+            }
+            if constexpr (m < 8) {
+              constexpr int u = m >> 1, hh = m & 1;
+              constexpr bool conj = sy_rot_conj<REL>(WT, u);
+              const u32x4 tt = t[sy_rot_tidx<REL>(WT, u)];
+              const u32x4 ww = REL ? tw[REL ? sy_rot_tidx<REL>(WT, u) : 0] : swap_halves(tt);
+              // (vector elements go through scalars: this clang lowers some
+              // element accesses of u32x4 as element 0)
+              if constexpr (hh == 0) {
+                const uint32_t x0 = x[u].x, x1 = x[u].y, c0 = tt.x, c1 = tt.y, w0 = ww.x, w1 = ww.y;
+                uint32_t y0, y1;
+                rot_pairs_w<conj>(x0, x1, c0, c1, w0, w1, y0, y1);
+                x[u].x = y0;
+                x[u].y = y1;
+              } else {
+                const uint32_t x2 = x[u].z, x3 = x[u].w, c2 = tt.z, c3 = tt.w, w2 = ww.z, w3 = ww.w;
+                uint32_t y2, y3;
+                rot_pairs_w<conj>(x2, x3, c2, c3, w2, w3, y2, y3);
+                x[u].z = y2;
+                x[u].w = y3;
+                put_rot(s + 1, std::integral_constant<int, u>(), x[u]);
+              }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+          });
+        } else {
+          sy_static_for<NM>([&](auto mc) {
+            constexpr int m = decltype(mc)::value;
+            mfma_m(f0, mc);
+            if constexpr (m == 0) dma_x(d, I0());
+            if constexpr (m == 2) dma_x(d, I1());
+            if constexpr (m == KW) sy_wait<NWAIT>();
+          });
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        sy_barrier();
+        read_frags(f0, s + 1, 0);
+        if constexpr (ROPE && !REL) {
+          const StageDma dt = stage_dma(s + 2);
+          sy_static_for<4>([&](auto ic) { dma_t(dt, ic); });
+        }
         __builtin_amdgcn_sched_barrier(0);
         sy_static_for<NM>([&](auto mc) {
           constexpr int m = decltype(mc)::value;
-          mfma_m(f0, mc);
-          if constexpr (m == 0) {
+          mfma_m(f1, mc);
+          if constexpr (m == 1) {
             if (issue) {
-              dma_x(d, I0());
-              if constexpr (PAIR) dma_x(d2, I0());
+              dma_x(d, I2());
+              if constexpr (PAIR) dma_x(d2, I2());
             }
           }
-          if constexpr (m == 2) {
+          if constexpr (m == 3) {
             if (issue) {
-              dma_x(d, I1());
-              if constexpr (PAIR) dma_x(d2, I1());
+              dma_x(d, I3());
+              if constexpr (PAIR) dma_x(d2, I3());
             }
           }
-          if constexpr (m < 8) {
-            constexpr int u = m >> 1, hh = m & 1;
-            constexpr bool conj = sy_rot_conj<REL>(WT, u);
-            const u32x4 tt = t[sy_rot_tidx<REL>(WT, u)];
-            // (vector elements go through scalars: this clang lowers some
-            // element accesses of u32x4 as element 0)
-            if constexpr (hh == 0) {
-              const uint32_t x0 = x[u].x, x1 = x[u].y, c0 = tt.x, c1 = tt.y;
-              uint32_t y0, y1;
-              rot_pairs<conj>(x0, x1, c0, c1, y0, y1);
-              x[u].x = y0;
-              x[u].y = y1;
-            } else {
-              const uint32_t x2 = x[u].z, x3 = x[u].w, c2 = tt.z, c3 = tt.w;
-              uint32_t y2, y3;
-              rot_pairs<conj>(x2, x3, c2, c3, y2, y3);
-              x[u].z = y2;
-              x[u].w = y3;
-              put_rot(s + 1, std::integral_constant<int, u>(), x[u]);
-            }
-          }
-          __builtin_amdgcn_sched_barrier(0);
-        });
-      } else {
-        sy_static_for<NM>([&](auto mc) {
-          constexpr int m = decltype(mc)::value;
-          mfma_m(f0, mc);
-          if constexpr (m == 0) dma_x(d, I0());
-          if constexpr (m == 2) dma_x(d, I1());
-          if constexpr (m == KW) sy_wait<NWAIT>();
         });
       }
-      __builtin_amdgcn_sched_barrier(0);
-      sy_barrier();
-      read_frags(f0, s + 1, 0);
-      if constexpr (ROPE && !REL) {
-        const StageDma dt = stage_dma(s + 2);
-        sy_static_for<4>([&](auto ic) { dma_t(dt, ic); });
-      }
-      __builtin_amdgcn_sched_barrier(0);
-      sy_static_for<NM>([&](auto mc) {
-        constexpr int m = decltype(mc)::value;
-        mfma_m(f1, mc);
-        if constexpr (m == 1) {
-          if (issue) {
-            dma_x(d, I2());
-            if constexpr (PAIR) dma_x(d2, I2());
-          }
-        }
-        if constexpr (m == 3) {
-          if (issue) {
-            dma_x(d, I3());
-            if constexpr (PAIR) dma_x(d2, I3());
-          }
-        }
-      });
+      // last stage: nothing left to load or rotate
+      read_frags(f1, nst - 1, 1);
+      sy_static_for<NM>([&](auto mc) { mfma_m(f0, mc); });
+      sy_static_for<NM>([&](auto mc) { mfma_m(f1, mc); });
+      // the re-loads past the end must land before the workgroup's LDS is freed
+      sy_wait<0>();
     }
-    // last stage: nothing left to load or rotate
-    read_frags(f1, nst - 1, 1);
-    sy_static_for<NM>([&](auto mc) { mfma_m(f0, mc); });
-    sy_static_for<NM>([&](auto mc) { mfma_m(f1, mc); });
-    // the re-loads past the end must land before the workgroup's LDS is freed
-    sy_wait<0>();
 
     // ------------------------------------------------------------ epilogue
     if constexpr (GOUT) {
@@ -1637,6 +1753,13 @@ bool sy_keeps_scores(const bdh_tensor4* q, const bdh_tensor4* v, size_t* scores_
 
 namespace {
 
+// Schedule of the relative-RoPE score kernel (BDH_SY_SCHEDULE): 0 lockstep
+// (default), 1 ping-pong; both give the same bits.
+int sy_schedule() {
+  const char* e = std::getenv("BDH_SY_SCHEDULE");
+  return e != nullptr && std::strcmp(e, "pingpong") == 0 ? 1 : 0;
+}
+
 // past > 0 (no RoPE): out holds rows past.. only, and the score tiles of the
 // row tiles below past / 256 are neither computed nor stored.
 int sy_run(const bdh_tensor4* q, const bdh_tensor4* k, const bdh_tensor4* v, const bdh_tensor4* out,
@@ -1707,8 +1830,13 @@ int sy_run(const bdh_tensor4* q, const bdh_tensor4* k, const bdh_tensor4* v, con
   // row strides of a multiple of 64 KB: paired stages (both halves of each
   // 128-byte line requested together)
   const bool pair = rel && (q->stride[2] * 2) % 65536 == 0;
-  if (pair)
+  const int sch = rel ? sy_schedule() : 0;
+  if (pair && sch == 1)
+    BDH_LAUNCH("k_sy_scores_paired", (k_sy_scores<2, true, false, true, 1>), gs, dim3(kSyThreads), 0, s, a);
+  else if (pair)
     BDH_LAUNCH("k_sy_scores_paired", (k_sy_scores<2, true, false, true>), gs, dim3(kSyThreads), 0, s, a);
+  else if (sch == 1)
+    BDH_LAUNCH("k_sy_scores", (k_sy_scores<2, true, false, false, 1>), gs, dim3(kSyThreads), 0, s, a);
   else if (rel)
     BDH_LAUNCH("k_sy_scores", (k_sy_scores<2, true>), gs, dim3(kSyThreads), 0, s, a);
   else if (rope)

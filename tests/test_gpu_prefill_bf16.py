@@ -295,3 +295,48 @@ def test_bf16_fused_rope_paired_stages_on_64k_rows(B, H, T, N):
     dx_c, dv_c = ext.tril_rope_score_v_bwd_saved(x_cont, v, d, freqs, 0, ws_c)
     assert torch.equal(dv_p, dv_c)
     assert torch.equal(dx_p, dx_c)
+
+
+# (B, H, T, N, D, permuted (B, T, H, N) rows)
+SCHEDULE_SHAPES = [
+    (8, 4, 512, 8192, 256, False),   # C1: 4 splits, full tile + diagonal pair
+    (2, 3, 700, 1024, 64, False),    # three row tiles: a lone diagonal tile
+    (1, 2, 300, 512, 128, False),    # ragged rows, 8 splits
+    (3, 1, 1, 256, 64, False),       # one row
+    (2, 2, 256, 2048, 256, False),   # one row tile (diagonal alone)
+    (2, 4, 517, 8192, 256, True),    # 64 KB rows: paired stages
+    (1, 8, 2048, 8192, 256, True),   # C5-like slab: one split, 256 stages, paired
+]
+
+
+@pytest.mark.parametrize("shape", SCHEDULE_SHAPES)
+def test_bf16_fused_rope_schedules_agree(shape, monkeypatch):
+    """The relative-RoPE score kernel's schedules (lockstep; ping-pong, two wave
+    groups a barrier apart) run the same instructions in other orders: same DMA
+    chunks, entries, rotations and MFMA sequence per accumulator.  Outputs and
+    kept score tiles equal bit for bit; against the oracle within 2e-2."""
+    B, H, T, N, D, perm = shape
+    print(f"ping-pong vs lockstep {shape}", flush=True)
+    g = torch.Generator(device=DEV).manual_seed(T + N + D)
+    if perm:
+        x = torch.relu(0.32 * torch.randn(B, T, H, N, generator=g, device=DEV)).to(BF).permute(0, 2, 1, 3)
+    else:
+        x = torch.relu(0.32 * torch.randn(B, H, T, N, generator=g, device=DEV)).to(BF)
+    v = torch.randn(B, 1, T, D, generator=g, device=DEV).to(BF)
+    freqs = torch.from_numpy(O.get_freqs(N)).to(DEV)
+    runs = {}
+    for sched in ("lockstep", "pingpong"):
+        monkeypatch.setenv("BDH_SY_SCHEDULE", sched)
+        out, ws = ext.tril_rope_score_v_save(x, v, freqs, 3)
+        assert ws is not None
+        runs[sched] = (out, ws)
+    assert torch.equal(runs["pingpong"][0], runs["lockstep"][0])
+    # the kept tiles, through the saved backward's dV (the workspace's table
+    # region is not written in the relative mode)
+    d = torch.randn(B, H, T, D, generator=g, device=DEV).to(BF)
+    dv = [ext.tril_rope_score_v_bwd_saved(x, v, d, freqs, 3, runs[k][1])[1] for k in ("lockstep", "pingpong")]
+    assert torch.equal(dv[0], dv[1])
+    b0 = np_of(x[:1])
+    want, _ = O.tril_rope_score_v(b0, np_of(v[:1]), O.get_freqs(N), 3, bf16=True)
+    assert rel_fro(np_of(runs["pingpong"][0][:1]), want) <= TOL[BF]
+    assert not runs["pingpong"][0][:, :, 0].any().item()
