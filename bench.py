@@ -596,6 +596,17 @@ def run_extra(torch, ext, kernels, dev, steps, warmup, x, v) -> dict:
     ms_r = time_steps(lambda: kernels.bdh_rope_rotate(x, cos, sin, out=qr, impl="hip"), steps, warmup)
     out["c1_rope_apply_hip"] = {"us": ms_r * 1e3, "gbs": 2 * x.numel() * 2 / ms_r / 1e6}
 
+    # The unchanged caller's cold prefill (bdh.py:405-412): RoPE into a fresh
+    # QR, then bdh_attn(QR, QR, V), both on the HIP kernels.
+    def bdh_py_route():
+        q = kernels.bdh_rope_rotate(x, cos, sin, impl="hip")
+        return kernels.bdh_attn(q, q, v, impl="hip")
+
+    ms_b = time_steps(bdh_py_route, steps, warmup)
+    out["c1_bdh_py_route"] = {"us": ms_b * 1e3, "tflops": F / ms_b / 1e9,
+                              "frac_bf16_peak": F / ms_b / 1e9 / PEAK_BF16_TFLOPS}
+    log(f"[bench] bdh.py route (RoPE pass + bdh_attn): {ms_b * 1e3:.1f} us, {F / ms_b / 1e9:.1f} TFLOP/s")
+
     def eager():
         s = qr @ qr.mT.contiguous()
         s.tril_(-1)
