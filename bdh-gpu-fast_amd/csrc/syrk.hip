@@ -1407,6 +1407,7 @@ struct SvArgs {
   int self = 1;        // Q = K: diagonal tiles hold their 36 lower blocks (else every tile is full)
   int nrbk = 1;        // row blocks per slab in this launch
   int nslab = 0;
+  int o16 = 0;         // output rows 16-byte aligned in groups of eight columns
 };
 
 template <typename TO, typename TV, int NS>
@@ -1601,16 +1602,57 @@ __global__ __launch_bounds__(512, 1) void k_sy_sv(const SvArgs a) {
   __syncthreads();
   if (kh == 1) return;
   TO* o = static_cast<TO*>(const_cast<void*>(a.o.p)) + b * a.o.s0 + h * a.o.s1;
+  if (!a.o16) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int row = r0 + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+          const float val = acc[i][c][r] + red[(wc * 64 + (i * 2 + c) * 16 + r) * 64 + lane];
+          if (row >= a.past && row < a.T && dok[c]) o[int64_t(row - a.past) * a.o.s2 + dcol[c]] = from_f<TO>(val);
+        }
+    return;
+  }
+  // 16-byte output rows: wave wc sums its 64 x 64 block into its own 16 KB of
+  // the reduction buffer (only it reads that region from here on), row-major
+  // fp32, then writes the block back out as eight consecutive columns a lane
+  // (one 16-byte store of bf16, two of fp32) instead of one element a store.
+  float vals[2][2][16];
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
     for (int c = 0; c < 2; ++c)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int row = r0 + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-        const float val = acc[i][c][r] + red[(wc * 64 + (i * 2 + c) * 16 + r) * 64 + lane];
-        if (row >= a.past && row < a.T && dok[c]) o[int64_t(row - a.past) * a.o.s2 + dcol[c]] = from_f<TO>(val);
-      }
+      for (int r = 0; r < 16; ++r) vals[i][c][r] = acc[i][c][r] + red[(wc * 64 + (i * 2 + c) * 16 + r) * 64 + lane];
+  float* const ob = red + wc * 64 * 64;  // [64 rows][64 columns] of this wave
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        ob[(32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)) * 64 + 32 * c + (lane & 31)] = vals[i][c][r];
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this wave's own writes
+  const int lc = (lane & 7) * 8;  // first of the lane's eight columns
+  const bool cok = 64 * wc + lc < a.D;
+#pragma unroll
+  for (int pass = 0; pass < 8; ++pass) {
+    const int lr = pass * 8 + (lane >> 3), row = r0 + lr;
+    const f32x4 v0 = *reinterpret_cast<const f32x4*>(ob + lr * 64 + lc);
+    const f32x4 v1 = *reinterpret_cast<const f32x4*>(ob + lr * 64 + lc + 4);
+    if (row < a.past || row >= a.T || !cok) continue;
+    TO* dst = o + int64_t(row - a.past) * a.o.s2 + 64 * wc + lc;
+    const float f[8] = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+    if constexpr (sizeof(TO) == 2) {
+      *reinterpret_cast<u32x4*>(dst) = u32x4{pack_bf2(f[0], f[1]), pack_bf2(f[2], f[3]), pack_bf2(f[4], f[5]),
+                                             pack_bf2(f[6], f[7])};
+    } else {
+      *reinterpret_cast<f32x4*>(dst) = v0;
+      *reinterpret_cast<f32x4*>(dst + 4) = v1;
+    }
+  }
 }
 
 template <typename TO, typename TV>
@@ -1866,6 +1908,15 @@ int sy_run(const bdh_tensor4* q, const bdh_tensor4* k, const bdh_tensor4* v, con
   sa.self = self ? 1 : 0;
   sa.nrbk = int((T + 63) / 64 - sa.rb0);
   sa.nslab = int(nslab);
+  {
+    // 16-byte stores of eight output columns need every group of eight
+    // columns 16-byte aligned (each launch's column offset is a multiple of 256)
+    const int64_t es = esize(out->dtype);
+    bool al = (reinterpret_cast<uintptr_t>(out->data) % 16) == 0;
+    for (int i = 0; i < 3; ++i)
+      if (out->size[i] > 1 && (out->stride[i] * es) % 16 != 0) al = false;
+    sa.o16 = al ? 1 : 0;
+  }
   const dim3 gsv(unsigned(8 * ((nslab + 7) / 8) * sa.nrbk));
   const bool o16 = out->dtype == BDH_BF16, v16 = v->dtype == BDH_BF16;
   // one launch per 256 columns of V (the score tiles are read again by each)
