@@ -359,7 +359,7 @@ __global__ __launch_bounds__(kSyThreads, 1) void k_sy_scores(const SyArgs a) {
   constexpr bool ROPE = RM != 0;
   constexpr bool REL = RM == 2;
   static_assert(!PAIR || REL, "paired stages: relative RoPE");
-  static_assert(SCH == 0 || REL, "ping-pong schedule: relative RoPE");
+  static_assert(SCH == 0 || (RM != 1 && !GOUT), "ping-pong schedule: relative RoPE or none");
   constexpr bool PP = SCH == 1;
   static_assert(!GOUT || (!SELF && !ROPE), "G epilogue: distinct operands, no RoPE");
   static_assert(!REL || SELF, "relative RoPE: self attention");
@@ -608,6 +608,7 @@ __global__ __launch_bounds__(kSyThreads, 1) void k_sy_scores(const SyArgs a) {
       // the slot of stage j - 1, which group 1 last read in its MEM(j - 1),
       // the interval before group 0's MEM(j).
       const bool g1 = w >= 4;
+      constexpr int L = NX - 1;  // stages issued ahead: 3 with RoPE, 4 without
       auto rotate_stage = [&](int st) {
         u32x4 x[4], t[NT];
         sy_static_for<4>([&](auto uc) {
@@ -630,13 +631,13 @@ __global__ __launch_bounds__(kSyThreads, 1) void k_sy_scores(const SyArgs a) {
         });
         sy_wait<1>();  // stage 0 landed (chunk 3 of stage 1 issued after it)
       } else {
-        sy_static_for<3>([&](auto sc) {
+        sy_static_for<L>([&](auto sc) {
           const StageDma d = stage_dma(decltype(sc)::value);
           sy_static_for<4>([&](auto uc) { dma_x(d, uc); });
         });
-        sy_wait<8>();  // stage 0 landed (stages 1 and 2 issued after it)
+        sy_wait<4 * (L - 1)>();  // stage 0 landed (stages 1 .. L - 1 issued after it)
       }
-      rotate_stage(0);
+      if constexpr (REL) rotate_stage(0);
       __builtin_amdgcn_sched_barrier(0);
       sy_barrier_asm();
       if (g1) sy_barrier_asm();
@@ -648,7 +649,7 @@ __global__ __launch_bounds__(kSyThreads, 1) void k_sy_scores(const SyArgs a) {
         if (j + 1 < nst) {
           // operations issued after this wave's chunks of stage j + 1: PAIR
           // even j, the eight of j + 2 and j + 3 just issued; PAIR odd j, chunk
-          // 3 of j + 2; otherwise stages j + 2 and j + 3
+          // 3 of j + 2; otherwise stages j + 2 .. j + L
           if constexpr (PAIR) {
             if ((j & 1) == 0) {
               const StageDma d = stage_dma(j + 2), d2 = stage_dma(j + 3);
@@ -661,11 +662,11 @@ __global__ __launch_bounds__(kSyThreads, 1) void k_sy_scores(const SyArgs a) {
               sy_wait<1>();
             }
           } else {
-            const StageDma d = stage_dma(j + 3);
+            const StageDma d = stage_dma(j + L);
             sy_static_for<4>([&](auto uc) { dma_x(d, uc); });
-            sy_wait<8>();
+            sy_wait<4 * (L - 1)>();
           }
-          rotate_stage(j + 1);
+          if constexpr (REL) rotate_stage(j + 1);
         }
         __builtin_amdgcn_sched_barrier(0);
         sy_barrier_asm();
@@ -1872,19 +1873,23 @@ int sy_run(const bdh_tensor4* q, const bdh_tensor4* k, const bdh_tensor4* v, con
   // row strides of a multiple of 64 KB: paired stages (both halves of each
   // 128-byte line requested together)
   const bool pair = rel && (q->stride[2] * 2) % 65536 == 0;
-  const int sch = rel ? sy_schedule() : 0;
+  const int sch = sy_schedule();
   if (pair && sch == 1)
     BDH_LAUNCH("k_sy_scores_paired", (k_sy_scores<2, true, false, true, 1>), gs, dim3(kSyThreads), 0, s, a);
   else if (pair)
     BDH_LAUNCH("k_sy_scores_paired", (k_sy_scores<2, true, false, true>), gs, dim3(kSyThreads), 0, s, a);
-  else if (sch == 1)
+  else if (rel && sch == 1)
     BDH_LAUNCH("k_sy_scores", (k_sy_scores<2, true, false, false, 1>), gs, dim3(kSyThreads), 0, s, a);
   else if (rel)
     BDH_LAUNCH("k_sy_scores", (k_sy_scores<2, true>), gs, dim3(kSyThreads), 0, s, a);
   else if (rope)
     BDH_LAUNCH("k_sy_scores", (k_sy_scores<1, true>), gs, dim3(kSyThreads), 0, s, a);
+  else if (self && sch == 1)
+    BDH_LAUNCH("k_sy_scores", (k_sy_scores<0, true, false, false, 1>), gs, dim3(kSyThreads), 0, s, a);
   else if (self)
     BDH_LAUNCH("k_sy_scores", (k_sy_scores<0, true>), gs, dim3(kSyThreads), 0, s, a);
+  else if (sch == 1)
+    BDH_LAUNCH("k_sy_scores", (k_sy_scores<0, false, false, false, 1>), gs, dim3(kSyThreads), 0, s, a);
   else
     BDH_LAUNCH("k_sy_scores", (k_sy_scores<0, false>), gs, dim3(kSyThreads), 0, s, a);
   if (numel4(out) == 0) return BDH_OK;
