@@ -303,7 +303,7 @@ int rope_fast_bwd(const bdh_tensor4* x, const bdh_tensor4* v, const bdh_tensor4*
   if (numel4(dv) > 0) BDH_TRY(step(sy_bwd_dv(&qr, v, dout, dv, nullptr, 0, s, tiles)));
   if (numel4(dx) == 0) return BDH_OK;
   BDH_TRY(step(sy_bwd_g(dout, v, w + p.r_g, p.tpad, s)));
-  return step(sy_dq(w + p.r_g, p.tpad, &qr, dx, s, freqs, rope_start));
+  return step(sy_dq(w + p.r_g, p.tpad, true, &qr, dx, s, freqs, rope_start));
 }
 
 // The fused RoPE op's backward from the score tiles its forward kept
@@ -345,7 +345,7 @@ int rope_saved_bwd(const bdh_tensor4* x, const bdh_tensor4* v, const bdh_tensor4
   if (numel4(dv) > 0) BDH_TRY(step(sy_bwd_dv(x, v, dout, dv, nullptr, 0, s, tiles, rel)));
   if (numel4(dx) == 0) return BDH_OK;
   BDH_TRY(step(sy_bwd_g(dout, v, w + g_off, tpad, s)));
-  return step(sy_dq(w + g_off, tpad, x, dx, s, freqs, rope_start, true));
+  return step(sy_dq(w + g_off, tpad, true, x, dx, s, freqs, rope_start, true));
 }
 
 bool vec4_rows(const bdh_tensor4* t) {
@@ -519,7 +519,7 @@ int run_bwd(const bdh_tensor4* q, const bdh_tensor4* k, const bdh_tensor4* v, co
     // bf16 self attention without RoPE: the MFMA kernel with transposing LDS
     // reads (syrk.hip); otherwise the generic tile kernel below
     int fast = kNotEligible;
-    if (self && bf && !rope) fast = sy_dq(ga.g, p.tpad, q, dq, s);
+    if (self && bf && !rope) fast = sy_dq(ga.g, p.tpad, gfast != kNotEligible, q, dq, s);
     if (fast != kNotEligible) {
       BDH_TRY(fast);
     } else if (self) {

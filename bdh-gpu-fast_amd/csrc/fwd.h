@@ -88,7 +88,9 @@ int sy_bwd_g(const bdh_tensor4* dout, const bdh_tensor4* v, void* g, int64_t tpa
 // Backward dQ = G X on the MFMA path (syrk.hip): bf16 X, self attention.
 // With freqs, out = R^T(G X) at positions rope_start + t (X = R(x)).
 // rot_b (with freqs): x is x itself, rotated in the kernel as it is staged.
-int sy_dq(const void* g, int64_t tpad, const bdh_tensor4* x, const bdh_tensor4* out, hipStream_t s,
+// g_sym: G is exactly symmetric (written by sy_bwd_g), so its rows stand in
+// for its columns and both operands stream as whole 128-byte lines.
+int sy_dq(const void* g, int64_t tpad, bool g_sym, const bdh_tensor4* x, const bdh_tensor4* out, hipStream_t s,
           const float* freqs = nullptr, int64_t rope_start = 0, bool rot_b = false);
 // Backward of the fused RoPE op on the MFMA path (syrk.hip): the score tiles
 // of R(x) R(x)^T with R(x) written to qr (absolute positions; ws starts with

@@ -961,6 +961,13 @@ __global__ __launch_bounds__(kSyThreads, 1) void k_sy_scores(const SyArgs a) {
 //  * A (G rows) uses the 64-byte-row swizzle of k_sy_scores; B rows are 512
 //    bytes with 16-byte chunk c stored at c ^ 4 (row & 3), so the four rows of
 //    one transposing read fall in different banks.
+//  * KM (G exactly symmetric, as the score kernel's G epilogue writes it):
+//    A[i][t] = G[t][i], so A is staged like B, 32 rows t x 512 bytes of
+//    columns i per stage, and read with the same transposing loads.  Every
+//    DMA row piece is then 512 bytes (four whole 128-byte lines) instead of
+//    A's 64-byte halves of a line: a stage needs 256 line requests instead of
+//    384, and the L1-to-L2 request stream, not the MFMAs, bounds this kernel.
+//    The products are the same bits (the same G values, the same order).
 typedef __attribute__((__vector_size__(4 * sizeof(__bf16)))) __bf16 bf16x4;
 typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
 
@@ -984,7 +991,7 @@ __device__ __forceinline__ bf16x4 lds_tr4(const uint8_t* p) {
 // barrier that hands the stage to the fragment reads, with the table
 // kernel's (cos, sin) entries and the score kernel's rotation, so the
 // product sees the bits of the R(x) copy the absolute score pass writes.
-template <typename TO, bool ROPE = false, bool ROTB = false>
+template <typename TO, bool ROPE = false, bool ROTB = false, bool KM = false>
 __global__ __launch_bounds__(kSyThreads, 1) void k_dq_sy(const DqsArgs a) {
   static_assert(!ROTB || ROPE, "B rotation: RoPE output");
   const int bid = blockIdx.x;
@@ -1010,13 +1017,19 @@ __global__ __launch_bounds__(kSyThreads, 1) void k_dq_sy(const DqsArgs a) {
 #pragma unroll
   for (int u = 0; u < 2; ++u) {
     const int q = (u * 8 + w) * 1024 + lane * 16;
-    const int row = q >> 6;
-    const int c = ((q >> 4) & 3) ^ ((row >> 2) & 3);
-    const int gi = min(i0 + row, a.tpad - 1);  // rows past tpad: garbage, not stored
-    aoff[u] = uint32_t((gi * a.tpad + 8 * c) * 2);
-    const int rb = q >> 9, pb = (q >> 4) & 31;
+    const int rb = q >> 9, pb = (q >> 4) & 31, pc = pb ^ (4 * (rb & 3));
+    if constexpr (KM) {
+      // row rb of the stage, columns i0 + 8 pc ..; columns past tpad (output
+      // rows past tpad): garbage, not stored
+      aoff[u] = uint32_t((rb * a.tpad + min(i0 + 8 * pc, a.tpad - 8)) * 2);
+    } else {
+      const int row = q >> 6;
+      const int c = ((q >> 4) & 3) ^ ((row >> 2) & 3);
+      const int gi = min(i0 + row, a.tpad - 1);  // rows past tpad: garbage, not stored
+      aoff[u] = uint32_t((gi * a.tpad + 8 * c) * 2);
+    }
     brow[u] = rb;
-    bcol[u] = uint32_t((n0 + 8 * (pb ^ (4 * (rb & 3)))) * 2);
+    bcol[u] = uint32_t((n0 + 8 * pc) * 2);
   }
   constexpr int NX = 5, lead = NX - 1;
   auto slot = [&](int st) { return sy_lds + (st % NX) * kSySlot; };
@@ -1028,7 +1041,7 @@ __global__ __launch_bounds__(kSyThreads, 1) void k_dq_sy(const DqsArgs a) {
     StageDma d;
     d.m0 = wl + uint32_t((st % NX) * kSySlot);
     const int sc = min(st, nst - 1);
-    d.ka = uint32_t(sc * 64);
+    d.ka = KM ? uint32_t(sc) * uint32_t(64 * a.tpad) : uint32_t(sc * 64);  // tpad^2 * 2 < 2^31
     d.krow = uint32_t(sc * 32);
     return d;
   };
@@ -1051,13 +1064,19 @@ __global__ __launch_bounds__(kSyThreads, 1) void k_dq_sy(const DqsArgs a) {
     loff[k2] = uint32_t((lane & 31) * 64 + c * 16);
   }
   const int g4 = lane >> 4, q = lane & 15;
+  // transposing-read address of 32 columns from col0 in a 32 x 512-byte block
+  auto tr_off = [&](int col0) {
+    const int col = col0 + 16 * (g4 & 1) + 4 * (q & 3);
+    const int row = 8 * (g4 >> 1) + (q >> 2);
+    return row * 512 + (((col >> 3) ^ (4 * (row & 3))) * 16) + ((col >> 2) & 1) * 8;
+  };
   int boff[2];
 #pragma unroll
-  for (int jb = 0; jb < 2; ++jb) {
-    const int col = 64 * wn + 32 * jb + 16 * (g4 & 1) + 4 * (q & 3);
-    const int row = 8 * (g4 >> 1) + (q >> 2);
-    boff[jb] = kSyBlk + row * 512 + (((col >> 3) ^ (4 * (row & 3))) * 16) + ((col >> 2) & 1) * 8;
-  }
+  for (int jb = 0; jb < 2; ++jb) boff[jb] = kSyBlk + tr_off(64 * wn + 32 * jb);
+  // KM: A rows 128 wm + 32 i as columns of the stage's A block
+  int akm[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) akm[i] = KM ? tr_off(128 * wm + 32 * i) : 0;
   f32x16 acc[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i)
@@ -1088,8 +1107,17 @@ __global__ __launch_bounds__(kSyThreads, 1) void k_dq_sy(const DqsArgs a) {
   bf16x8 f0[6], f1[6];
   auto read_frags = [&](bf16x8(&f)[6], int st, int hf) {
     const uint8_t* sl = slot(st);
+    if constexpr (KM) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) f[i] = *reinterpret_cast<const bf16x8*>(sl + (4 * wm + i) * 2048 + loff[hf]);
+      for (int i = 0; i < 4; ++i) {
+        const uint8_t* pa = sl + akm[i] + hf * 16 * 512;
+        const bf16x4 lo = lds_tr4(pa), hi = lds_tr4(pa + 4 * 512);
+        f[i] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) f[i] = *reinterpret_cast<const bf16x8*>(sl + (4 * wm + i) * 2048 + loff[hf]);
+    }
 #pragma unroll
     for (int jb = 0; jb < 2; ++jb) {
       const uint8_t* pb = sl + boff[jb] + hf * 16 * 512;
@@ -1987,7 +2015,29 @@ int sy_past(const bdh_tensor4* q, const bdh_tensor4* k, const bdh_tensor4* v, co
 // dQ = G X (self attention, bf16 X) on the MFMA path; with freqs, out =
 // R^T(G X) at positions rope_start + t (x is then R(x)).  kNotEligible when
 // the shapes fall outside it.
-int sy_dq(const void* g, int64_t tpad, const bdh_tensor4* x, const bdh_tensor4* out, hipStream_t s,
+namespace {
+template <bool KM>
+int launch_dq(const DqsArgs& a, bool bf_out, bool rope, bool rot_b, dim3 gs, hipStream_t s) {
+  if (rope && rot_b) {
+    if (bf_out)
+      BDH_LAUNCH("k_dq_sy", (k_dq_sy<bf16_t, true, true, KM>), gs, dim3(kSyThreads), 0, s, a);
+    else
+      BDH_LAUNCH("k_dq_sy", (k_dq_sy<float, true, true, KM>), gs, dim3(kSyThreads), 0, s, a);
+  } else if (rope) {
+    if (bf_out)
+      BDH_LAUNCH("k_dq_sy", (k_dq_sy<bf16_t, true, false, KM>), gs, dim3(kSyThreads), 0, s, a);
+    else
+      BDH_LAUNCH("k_dq_sy", (k_dq_sy<float, true, false, KM>), gs, dim3(kSyThreads), 0, s, a);
+  } else if (bf_out) {
+    BDH_LAUNCH("k_dq_sy", (k_dq_sy<bf16_t, false, false, KM>), gs, dim3(kSyThreads), 0, s, a);
+  } else {
+    BDH_LAUNCH("k_dq_sy", (k_dq_sy<float, false, false, KM>), gs, dim3(kSyThreads), 0, s, a);
+  }
+  return BDH_OK;
+}
+}  // namespace
+
+int sy_dq(const void* g, int64_t tpad, bool g_sym, const bdh_tensor4* x, const bdh_tensor4* out, hipStream_t s,
           const float* freqs, int64_t rope_start, bool rot_b) {
   const int64_t B = x->size[0], H = x->size[1], T = x->size[2], N = x->size[3];
   if (x->dtype != BDH_BF16 || N % kSyTile != 0 || T < 1 || !rows16(x)) return kNotEligible;
@@ -2018,22 +2068,8 @@ int sy_dq(const void* g, int64_t tpad, const bdh_tensor4* x, const bdh_tensor4* 
   a.freqs = freqs;
   a.rope_start = rope_start;
   const dim3 gs{unsigned(grid)};
-  if (freqs != nullptr && rot_b) {
-    if (out->dtype == BDH_BF16)
-      BDH_LAUNCH("k_dq_sy", (k_dq_sy<bf16_t, true, true>), gs, dim3(kSyThreads), 0, s, a);
-    else
-      BDH_LAUNCH("k_dq_sy", (k_dq_sy<float, true, true>), gs, dim3(kSyThreads), 0, s, a);
-  } else if (freqs != nullptr) {
-    if (out->dtype == BDH_BF16)
-      BDH_LAUNCH("k_dq_sy", (k_dq_sy<bf16_t, true>), gs, dim3(kSyThreads), 0, s, a);
-    else
-      BDH_LAUNCH("k_dq_sy", (k_dq_sy<float, true>), gs, dim3(kSyThreads), 0, s, a);
-  } else if (out->dtype == BDH_BF16) {
-    BDH_LAUNCH("k_dq_sy", k_dq_sy<bf16_t>, gs, dim3(kSyThreads), 0, s, a);
-  } else {
-    BDH_LAUNCH("k_dq_sy", k_dq_sy<float>, gs, dim3(kSyThreads), 0, s, a);
-  }
-  return BDH_OK;
+  if (g_sym) return launch_dq<true>(a, out->dtype == BDH_BF16, freqs != nullptr, rot_b, gs, s);
+  return launch_dq<false>(a, out->dtype == BDH_BF16, freqs != nullptr, rot_b, gs, s);
 }
 
 
