@@ -985,6 +985,16 @@ struct DqsArgs {
 __device__ __forceinline__ bf16x4 lds_tr4(const uint8_t* p) {
   return __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(p));
 }
+typedef __attribute__((address_space(3))) bf16x8 lds_bf16x8;
+// An LDS byte address as an LDS pointer: reads at a wave-uniform slot base plus
+// a per-lane offset take one VALU add, and constant offsets go into the
+// instruction's offset field.
+__device__ __forceinline__ const lds_u8* lds_at(uint32_t addr) {
+  return reinterpret_cast<const lds_u8*>(size_t(addr));
+}
+__device__ __forceinline__ bf16x4 lds_tr4(const lds_u8* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(p));
+}
 
 // ROTB (with ROPE): X is x itself and each lane rotates the B chunks it
 // loaded (positions rope_start + row) in LDS after they land and before the
@@ -1031,15 +1041,18 @@ __global__ __launch_bounds__(kSyThreads, 1) void k_dq_sy(const DqsArgs a) {
     brow[u] = rb;
     bcol[u] = uint32_t((n0 + 8 * pc) * 2);
   }
+  // ring of NX slots: stage st in slot st % NX, tracked as rotating scalar
+  // slot indices in the loop (a modulo of the stage index made the compiler
+  // rebuild every fragment address per stage)
   constexpr int NX = 5, lead = NX - 1;
-  auto slot = [&](int st) { return sy_lds + (st % NX) * kSySlot; };
+  auto slot_addr = [&](int k) { return lds0 + uint32_t(k * kSySlot); };
   struct StageDma {
     uint32_t m0, ka, krow;
   };
   const uint32_t wl = lds0 + uint32_t(w) * 1024u;
-  auto stage_dma = [&](int st) {
+  auto stage_dma = [&](int st, int k) {
     StageDma d;
-    d.m0 = wl + uint32_t((st % NX) * kSySlot);
+    d.m0 = wl + uint32_t(k * kSySlot);
     const int sc = min(st, nst - 1);
     d.ka = KM ? uint32_t(sc) * uint32_t(64 * a.tpad) : uint32_t(sc * 64);  // tpad^2 * 2 < 2^31
     d.krow = uint32_t(sc * 32);
@@ -1091,11 +1104,11 @@ __global__ __launch_bounds__(kSyThreads, 1) void k_dq_sy(const DqsArgs a) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) bfq[u][j] = a.freqs[(bcol[u] >> 1) + 2 * j];
   }
-  auto rotate_b = [&](int st) __attribute__((always_inline)) {
+  auto rotate_b = [&](int st, int k) __attribute__((always_inline)) {
     if constexpr (ROTB) {
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
-        uint8_t* const pc = slot(st) + kSyBlk + u * 8192 + w * 1024 + lane * 16;
+        uint8_t* const pc = sy_lds + k * kSySlot + kSyBlk + u * 8192 + w * 1024 + lane * 16;
         const u32x4 xv = *reinterpret_cast<const u32x4*>(pc);
         const float pos = float(a.rope_start + st * 32 + brow[u]);
         const u32x4 cs{rope_cs(pos, bfq[u][0]), rope_cs(pos, bfq[u][1]), rope_cs(pos, bfq[u][2]),
@@ -1105,22 +1118,23 @@ __global__ __launch_bounds__(kSyThreads, 1) void k_dq_sy(const DqsArgs a) {
     }
   };
   bf16x8 f0[6], f1[6];
-  auto read_frags = [&](bf16x8(&f)[6], int st, int hf) {
-    const uint8_t* sl = slot(st);
+  // sa: LDS address of the stage's slot (wave-uniform)
+  auto read_frags = [&](bf16x8(&f)[6], uint32_t sa, int hf) {
     if constexpr (KM) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const uint8_t* pa = sl + akm[i] + hf * 16 * 512;
+        const lds_u8* pa = lds_at(sa + uint32_t(akm[i])) + hf * 16 * 512;
         const bf16x4 lo = lds_tr4(pa), hi = lds_tr4(pa + 4 * 512);
         f[i] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
       }
     } else {
+      const lds_u8* pa = lds_at(sa + uint32_t(wm * 8192) + loff[hf]);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) f[i] = *reinterpret_cast<const bf16x8*>(sl + (4 * wm + i) * 2048 + loff[hf]);
+      for (int i = 0; i < 4; ++i) f[i] = *reinterpret_cast<const lds_bf16x8*>(pa + i * 2048);
     }
 #pragma unroll
     for (int jb = 0; jb < 2; ++jb) {
-      const uint8_t* pb = sl + boff[jb] + hf * 16 * 512;
+      const lds_u8* pb = lds_at(sa + uint32_t(boff[jb])) + hf * 16 * 512;
       const bf16x4 lo = lds_tr4(pb), hi = lds_tr4(pb + 4 * 512);
       f[4 + jb] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
     }
@@ -1130,23 +1144,26 @@ __global__ __launch_bounds__(kSyThreads, 1) void k_dq_sy(const DqsArgs a) {
 
   // prologue: stages 0 .. lead-1, then stage 0 landed
   for (int st = 0; st < lead; ++st) {
-    const StageDma d = stage_dma(st);
+    const StageDma d = stage_dma(st, st);
     dma_a(d, I0());
     dma_a(d, I1());
     dma_b(d, I0());
     dma_b(d, I1());
   }
   sy_wait<(lead - 1) * 4>();
-  rotate_b(0);
+  rotate_b(0, 0);
   sy_barrier();
-  read_frags(f0, 0, 0);
+  read_frags(f0, slot_addr(0), 0);
   // stage s: second-half fragment reads; first-half MFMAs with the A chunks of
   // stage s + lead; wait for stage s+1; barrier; first-half fragments of s+1;
-  // second-half MFMAs with the B chunks of stage s + lead
+  // second-half MFMAs with the B chunks of stage s + lead.  Slots: ks of
+  // stage s, kn of s + 1, kl of s + lead (= s - 1 mod NX).
+  int ks = 0;
   for (int s = 0; s + 1 < nst; ++s) {
-    read_frags(f1, s, 1);
+    const int kn = ks == NX - 1 ? 0 : ks + 1, kl = ks == 0 ? NX - 1 : ks - 1;
+    read_frags(f1, slot_addr(ks), 1);
     __builtin_amdgcn_sched_barrier(0);
-    const StageDma d = stage_dma(s + lead);
+    const StageDma d = stage_dma(s + lead, kl);
     sy_static_for<8>([&](auto mc) {
       constexpr int m = decltype(mc)::value;
       acc[m] = mma(f0[m >> 1], f0[4 + (m & 1)], acc[m]);
@@ -1155,9 +1172,9 @@ __global__ __launch_bounds__(kSyThreads, 1) void k_dq_sy(const DqsArgs a) {
       if constexpr (m == 3) sy_wait<(lead - 2) * 4 + 2>();  // stage s+1 landed
     });
     __builtin_amdgcn_sched_barrier(0);
-    rotate_b(s + 1);
+    rotate_b(s + 1, kn);
     sy_barrier();
-    read_frags(f0, s + 1, 0);
+    read_frags(f0, slot_addr(kn), 0);
     __builtin_amdgcn_sched_barrier(0);
     sy_static_for<8>([&](auto mc) {
       constexpr int m = decltype(mc)::value;
@@ -1165,8 +1182,9 @@ __global__ __launch_bounds__(kSyThreads, 1) void k_dq_sy(const DqsArgs a) {
       if constexpr (m == 1) dma_b(d, I0());
       if constexpr (m == 3) dma_b(d, I1());
     });
+    ks = kn;
   }
-  read_frags(f1, nst - 1, 1);
+  read_frags(f1, slot_addr(ks), 1);
   sy_static_for<8>([&](auto mc) {
     constexpr int m = decltype(mc)::value;
     acc[m] = mma(f0[m >> 1], f0[4 + (m & 1)], acc[m]);
