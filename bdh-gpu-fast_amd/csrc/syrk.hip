@@ -1196,48 +1196,70 @@ __global__ __launch_bounds__(kSyThreads, 1) void k_dq_sy(const DqsArgs a) {
   sy_wait<0>();  // the re-loads past the end land before the LDS is freed
 
   TO* o = static_cast<TO*>(a.o) + b * a.o0 + h * a.o1;
-  if constexpr (ROPE) {
-    // R^T of the RoPE pair (2p, 2p + 1) = columns of lanes l and l ^ 1:
-    // dx[2p] = g[2p] c + g[2p+1] s, dx[2p+1] = g[2p+1] c - g[2p] s, with the
-    // (cos, sin) dword of rope_cs (the table kernel's bits) at position
-    // rope_start + row, fp32 arithmetic, one rounding to TO
-    // Lanes l and l ^ 1 share every (row, pair): each makes the dwords of the
-    // values r with r % 2 == l % 2 and takes the others from its partner, and
-    // partners swap values with a DPP quad permute (1, 0, 3, 2).
-    const bool odd = (lane & 1) != 0;
-    auto swap1 = [](uint32_t u) { return uint32_t(__builtin_amdgcn_mov_dpp(int(u), 0xB1, 0xF, 0xF, false)); };
-    float fq[2];
-#pragma unroll
-    for (int u = 0; u < 2; ++u) fq[u] = a.freqs[(n0 + 64 * wn + 32 * u + (lane & 31)) & ~1];
-#pragma unroll
-    for (int m = 0; m < 8; ++m)
-#pragma unroll
-      for (int r = 0; r < 16; r += 2) {
-        const int row0 = i0 + 128 * wm + 32 * (m >> 1) + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+  // Element (m, r) of this lane: row i0 + 128 wm + rr(m, r) + 4 (lane >> 5),
+  // column n0 + 64 wn + 32 (m & 1) + (lane & 31).  On a full row block (every
+  // row below T; wave-uniform) each store's row base is a scalar pointer and
+  // the lane's part a 32-bit offset (the host keeps 4 rows of out below 2^31
+  // bytes), so the stores need no per-lane 64-bit address arithmetic and no
+  // exec-mask branch; the last, partial row block keeps the per-row check.
+  auto rr_of = [](int m, int r) { return 32 * (m >> 1) + 8 * (r >> 2) + (r & 3); };
+  char* const ob = reinterpret_cast<char*>(o + int64_t(i0 + 128 * wm) * a.o2 + (n0 + 64 * wn));
+  const int64_t o2b = a.o2 * int64_t(sizeof(TO));
+  const uint32_t lofs = uint32_t(4 * (lane >> 5)) * uint32_t(o2b) + uint32_t((lane & 31) * sizeof(TO));
+  auto epilogue = [&](auto fullc) __attribute__((always_inline)) {
+    constexpr bool FULL = decltype(fullc)::value;
+    auto put = [&](int m, int r, float y) __attribute__((always_inline)) {
+      if constexpr (FULL) {
+        char* const rp = ob + int64_t(rr_of(m, r)) * o2b + 32 * (m & 1) * int(sizeof(TO));
+        *reinterpret_cast<TO*>(rp + lofs) = from_f<TO>(y);
+      } else {
+        const int row = i0 + 128 * wm + rr_of(m, r) + 4 * (lane >> 5);
         const int col = n0 + 64 * wn + 32 * (m & 1) + (lane & 31);
-        // this lane makes the dword of value r + (lane & 1); the partner the other
-        const uint32_t mine = rope_cs(float(a.rope_start + row0 + (odd ? 1 : 0)), fq[m & 1]);
-        const uint32_t theirs = swap1(mine);
-        const uint32_t cws[2] = {odd ? theirs : mine, odd ? mine : theirs};
-#pragma unroll
-        for (int e = 0; e < 2; ++e) {
-          const float v = acc[m][r + e];
-          const float pv = __uint_as_float(swap1(__float_as_uint(v)));
-          const float c = __uint_as_float(cws[e] << 16), sn = __uint_as_float(cws[e] & 0xffff0000u);
-          const float y = odd ? fmaf(v, c, -(pv * sn)) : fmaf(v, c, pv * sn);
-          if (row0 + e < a.T) o[int64_t(row0 + e) * a.o2 + col] = from_f<TO>(y);
-        }
+        if (row < a.T) o[int64_t(row) * a.o2 + col] = from_f<TO>(y);
       }
-    return;
-  }
+    };
+    if constexpr (ROPE) {
+      // R^T of the RoPE pair (2p, 2p + 1) = columns of lanes l and l ^ 1:
+      // dx[2p] = g[2p] c + g[2p+1] s, dx[2p+1] = g[2p+1] c - g[2p] s, with the
+      // (cos, sin) dword of rope_cs (the table kernel's bits) at position
+      // rope_start + row, fp32 arithmetic, one rounding to TO
+      // Lanes l and l ^ 1 share every (row, pair): each makes the dwords of the
+      // values r with r % 2 == l % 2 and takes the others from its partner, and
+      // partners swap values with a DPP quad permute (1, 0, 3, 2).
+      const bool odd = (lane & 1) != 0;
+      auto swap1 = [](uint32_t u) { return uint32_t(__builtin_amdgcn_mov_dpp(int(u), 0xB1, 0xF, 0xF, false)); };
+      float fq[2];
 #pragma unroll
-  for (int m = 0; m < 8; ++m)
+      for (int u = 0; u < 2; ++u) fq[u] = a.freqs[(n0 + 64 * wn + 32 * u + (lane & 31)) & ~1];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int row = i0 + 128 * wm + 32 * (m >> 1) + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-      const int col = n0 + 64 * wn + 32 * (m & 1) + (lane & 31);
-      if (row < a.T) o[int64_t(row) * a.o2 + col] = from_f<TO>(acc[m][r]);
+      for (int m = 0; m < 8; ++m)
+#pragma unroll
+        for (int r = 0; r < 16; r += 2) {
+          const int row0 = i0 + 128 * wm + rr_of(m, r) + 4 * (lane >> 5);
+          // this lane makes the dword of value r + (lane & 1); the partner the other
+          const uint32_t mine = rope_cs(float(a.rope_start + row0 + (odd ? 1 : 0)), fq[m & 1]);
+          const uint32_t theirs = swap1(mine);
+          const uint32_t cws[2] = {odd ? theirs : mine, odd ? mine : theirs};
+#pragma unroll
+          for (int e = 0; e < 2; ++e) {
+            const float v = acc[m][r + e];
+            const float pv = __uint_as_float(swap1(__float_as_uint(v)));
+            const float c = __uint_as_float(cws[e] << 16), sn = __uint_as_float(cws[e] & 0xffff0000u);
+            const float y = odd ? fmaf(v, c, -(pv * sn)) : fmaf(v, c, pv * sn);
+            put(m, r + e, y);
+          }
+        }
+    } else {
+#pragma unroll
+      for (int m = 0; m < 8; ++m)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) put(m, r, acc[m][r]);
     }
+  };
+  if (i0 + kSyTile <= a.T)
+    epilogue(std::true_type());
+  else
+    epilogue(std::false_type());
 }
 
 // ---------------------------------------- backward: dV from score tiles
@@ -2062,6 +2084,7 @@ int sy_dq(const void* g, int64_t tpad, bool g_sym, const bdh_tensor4* x, const b
   if (out->size[0] != B || out->size[1] != H || out->size[2] != T || out->size[3] != N) return kNotEligible;
   if (tpad % 32 != 0 || tpad * tpad * 2 >= (int64_t(1) << 31)) return kNotEligible;
   if (((T - 1) * x->stride[2] + N) * 2 >= (int64_t(1) << 31)) return kNotEligible;
+  if (out->stride[2] >= (int64_t(1) << 26)) return kNotEligible;  // 4 rows of out < 2^31 bytes
   const int64_t nslab = B * H;
   const int64_t nti = (T + kSyTile - 1) / kSyTile, ntn = N / kSyTile;
   const int64_t grid = 8 * ((nslab + 7) / 8) * nti * ntn;
