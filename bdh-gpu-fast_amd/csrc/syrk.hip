@@ -12,10 +12,11 @@
 //     * 256x256 output tiles over the lower triangle of each (b,h) slab; with
 //       Q = K the diagonal tiles go in pairs, each computing its 36 lower
 //       32x32 blocks (four 9-block wave programs per tile).
-//     * split-K: split s of n handles the 64-wide k-chunks s, s+n, s+2n, ...;
-//       all items of a slab run the same number of stages on one XCD
-//       (workgroup id % 8 selects the XCD), so the tiles that load the same
-//       row blocks walk k in step and the second load is an L2 hit.
+//     * split-K: split s of n handles a contiguous range of 64-wide k-chunks,
+//       walked from an offset set by the slab's group on its XCD; all items
+//       of a slab run on one XCD (workgroup id % 8 selects the XCD), so the
+//       tiles that load the same row blocks walk k in step and the second
+//       load is an L2 hit.
 //     * x streams HBM -> LDS through global_load_lds_dwordx4 into a ring of
 //       32-wide k stages (5 slots issued four stages ahead; with RoPE 4 slots,
 //       and a fifth for the next stage's table entries or the frequencies).  The 16-byte chunk
@@ -23,7 +24,7 @@
 //       row, which makes the MFMA fragment reads bank-conflict free.
 //     * RoPE is applied in place in the stage before its MFMAs: each lane
 //       rotates the chunks it loaded itself (per pair two v_dot2_f32_bf16,
-//       products exact in fp32, one v_cvt_pk_bf16_f32 and one v_alignbit_b32).
+//       products exact in fp32, and one v_cvt_pk_bf16_f32).
 //     * A barrier between the two k16 halves of a stage, fragments of the
 //       next half read before the current half's MFMAs.
 //     * v_mfma_f32_32x32x16_bf16 with fp32 accumulators; the epilogue stores
@@ -377,7 +378,9 @@ __global__ __launch_bounds__(kSyThreads, 1) void k_sy_scores(const SyArgs a) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int S = a.nsplit;
-  const int nch = (a.nchunk - split + S - 1) / S;
+  // k chunks (64 wide) of this split: the contiguous range [kc0, kc0 + nch)
+  const int kc0 = (split * a.nchunk) / S;
+  const int nch = ((split + 1) * a.nchunk) / S - kc0;
   const int nst = 2 * nch;
 
   const void* baseA = sgpr_ptr(a.q + b * a.q0 + h * a.q1);
@@ -433,7 +436,21 @@ __global__ __launch_bounds__(kSyThreads, 1) void k_sy_scores(const SyArgs a) {
   // block only for a single diagonal tile, which loads it twice).
   const bool write_qr = RM == 1 && a.qr != nullptr && diag;
 
-  auto kofs = [&](int s) { return (split + S * (s >> 1)) * 64 + (s & 1) * 32; };
+  // Stage s reads half s & 1 of the split's chunk (s / 2 + krs) mod nch.  The
+  // four slab groups on one XCD (slab / 8) start a quarter of the range apart,
+  // so at any time the XCD's items read x at different offsets of their rows:
+  // rows 16 KB or 64 KB apart at one offset fall on few memory channels.  C1
+  // without RoPE 75 -> 66 us, the model's (B, T, nh, N) view at C2 501 ->
+  // 245 us (plain) and 389 -> 355 us (fused, paired); against splits that
+  // interleave 64-wide chunks, all started at offset 0.  Both items of a split
+  // (the full tile and the diagonal pair) walk the same order, so the second
+  // reader of a row piece finds it in L2.
+  const int krs = ((slab >> 3) * (nch >> 2 > 0 ? nch >> 2 : 1)) % nch;
+  auto kofs = [&](int s) {
+    int c = (s >> 1) + krs;
+    c = c >= nch ? c - nch : c;
+    return (kc0 + c) * 64 + (s & 1) * 32;
+  };
   // LDS: an x ring of NX slots, issued lead = NX - 1 stages ahead; with RoPE
   // four x slots and a fifth slot: absolute positions, the table entries of
   // the next stage; relative, the frequencies of this workgroup's stages
@@ -1752,8 +1769,8 @@ struct SyPlan {
 // Work items of one (b, h) slab: with Q = K the full tiles below the diagonal
 // plus the diagonal tiles in pairs (each pair costs about one full tile and
 // loads two row blocks, like a full tile), else every lower tile in full.
-// Every item of a slab runs the same split count, so all items have the same
-// number of stages and walk k in step: a full tile and the diagonal pair of
+// Every item of a slab runs the same split count, and the items of one split
+// the same stages in the same order: a full tile and the diagonal pair of
 // the same two row blocks then load the same bytes at the same time and the
 // second load is served by the XCD's L2.  The split count is the smallest
 // that gives every CU a work item.  s0 > 0 keeps the row tiles from s0 on
