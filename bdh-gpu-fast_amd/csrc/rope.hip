@@ -145,21 +145,24 @@ __global__ __launch_bounds__(256) void k_rope8(RopeArgs a) {
   store8(static_cast<TO*>(const_cast<void*>(a.o.p)) + b * a.o.s0 + h * a.o.s1 + t * a.o.s2 + e0, y);
 }
 
-// Tables broadcast over batch and heads (the model's case): grid (N / 2048,
-// T, ceil(B * H / 8)); each thread loads its cos/sin once and rotates its
-// eight elements in a run of up to eight (b, h) rows, all eight loads in
-// flight, with non-temporal loads and stores.  So the tables are read once
-// per eight rows, and the grid spans the batch rows too (at C1: 98.6 against
-// 126 us with one workgroup per (column block, t) walking all B * H rows,
-// four in flight; a plain copy of x takes 89 us).
+// Tables broadcast over batch and heads (the model's case): grid
+// (ceil(B * H / 8), N / 2048, T); each thread loads its cos/sin once and
+// rotates its eight elements in a run of up to eight (b, h) rows, all eight
+// loads in flight, with non-temporal loads and stores.  So the tables are
+// read once per eight rows, and the grid spans the batch rows too (at C1:
+// 98.6 against 126 us with one workgroup per (column block, t) walking all
+// B * H rows, four in flight; a plain copy of x takes 89 us).  The row runs
+// that share a table entry are neighbours in the grid, so they run together
+// and the later ones find the entry in L2 (C1: 109.8 -> 106.2 us against
+// the same grid with the row runs slowest; 16 rows a run: 117 us).
 constexpr int kRopeRows = 8;  // (b, h) rows per workgroup of k_rope8_bc
 
 template <typename TV, typename TC, typename TO>
 __global__ __launch_bounds__(256) void k_rope8_bc(RopeArgs a) {
 #pragma clang fp contract(off)
-  const int64_t e0 = (int64_t(blockIdx.x) * 256 + threadIdx.x) * 8;
+  const int64_t e0 = (int64_t(blockIdx.y) * 256 + threadIdx.x) * 8;
   if (e0 >= a.N) return;
-  const int64_t t = blockIdx.y;
+  const int64_t t = blockIdx.z;
   const Vec8<TC> c = load8(static_cast<const TC*>(a.c.p) + t * a.c.s2 + e0);
   const Vec8<TC> sn = load8(static_cast<const TC*>(a.s.p) + t * a.s.s2 + e0);
   float cf[8], sf[8];
@@ -201,7 +204,7 @@ __global__ __launch_bounds__(256) void k_rope8_bc(RopeArgs a) {
   };
   const TV* vp = static_cast<const TV*>(a.v.p) + t * a.v.s2 + e0;
   TO* op = static_cast<TO*>(const_cast<void*>(a.o.p)) + t * a.o.s2 + e0;
-  const int64_t bh0 = int64_t(blockIdx.z) * kRopeRows;
+  const int64_t bh0 = int64_t(blockIdx.x) * kRopeRows;
   const int64_t bh1 = bh0 + kRopeRows < a.BH ? bh0 + kRopeRows : a.BH;
   if (bh1 - bh0 == kRopeRows) {
     Vec8<TV> x[kRopeRows];
@@ -238,7 +241,7 @@ static int launch_rope(const RopeArgs& a, hipStream_t s) {
   // per-row kernel, whose grid also spans B * H.
   const int64_t bc_wgs = (a.N + 2047) / 2048 * a.T;
   if (a.vec8 && a.bcast && bc_wgs >= 512) {
-    dim3 grid((unsigned)((a.N + 2047) / 2048), (unsigned)a.T, (unsigned)((a.BH + kRopeRows - 1) / kRopeRows));
+    dim3 grid((unsigned)((a.BH + kRopeRows - 1) / kRopeRows), (unsigned)((a.N + 2047) / 2048), (unsigned)a.T);
     BDH_LAUNCH("k_rope", (k_rope8_bc<TV, TC, TO>), grid, dim3(256), 0, s, a);
     return BDH_OK;
   }
