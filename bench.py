@@ -27,7 +27,9 @@ The JSON line also carries:
     profiler's kernel trace).  ``traffic`` is the HBM
     bytes per launch from the committed rocprofv3 counter runs (read requests
     by size, 128 x TCC_EA0_RDREQ_128B + 64 x ..._64B + 32 x ..._32B, plus
-    WRITE_SIZE; profiles/<kernel>_c1_bf16_pmc.txt) when present, else null.
+    WRITE_SIZE; profiles/<kernel>_c1_bf16_pmc.txt) when present, else null;
+    ``traffic_source`` names that file, the SHA-1 of the kernel source it
+    was measured on and whether the source built here is the same.
   * ``device``: CU count, architecture, the shader clock amd-smi reports while
     the step runs back to back, and how the settle phase ended.
   * ``cpu_baseline``: the CPU oracle (numpy restatement of the reference CPU
@@ -227,13 +229,34 @@ def _agg(recs, steps: int) -> dict:
     return {k: (sum(v) / len(v), len(v) // steps) for k, v in agg.items()}
 
 
+KERNEL_SOURCE = ROOT / "bdh-gpu-fast_amd" / "csrc" / "syrk.hip"
+
+
+def source_sha1(path: Path = KERNEL_SOURCE) -> str:
+    import hashlib
+
+    return hashlib.sha1(path.read_bytes()).hexdigest()
+
+
 def pmc_traffic(kernel: str, workload_tag: str):
-    """HBM bytes per launch of ``kernel`` from the committed rocprofv3 summary, or None."""
+    """HBM bytes per launch of ``kernel`` from the committed rocprofv3 summary
+    and where they come from: (bytes or None, source dict).  rocprofv3's
+    counter runs profile a process of their own, so the figure is the
+    committed one; the summary records the SHA-1 of the kernel source it was
+    measured on, and the source dict says whether that is the source built
+    here (``matches_current_source``)."""
     path = ROOT / "profiles" / f"{kernel}_{workload_tag}_pmc.txt"
     if not path.exists():
-        return None
-    m = re.search(r"hbm_bytes_per_launch\s*[:=]\s*([0-9.eE+]+)", path.read_text())
-    return float(m.group(1)) if m else None
+        return None, None
+    text = path.read_text()
+    m = re.search(r"hbm_bytes_per_launch\s*[:=]\s*([0-9.eE+]+)", text)
+    h = re.search(r"kernel_source_sha1\s*[:=]\s*([0-9a-f]{40})", text)
+    src = {
+        "file": str(path.relative_to(ROOT)),
+        "kernel_source_sha1": h.group(1) if h else None,
+        "matches_current_source": bool(h) and h.group(1) == source_sha1(),
+    }
+    return (float(m.group(1)) if m else None), src
 
 
 def cpu_baseline(reps: int = 3) -> dict:
@@ -403,7 +426,7 @@ def main() -> int:
         "--pmc-targets",
         action="store_true",
         help="run only the profiled kernels a few times each (for rocprofv3 counter passes): the C1 fused "
-        "forward, the C4 training op, one C2 layer's gated GEMM, one C2 layer's RoPE attention backward "
+        "forward in bf16 and in fp32, the C5 attention op, the C4 training op, one C2 layer's gated GEMM, one C2 layer's RoPE attention backward "
         "on both routes (recomputed tiles; kept tiles, as the training step runs it), the C3 decode step at "
         "S=511, and the calibration multiply",
     )
@@ -492,7 +515,7 @@ def main() -> int:
     # the score tiles R R^T over the strict lower triangle: B*nh*N*T*(T-1) flops
     F_scores = float(B * nh * N * T * (T - 1))
     achieved = F_scores / (k_ms * 1e-3) / 1e12
-    traffic = pmc_traffic(kname, "c1_bf16")
+    traffic, traffic_src = pmc_traffic(kname, "c1_bf16")
     roofline = {
         "bound": "mfma",
         "kernel": kname,
@@ -501,6 +524,7 @@ def main() -> int:
         "unit": "TFLOP/s",
         "frac": achieved / PEAK_BF16_TFLOPS,
         "traffic": traffic,
+        "traffic_source": traffic_src,
         "kernel_us": k_ms * 1e3,
         "ms_per_step_observed": ms_obs,
         "kernels_us": {k: round(v[0] * 1e3, 2) for k, v in means.items()},
@@ -844,7 +868,23 @@ def run_pmc_targets(torch, ext, kernels, dev, reps: int = 3) -> None:
     f = kernels.get_freqs(N).to(dev)
     for _ in range(reps):
         kernels.bdh_attn_rope(x, v, f, 0, impl="hip")
+    section_end()
+    # C1 as BASELINE.json states it, fp32 operands (the generic MFMA kernels
+    # k_scores, k_score_v)
+    x32, v32 = x.float(), v.float()
     del x, v
+    for _ in range(reps):
+        kernels.bdh_attn_rope(x32, v32, f, 0, impl="hip")
+    del x32, v32
+    section_end()
+    # C5 attention op (B=4 nh=8 T=2048 N=8192 D=512, fused RoPE, one split)
+    N5 = C5["mult"] * C5["D"] // C5["nh"]
+    x5 = torch.relu(0.32 * torch.randn(C5["B"], C5["nh"], C5["T"], N5, generator=g, device=dev)).to(bf)
+    v5 = torch.randn(C5["B"], 1, C5["T"], C5["D"], generator=g, device=dev).to(bf)
+    f5 = kernels.get_freqs(N5).to(dev)
+    for _ in range(reps):
+        kernels.bdh_attn_rope(x5, v5, f5, 0, impl="hip")
+    del x5, v5
     section_end()
     # C4 training op (k_sy_scores, k_dv_sy, G, k_dq_sy)
     B4, n4, T4, N4, D4 = (C4[k] for k in ("B", "nh", "T", "N", "D"))
