@@ -58,6 +58,7 @@ def check_scores(B, nh, T, N, strides, numel):
     S, ntl = p["nsplit"], p["ntl"]
     grid = 8 * ((nslab + 7) // 8) * p["ips"]
     seen = set()
+    chunks_seen = {}
     for bid in range(grid):
         xcd, kk = bid & 7, bid >> 3
         grp = kk // p["ips"]
@@ -80,11 +81,17 @@ def check_scores(B, nh, T, N, strides, numel):
             seen.add(key)
         # x loads: rows min(tile * 256 + r, T - 1) of both row blocks; stage
         # columns kofs(s) + 8 c + [0, 8) for stages s < 2 nch (later stages
-        # re-load the last one)
-        nch = (p["nchunk"] - split + S - 1) // S
-        last = split + S * (nch - 1)
-        assert 0 <= last < p["nchunk"]
-        max_col = last * 64 + 32 + 8 * 3 + 8
+        # re-load the last one).  Split `split` owns the contiguous chunk range
+        # [kc0, kc0 + nch) and walks it from chunk krs (set by the slab's group
+        # on its XCD): every chunk of the range once per k16 half.
+        kc0 = split * p["nchunk"] // S
+        nch = (split + 1) * p["nchunk"] // S - kc0
+        assert nch >= 1
+        krs = ((slab >> 3) * max(1, nch >> 2)) % nch
+        cols = [(kc0 + ((s >> 1) + krs) % nch) * 64 + (s & 1) * 32 for s in range(2 * nch)]
+        assert sorted(cols) == [kc0 * 64 + 32 * i for i in range(2 * nch)]
+        chunks_seen.setdefault((slab, kind), set()).update((c // 64, split) for c in cols)
+        max_col = max(cols) + 8 * 3 + 8
         assert max_col <= N
         b, h = divmod(slab, nh)
         max_row = min(max(ta, tb) * TILE + TILE - 1, T - 1)
@@ -96,6 +103,9 @@ def check_scores(B, nh, T, N, strides, numel):
             top = ((slab * ntl + t) * S + split) * TILE_ELEMS + (nws - 1) * nm * 1024 + (nm - 1) * 1024 + 512 + 63 * 8 + 8
             assert top <= (slab * ntl + t + 1) * S * TILE_ELEMS
     assert len(seen) == nslab * ntl * S
+    # the splits of one slab cover every k chunk, each with exactly one split
+    for (slab, kind), cs in chunks_seen.items():
+        assert sorted(c for c, _ in cs) == list(range(p["nchunk"])), (slab, kind)
     return p
 
 
