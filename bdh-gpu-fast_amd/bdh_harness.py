@@ -167,6 +167,17 @@ def _gated_product(x_bthn: torch.Tensor, y_ln: torch.Tensor, w: torch.Tensor, wt
     return kernels.relu_mul(x_bthn, y.view(nh, B, T, N).permute(1, 2, 0, 3))
 
 
+def _chains_decoder(x_bthn: torch.Tensor, y_ln: torch.Tensor, dec: torch.Tensor) -> bool:
+    """Whether ``kernels.gated_decoder`` takes the layer's gated product and
+    decoder: bf16 operands, n_embd = 256 (its K and D), N a multiple of 32,
+    more than 256 tokens (a decode step keeps the split-K decoder), one
+    head's rows of encoder_v and of the decoder under 4 GiB."""
+    B, T, nh, N = x_bthn.shape
+    D = y_ln.size(-1)
+    return (x_bthn.dtype == torch.bfloat16 and y_ln.dtype == torch.bfloat16 and dec.dtype == torch.bfloat16
+            and D == 256 and dec.size(1) == 256 and N % 32 == 0 and B * T > 256 and N * D * 2 < 2**32)
+
+
 def _follows(past: torch.Tensor, new: torch.Tensor) -> Optional[torch.Tensor]:
     """past||new as one view when ``new`` is the rows right after ``past`` in the
     same buffer (the reserved slot after the committed rows), else None."""
@@ -315,12 +326,17 @@ class BDH(nn.Module):
             x_sparse = x_bthn.permute(0, 2, 1, 3)  # (B, nh, T, N) view
             y_kv = self._attention(level, x_sparse, x.unsqueeze(1), rope_start, cache, impl, cos_sin)
             if fast:
-                xy = _gated_product(x_bthn, _ln_fast(y_kv, dt=_compute_dtype(x_bthn)), self.encoder_v, prep["encv_t"])
-                if B * T <= 256 and xy.dtype == torch.bfloat16:
-                    # few rows (decode): split-K GEMM instead of a few tiles down K = nh*N
-                    y_mlp = kernels.small_gemm(xy.view(B * T, nh * N), prep["dec"]).view(B, T, -1)
+                y_ln = _ln_fast(y_kv, dt=_compute_dtype(x_bthn))
+                if _chains_decoder(x_bthn, y_ln, prep["dec"]):
+                    # the gated product chained into the decoder: xy never stored
+                    y_mlp = kernels.gated_decoder(y_ln.contiguous(), prep["encv_t"], x_bthn, prep["dec"])
                 else:
-                    y_mlp = xy.view(B, T, nh * N) @ prep["dec"]
+                    xy = _gated_product(x_bthn, y_ln, self.encoder_v, prep["encv_t"])
+                    if B * T <= 256 and xy.dtype == torch.bfloat16:
+                        # few rows (decode): split-K GEMM instead of a few tiles down K = nh*N
+                        y_mlp = kernels.small_gemm(xy.view(B * T, nh * N), prep["dec"]).view(B, T, -1)
+                    else:
+                        y_mlp = xy.view(B, T, nh * N) @ prep["dec"]
             else:
                 xy = x_bthn * _encode_heads(_ln(y_kv), self.encoder_v)
                 y_mlp = xy.view(B, T, nh * N) @ self.decoder

@@ -49,6 +49,7 @@ __all__ = [
     "rope_rotate",
     "relu_mul",
     "gated_gemm",
+    "gated_decoder",
     "small_gemm",
     "layer_norm_rows",
     "profile_enable",
@@ -84,6 +85,8 @@ EXPORTED_SYMBOLS = (
     "bdh_tril_rope_score_v_bwd_saved",
     "bdh_relu_mul",
     "bdh_gated_gemm",
+    "bdh_gated_decoder_workspace",
+    "bdh_gated_decoder",
     "bdh_small_gemm_workspace",
     "bdh_small_gemm",
     "bdh_layer_norm_rows",
@@ -148,6 +151,8 @@ def _load():
         "bdh_relu_mul": (ctypes.c_int, [P, P, P, vp]),
         "bdh_layer_norm_rows": (ctypes.c_int, [P, P, P, vp]),
         "bdh_gated_gemm": (ctypes.c_int, [P, P, P, P, vp]),
+        "bdh_gated_decoder_workspace": (sz, [i64, i64]),
+        "bdh_gated_decoder": (ctypes.c_int, [P, P, P, P, P, vp, sz, vp]),
         "bdh_small_gemm_workspace": (sz, [i64, i64, i64]),
         "bdh_small_gemm": (ctypes.c_int, [P, P, P, vp, sz, vp]),
         "bdh_profile_enable": (None, [i32]),
@@ -655,6 +660,27 @@ def gated_gemm(y: torch.Tensor, wt: torch.Tensor, x: torch.Tensor, out: Optional
         rc = _lib.bdh_gated_gemm(ctypes.byref(_t4(y)), ctypes.byref(_t4(wt.unsqueeze(0))), ctypes.byref(_t4(x)),
                                  ctypes.byref(_t4(out)), _stream(dev))
     _check(rc, "gated_gemm")
+    return out
+
+
+def gated_decoder(y: torch.Tensor, wt: torch.Tensor, x: torch.Tensor, dec: torch.Tensor,
+                  out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
+    """``(x * relu(y @ wt^T)).view(B, T, nh*N) @ dec`` in one pass, bf16 operands:
+    y (B, nh, T, K), wt (nh, N, K), x (B, T, nh, N), dec (nh*N, D) -> (B, T, D) in
+    ``out_dtype`` (default fp32).  K = D = 256, N a multiple of 32."""
+    dev = _require_device(y, wt, x, dec)
+    if wt.dim() != 3 or dec.dim() != 2 or x.dim() != 4:
+        raise ValueError(f"gated_decoder: wt (nh, N, K), dec (nh*N, D), x (B, T, nh, N); got "
+                         f"{tuple(wt.shape)}, {tuple(dec.shape)}, {tuple(x.shape)}")
+    B, T, nh, N = x.shape
+    out = torch.empty(B, T, dec.size(1), dtype=out_dtype or torch.float32, device=dev)
+    with torch.cuda.device(dev):
+        ws, nb = _workspace(_lib.bdh_gated_decoder_workspace(nh, B * T), dev)
+        rc = _lib.bdh_gated_decoder(ctypes.byref(_t4(y)), ctypes.byref(_t4(wt.unsqueeze(0))), ctypes.byref(_t4(x)),
+                                    ctypes.byref(_t4(dec.view(1, 1, *dec.shape))),
+                                    ctypes.byref(_t4(out.view(B, T, 1, -1))),
+                                    ws.data_ptr() if ws is not None else None, nb, _stream(dev))
+    _check(rc, "gated_decoder")
     return out
 
 

@@ -68,6 +68,7 @@ from .cuda_attn import (
 from .hip_attn import (
     has_hip_ext,
     gated_gemm,
+    gated_decoder,
     has_hip_kernel,
     layer_norm_rows,
     relu_mul,
@@ -107,6 +108,7 @@ __all__ = [
     "tril_score_v_past",
     "relu_mul",
     "gated_gemm",
+    "gated_decoder",
     "small_gemm",
     "layer_norm_rows",
     "tril_rope_score_v",

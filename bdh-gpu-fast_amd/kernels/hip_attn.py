@@ -140,6 +140,14 @@ def gated_gemm(y: torch.Tensor, wt: torch.Tensor, x: torch.Tensor) -> torch.Tens
     return ext.gated_gemm(y, wt, x)
 
 
+def gated_decoder(y: torch.Tensor, wt: torch.Tensor, x: torch.Tensor, dec: torch.Tensor,
+                  out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
+    """``(x * relu(y @ wt^T)) @ decoder`` in one pass on the GPU (bdh.py:914-945), the
+    product never stored; fp32 output unless ``out_dtype`` says otherwise."""
+    ext = _require(y, wt, x, dec)
+    return ext.gated_decoder(y, wt, x, dec, out_dtype)
+
+
 def layer_norm_rows(y: torch.Tensor, x: Optional[torch.Tensor] = None,
                     out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
     """``LN(y)`` or ``LN(x + LN(y))`` over the last dim on the GPU (bdh.py:565-574, 731-750)."""
@@ -265,6 +273,7 @@ __all__ = [
     "tril_score_v_past",
     "relu_mul",
     "gated_gemm",
+    "gated_decoder",
     "small_gemm",
     "tril_rope_score_v",
     "tril_decode",

@@ -78,6 +78,8 @@ C5 = dict(n_layer=8, D=512, nh=8, mult=128, B=4, T=2048)
 C3_GEN = dict(n_layer=6, D=256, nh=4, mult=128, B=64, prompt=256, new=256, top_k=3, seed=5)
 CALIB_BYTES = 1 << 29  # reference elementwise pass that scales the HBM byte counters
 MARK_ELEMS = 1 << 16  # the section marker multiply of --pmc-targets (a grid no other target has)
+# the library kernels of the layer's gated product (alone, or chained into the decoder)
+GATED_KERNELS = ("k_gated_gemm", "k_relu_mul", "k_gated_dec", "k_head_sum")
 
 
 def log(msg: str) -> None:
@@ -778,7 +780,7 @@ def run_models(torch, ext, dev, only=None) -> dict:
             fwd_hip()
         rec = ext.profile_collect()
         ext.profile_enable(False)
-        mlp = ("k_gated_gemm", "k_relu_mul")
+        mlp = GATED_KERNELS
         leg["hip"]["attention_kernels_ms"] = sum(t for n, t in rec if n not in mlp)
         leg["hip"]["gated_product_kernels_ms"] = sum(t for n, t in rec if n in mlp)
         out[name] = leg
@@ -896,15 +898,19 @@ def run_pmc_targets(torch, ext, kernels, dev, reps: int = 3) -> None:
         ext.tril_score_v_bwd_saved(q4, v4, d4, sc)
     del q4, v4, d4, sc
     section_end()
-    # one C2 layer's gated product (k_gated_gemm): y (B, nh, T, D), encoder_v^T (nh, N, D), x (B, T, nh, N)
+    # one C2 layer's gated product (k_gated_gemm): y (B, nh, T, D), encoder_v^T (nh, N, D), x (B, T, nh, N);
+    # then the same product chained into the decoder (k_gated_dec, k_head_sum), dec (nh*N, D)
     c = C2
     N2 = c["mult"] * c["D"] // c["nh"]
     y = torch.randn(c["B"], c["nh"], c["T"], c["D"], generator=g, device=dev).to(bf)
     wt = (0.02 * torch.randn(c["nh"], N2, c["D"], generator=g, device=dev)).to(bf)
     xb = torch.relu(torch.randn(c["B"], c["T"], c["nh"], N2, generator=g, device=dev)).to(bf)
+    dec = (0.02 * torch.randn(c["nh"] * N2, c["D"], generator=g, device=dev)).to(bf)
     for _ in range(reps):
         kernels.gated_gemm(y, wt, xb)
-    del y, wt, xb
+    for _ in range(reps):
+        kernels.gated_decoder(y, wt, xb, dec)
+    del y, wt, xb, dec
     section_end()
     # one C2 layer's fused RoPE attention backward, bf16, x_sparse as the
     # model's permuted (B, T, nh, N) view: the route that recomputes the score
@@ -968,7 +974,7 @@ def run_train_step(torch, ext, dev, build) -> dict:
     step()
     rec = ext.profile_collect()
     ext.profile_enable(False)
-    leg["attention_kernels_ms"] = sum(t for n, t in rec if n not in ("k_gated_gemm", "k_relu_mul"))
+    leg["attention_kernels_ms"] = sum(t for n, t in rec if n not in GATED_KERNELS)
     log(f"[bench] c2_train_step: {ms:.1f} ms, {leg['tok_s']:.0f} tok/s (attention kernels {leg['attention_kernels_ms']:.2f} ms)")
     del m, opt
     torch.cuda.empty_cache()

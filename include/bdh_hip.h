@@ -270,6 +270,27 @@ int bdh_gated_gemm(const bdh_tensor4* y, const bdh_tensor4* wt, const bdh_tensor
                    const bdh_tensor4* out, bdh_stream stream);
 
 /*
+ * The gated product chained into the decoder product, bf16 operands, fp32
+ * accumulation:
+ *   out[b,t,0,:] = sum_h sum_n x[b,t,h,n] * max(sum_k y[b,h,t,k] * wt[0,h,n,k], 0)
+ *                  * dec[0,0,h*N+n,:]
+ * Replaces `_encoder_v_relu` (bdh.py:914-925) and the whole of _mlp_merge
+ * (bdh.py:927-945: `x_bthn * y_bthn`, then F.linear with the decoder) for the
+ * prefill; the product x * relu(...) never reaches memory.  y: (B, nh, T, K),
+ * the LayerNorm of the attention output; wt: (1, nh, N, K), encoder_v
+ * transposed; x: (B, T, nh, N); dec: (1, 1, nh*N, D), the decoder; out:
+ * (B, T, 1, D), bf16 or fp32, rows evenly spaced.  K = D = 256, N a multiple
+ * of 32, rows 16-byte aligned; one head's rows of wt and of dec span at most
+ * 4 GiB (else BDH_ERR_SHAPE).  Each product x * relu(...) is rounded to bf16
+ * once.  The workspace holds the heads' fp32 partial outputs (nh * B*T * D
+ * floats), summed in head order.
+ */
+size_t bdh_gated_decoder_workspace(int64_t nh, int64_t M);
+int bdh_gated_decoder(const bdh_tensor4* y, const bdh_tensor4* wt, const bdh_tensor4* x,
+                      const bdh_tensor4* dec, const bdh_tensor4* out, void* workspace,
+                      size_t workspace_bytes, bdh_stream stream);
+
+/*
  * Few-row GEMM with split K, bf16 operands, fp32 accumulation:
  *   out (1, 1, M, D) = a (1, 1, M, K) @ b (1, 1, K, D)
  * For the decoder product of a decode step (bdh.py:927-945, `_mlp_merge`'s
