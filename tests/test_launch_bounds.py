@@ -5,7 +5,8 @@ HIP legs run (csrc/syrk.hip: k_sy_scores work items, their x loads and
 partial-tile stores, k_sy_sv's partial, V and output accesses;
 csrc/decode.hip: k_decode_bf16's key, q and partial accesses; the training
 backward's k_dq_sy B loads on x and k_dv_sy; csrc/model.hip: k_gated_gemm's
-LDS-DMA operand loads and epilogue x loads) are restated here and evaluated over every
+LDS-DMA operand loads and epilogue x loads; csrc/gated_dec.hip: k_gated_dec's
+grid, operand DMA, LDS fragment reads and partial stores) are restated here and evaluated over every
 work item, with the strides of the views the harness passes (x_sparse as the
 permuted (B, T, nh, N) encoder output, the packed KV cache's
 capacity-strided past views).  Each access must fall inside its buffer and
@@ -313,3 +314,104 @@ def check_gated(B, T, nh, N, K):
                                        (3, 257, 3, 136, 64), (1, 1, 1, 8, 32)])
 def test_gated_gemm_launches_stay_in_bounds(B, T, nh, N, K):
     check_gated(B, T, nh, N, K)
+
+
+def check_gated_dec(B, T, nh, N):
+    """csrc/gated_dec.hip k_gated_dec + k_head_sum on the harness's contiguous operands y (B, nh, T,
+    256), wt (nh, N, 256), x (B, T, nh, N), dec (nh N, 256): the XCD-major grid covers each (head,
+    256-token block) once; the LDS-DMA sources of every chunk (encoder_v rows 2i + l / 32 chunk
+    (l % 32) ^ (row % 32); decoder rows 2 (i - 16) + l / 32 chunk (l % 32) ^ 4 (row % 4); x rows
+    16 (i - 32) + l / 4 chunk (l % 4) ^ ((row / 4) % 4), token clamped to M - 1) stay inside their
+    views with 32-bit offsets from the head's base; instruction i of a slot writes LDS bytes
+    [i KB + 16 l, +16) inside its 48 KB slot of the 3-slot ring; the fragment reads (encoder_v
+    row l % 32 chunk (2s + l / 32) ^ (l % 32); decoder transposing reads at 16 k2 + 4 (g4 / 2) +
+    q / 4 (+ 8) rows; x pieces) stay inside the region of the slot they read; the y loads, the
+    partial stores [h][m][256] (m < M) and k_head_sum's reads stay in bounds."""
+    K = D = MT = 256
+    NC, SLOT, RING = 32, 48 * 1024, 3
+    WV, DEC = NC * K * 2, NC * D * 2
+    M = B * T
+    ntb = (M + MT - 1) // MT
+    total = ntb * nh
+    per_xcd = (total + 7) // 8
+    seen = []
+    for bid in range(8 * per_xcd):
+        xcd, kk0 = bid & 7, bid >> 3
+        t = xcd * per_xcd + kk0
+        if t < total:
+            seen.append(divmod(t, ntb))
+    assert sorted(seen) == [(h, tb) for h in range(nh) for tb in range(ntb)]
+    assert RING * SLOT <= 160 * 1024
+    nck = N // NC
+    part_elems = nh * M * D
+    for h in {0, nh - 1}:
+        for tb in {0, ntb - 1}:
+            m0 = tb * MT
+            for w in range(4):
+                for lane in (0, 5, 31, 32, 47, 63):
+                    hl, l32 = lane >> 5, lane & 31
+                    for u in range(12):
+                        i = 4 * u + w
+                        for slot in range(RING):
+                            lds = slot * SLOT + u * 4096 + w * 1024 + 16 * lane
+                            assert slot * SLOT + i * 1024 <= lds and lds + 16 <= slot * SLOT + (i + 1) * 1024
+                            assert lds + 16 <= (slot + 1) * SLOT
+                        for ck in (0, nck - 1, nck, nck + 1):  # issue(ck + 2) past the end re-loads the last chunk
+                            cc = min(ck, nck - 1)
+                            if i < 16:
+                                r = 2 * i + hl
+                                c = l32 ^ (r & 31)
+                                assert 0 <= r < NC and 0 <= c < 32
+                                off = (cc * NC + r) * K + 8 * c  # from the head's base (wt + h N K)
+                                assert off * 2 < 2 ** 32 and h * N * K + off + 8 <= nh * N * K
+                            elif i < 32:
+                                r = 2 * (i - 16) + hl
+                                c = l32 ^ (4 * (r & 3))
+                                assert 0 <= c < 32
+                                off = (cc * NC + r) * D + 8 * c
+                                assert off * 2 < 2 ** 32 and h * N * D + off + 8 <= nh * N * D
+                            else:
+                                r = 16 * (i - 32) + (lane >> 2)
+                                c = (lane & 3) ^ ((r >> 2) & 3)
+                                assert 0 <= r < MT and 0 <= c < 4
+                                m = min(m0 + r, M - 1)
+                                b, tt = divmod(m, T)
+                                e = b * T * nh * N + tt * nh * N + h * N + 8 * c + cc * NC
+                                assert e + 8 <= B * T * nh * N and 8 * c + cc * NC + 8 <= N
+                    for j in range(2):
+                        m = min(m0 + 64 * w + 32 * j + l32, M - 1)
+                        b, tt = divmod(m, T)
+                        yo = b * nh * T * K + h * T * K + tt * K + 8 * hl
+                        assert yo + 16 * 15 + 8 <= B * nh * T * K
+                    for s in range(16):
+                        o = l32 * 512 + 16 * ((2 * s + hl) ^ l32)
+                        assert 0 <= o and o + 16 <= WV
+                    g4, q = lane >> 4, lane & 15
+                    drow = 4 * (g4 >> 1) + (q >> 2)
+                    for db in range(8):
+                        col = 32 * db + 16 * (g4 & 1) + 4 * (q & 3)
+                        o = WV + drow * 512 + (((col >> 3) ^ (4 * (drow & 3))) * 16) + ((col >> 2) & 1) * 8
+                        for k2 in range(2):
+                            for extra in (0, 8 * 512):
+                                p = o + k2 * 16 * 512 + extra
+                                assert WV <= p and p + 8 <= WV + DEC
+                    for j in range(2):
+                        r = 64 * w + 32 * j + l32
+                        for p in range(4):
+                            o = WV + DEC + r * 64 + 16 * (p ^ ((r >> 2) & 3)) + 8 * hl
+                            assert WV + DEC <= o and o + 8 <= SLOT
+                        for rr in range(16):
+                            m = m0 + 64 * w + 32 * j + 8 * (rr >> 2) + 4 * hl + (rr & 3)
+                            if m < M:
+                                for db in range(8):
+                                    assert (h * M + m) * D + 32 * db + l32 < part_elems
+    nthr = (M * D // 4 + 255) // 256
+    for e in {0, (nthr * 256 - 1) * 4, (M * D // 4 - 1) * 4}:
+        if e < M * D:
+            assert (nh - 1) * M * D + e + 4 <= part_elems
+
+
+@pytest.mark.parametrize("B,T,nh,N", [(32, 512, 4, 8192), (64, 256, 4, 8192), (2, 300, 2, 1024), (3, 129, 4, 96),
+                                      (1, 257, 1, 32)])
+def test_gated_decoder_launches_stay_in_bounds(B, T, nh, N):
+    check_gated_dec(B, T, nh, N)
