@@ -20,6 +20,7 @@ struct RopeArgs {
   int vec8;       // every view 16-byte aligned per 8 elements (k_rope8)
   int64_t BH;     // B * H
   int bcast;      // cos/sin do not vary over batch and heads (k_rope8_bc)
+  uint32_t nrr, ncb, total, per_xcd;  // k_rope8_bc work items: row runs x column blocks x T
 };
 
 template <typename TV, typename TC, typename TO>
@@ -87,15 +88,7 @@ __device__ __forceinline__ void store8(T* p, const Vec8<T>& r) {
     reinterpret_cast<u32x4*>(p)[1] = reinterpret_cast<const u32x4*>(r.e)[1];
   }
 }
-// Streaming forms (non-temporal: the rows are read and written once)
-template <typename T>
-__device__ __forceinline__ Vec8<T> load8_nt(const T* p) {
-  Vec8<T> r;
-  const u32x4* q = reinterpret_cast<const u32x4*>(p);
-  reinterpret_cast<u32x4*>(r.e)[0] = __builtin_nontemporal_load(q);
-  if constexpr (sizeof(T) == 4) reinterpret_cast<u32x4*>(r.e)[1] = __builtin_nontemporal_load(q + 1);
-  return r;
-}
+// Streaming store (non-temporal: the rows are written once)
 template <typename T>
 __device__ __forceinline__ void store8_nt(T* p, const Vec8<T>& r) {
   u32x4* q = reinterpret_cast<u32x4*>(p);
@@ -145,24 +138,30 @@ __global__ __launch_bounds__(256) void k_rope8(RopeArgs a) {
   store8(static_cast<TO*>(const_cast<void*>(a.o.p)) + b * a.o.s0 + h * a.o.s1 + t * a.o.s2 + e0, y);
 }
 
-// Tables broadcast over batch and heads (the model's case): grid
-// (ceil(B * H / 8), N / 2048, T); each thread loads its cos/sin once and
-// rotates its eight elements in a run of up to eight (b, h) rows, all eight
-// loads in flight, with non-temporal loads and stores.  So the tables are
-// read once per eight rows, and the grid spans the batch rows too (at C1:
-// 98.6 against 126 us with one workgroup per (column block, t) walking all
-// B * H rows, four in flight; a plain copy of x takes 89 us).  The row runs
-// that share a table entry are neighbours in the grid, so they run together
-// and the later ones find the entry in L2 (C1: 109.8 -> 106.2 us against
-// the same grid with the row runs slowest; 16 rows a run: 117 us).
-constexpr int kRopeRows = 8;  // (b, h) rows per workgroup of k_rope8_bc
+// Tables broadcast over batch and heads (the model's case): work items
+// (run of 16 (b, h) rows, column block of 2048, t); each thread loads its
+// cos/sin once and rotates its eight elements in each row of the run, all
+// sixteen loads in flight, non-temporal stores.  So the tables are read once
+// per sixteen rows, and the grid spans the batch rows too (at C1: 98.6
+// against 126 us with one workgroup per (column block, t) walking all B * H
+// rows, four in flight).  Work items go to XCDs in contiguous ranges
+// (workgroup i runs on XCD i % 8), so the row runs that share a table entry
+// run on one XCD and read it from one L2.  C1, one box, a plain copy of x
+// taking 98 us: 107.9-111.4 us with the runs of an entry on different XCDs,
+// 97.1-98.4 with them on one, 96.0-96.5 with 16 rows a run instead of 8
+// (32: 101.3); non-temporal loads of x cost 5 us more, plain stores 12 us.
+constexpr int kRopeRows = 16;  // (b, h) rows per workgroup of k_rope8_bc
 
 template <typename TV, typename TC, typename TO>
 __global__ __launch_bounds__(256) void k_rope8_bc(RopeArgs a) {
 #pragma clang fp contract(off)
-  const int64_t e0 = (int64_t(blockIdx.y) * 256 + threadIdx.x) * 8;
+  // 32-bit index arithmetic (the host checks the ranges): wave-uniform
+  // 64-bit divisions would cost far more than this kernel's own work
+  const uint32_t bid = blockIdx.x, L = (bid & 7) * a.per_xcd + (bid >> 3);
+  if ((bid >> 3) >= a.per_xcd || L >= a.total) return;
+  const uint32_t rr = L % a.nrr, q = L / a.nrr, cb = q % a.ncb, t = q / a.ncb;
+  const int64_t e0 = (int64_t(cb) * 256 + threadIdx.x) * 8;
   if (e0 >= a.N) return;
-  const int64_t t = blockIdx.z;
   const Vec8<TC> c = load8(static_cast<const TC*>(a.c.p) + t * a.c.s2 + e0);
   const Vec8<TC> sn = load8(static_cast<const TC*>(a.s.p) + t * a.s.s2 + e0);
   float cf[8], sf[8];
@@ -204,25 +203,34 @@ __global__ __launch_bounds__(256) void k_rope8_bc(RopeArgs a) {
   };
   const TV* vp = static_cast<const TV*>(a.v.p) + t * a.v.s2 + e0;
   TO* op = static_cast<TO*>(const_cast<void*>(a.o.p)) + t * a.o.s2 + e0;
-  const int64_t bh0 = int64_t(blockIdx.x) * kRopeRows;
-  const int64_t bh1 = bh0 + kRopeRows < a.BH ? bh0 + kRopeRows : a.BH;
-  if (bh1 - bh0 == kRopeRows) {
+  const uint32_t H = uint32_t(a.H), BH = uint32_t(a.BH), bh0 = rr * kRopeRows;
+  const uint32_t nrow = bh0 + kRopeRows < BH ? kRopeRows : BH - bh0;
+  // row bh0 + u is (b, h) = ((bh0 + u) / H, (bh0 + u) % H), stepped from (b0, h0)
+  uint32_t b = bh0 / H, h = bh0 - (bh0 / H) * H;
+  if (nrow == kRopeRows) {
+    int64_t vo[kRopeRows], oo[kRopeRows];
+#pragma unroll
+    for (int u = 0; u < kRopeRows; ++u) {
+      vo[u] = b * a.v.s0 + h * a.v.s1;
+      oo[u] = b * a.o.s0 + h * a.o.s1;
+      if (++h == H) {
+        h = 0;
+        ++b;
+      }
+    }
     Vec8<TV> x[kRopeRows];
 #pragma unroll
-    for (int u = 0; u < kRopeRows; ++u) {
-      const int64_t r = bh0 + u, h = r % a.H, b = r / a.H;
-      x[u] = load8_nt(vp + b * a.v.s0 + h * a.v.s1);
-    }
+    for (int u = 0; u < kRopeRows; ++u) x[u] = load8(vp + vo[u]);
 #pragma unroll
-    for (int u = 0; u < kRopeRows; ++u) {
-      const int64_t r = bh0 + u, h = r % a.H, b = r / a.H;
-      store8_nt(op + b * a.o.s0 + h * a.o.s1, rot(x[u]));
-    }
+    for (int u = 0; u < kRopeRows; ++u) store8_nt(op + oo[u], rot(x[u]));
     return;
   }
-  for (int64_t bh = bh0; bh < bh1; ++bh) {
-    const int64_t h = bh % a.H, b = bh / a.H;
-    store8_nt(op + b * a.o.s0 + h * a.o.s1, rot(load8_nt(vp + b * a.v.s0 + h * a.v.s1)));
+  for (uint32_t u = 0; u < nrow; ++u) {
+    store8_nt(op + b * a.o.s0 + h * a.o.s1, rot(load8(vp + b * a.v.s0 + h * a.v.s1)));
+    if (++h == H) {
+      h = 0;
+      ++b;
+    }
   }
 }
 
@@ -236,13 +244,21 @@ static bool vec8_ok(const bdh_tensor4* t) {
 
 template <typename TV, typename TC, typename TO>
 static int launch_rope(const RopeArgs& a, hipStream_t s) {
-  // The broadcast kernel has (N / 2048) x T workgroups: at short T (a decode
-  // step: 4 at N = 8192) that leaves the chip idle, so few time steps take the
-  // per-row kernel, whose grid also spans B * H.
+  // The broadcast kernel gains from its table reuse when there are many time
+  // steps; at short T (a decode step: 4 column blocks at N = 8192) its few
+  // workgroups leave the chip idle, so few time steps take the per-row kernel,
+  // one workgroup per (column block, t, row).
   const int64_t bc_wgs = (a.N + 2047) / 2048 * a.T;
   if (a.vec8 && a.bcast && bc_wgs >= 512) {
-    dim3 grid((unsigned)((a.BH + kRopeRows - 1) / kRopeRows), (unsigned)((a.N + 2047) / 2048), (unsigned)a.T);
-    BDH_LAUNCH("k_rope", (k_rope8_bc<TV, TC, TO>), grid, dim3(256), 0, s, a);
+    const int64_t nrr = (a.BH + kRopeRows - 1) / kRopeRows, ncb = (a.N + 2047) / 2048;
+    const int64_t total = nrr * ncb * a.T, per_xcd = (total + 7) / 8;
+    if (8 * per_xcd >= (int64_t(1) << 31)) return BDH_ERR_SHAPE;
+    RopeArgs b = a;
+    b.nrr = uint32_t(nrr);
+    b.ncb = uint32_t(ncb);
+    b.total = uint32_t(total);
+    b.per_xcd = uint32_t(per_xcd);
+    BDH_LAUNCH("k_rope", (k_rope8_bc<TV, TC, TO>), dim3(unsigned(8 * per_xcd)), dim3(256), 0, s, b);
     return BDH_OK;
   }
   if (a.vec8) {

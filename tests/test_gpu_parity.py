@@ -219,6 +219,28 @@ def test_rope_apply_paths_are_bit_exact(layout, vdt):
     assert np.array_equal(np_of(got), as_dtype_values(want, vdt))
 
 
+@pytest.mark.parametrize("permuted", [False, True])
+@pytest.mark.parametrize("backward", [False, True])
+@pytest.mark.parametrize("vdt", [torch.float32, torch.bfloat16])
+def test_rope_apply_broadcast_kernel_is_bit_exact(vdt, backward, permuted):
+    """The broadcast-table kernel (many time steps, tables shared by every
+    (b, h) row): B*H = 40 rows (two full runs of 16 and one of 8), N = 2560
+    (a last column block of 512), T = 256, contiguous and as the permuted
+    x_sparse view."""
+    B, H, T, N = 5, 8, 256, 2560
+    c, s = O.rope_cos_sin(T, 3, O.get_freqs(N))
+    x = as_dtype_values(normal((B, T, H, N) if permuted else (B, H, T, N), 9), vdt)
+    xv = np.ascontiguousarray(x.transpose(0, 2, 1, 3)) if permuted else x
+    fn = O.rope_rotate_backward if backward else O.rope_rotate
+    want = fn(xv, c.reshape(1, 1, T, N), s.reshape(1, 1, T, N), bf16=(vdt == torch.bfloat16))
+    xd = to_dev(x, vdt)
+    xd = xd.permute(0, 2, 1, 3) if permuted else xd
+    cd = torch.from_numpy(c).to(DEV).view(1, 1, T, N).expand(B, H, T, N)
+    sd = torch.from_numpy(s).to(DEV).view(1, 1, T, N).expand(B, H, T, N)
+    got = ext.rope_rotate(xd, cd, sd, backward=backward)
+    assert np.array_equal(np_of(got), as_dtype_values(want, vdt))
+
+
 # ---------------------------------------------------------------- backward
 BWD_SHAPES = [(1, 1, 5, 4, 3, 1), (2, 3, 70, 24, 16, 1), (1, 2, 200, 136, 72, 2), (1, 2, 300, 512, 256, 1)]
 
