@@ -146,6 +146,21 @@ def _encode_relu_epilogue(x: torch.Tensor, wc: torch.Tensor, zero: torch.Tensor,
     return out.view(*x.shape[:-1], nh, wc.size(1) // nh)
 
 
+def _encode_fast(x: torch.Tensor, prep: dict, nh: int) -> torch.Tensor:
+    """The encoder and its ReLU on the HIP forward: the library's streaming kernel
+    (``kernels.relu_gemm``, one workgroup per head and 256 tokens) for bf16 with
+    n_embd 256 or 512 when there are enough token blocks to fill the chip,
+    hipBLASLt's ReLU-epilogue GEMM otherwise (decode steps, short prompts)."""
+    B, T, D = x.shape
+    wt = prep["enc_t"]
+    N = wt.size(1)
+    if (wt.dtype == torch.bfloat16 and ((D == 256 and N % 64 == 0) or (D == 512 and N % 32 == 0))
+            and (B * T + 255) // 256 * nh >= 128):
+        xb = x.to(wt.dtype).contiguous()
+        return kernels.relu_gemm(xb.unsqueeze(1).expand(B, nh, T, D), wt)
+    return _encode_relu_epilogue(x, prep["enc"], prep["zero"], nh)
+
+
 def _gated_product(x_bthn: torch.Tensor, y_ln: torch.Tensor, w: torch.Tensor, wt=None) -> torch.Tensor:
     """x_bthn * relu(encoder_v GEMM), token-major (B, T, nh, N).
 
@@ -208,7 +223,8 @@ class BDH(nn.Module):
 
     def _prepared(self, dt: torch.dtype):
         """Inference layouts of the weights in the compute dtype, rebuilt when a weight changes:
-        encoder as (D, nh*N) with a zero bias (ReLU-epilogue GEMM), encoder_v transposed to
+        encoder as (D, nh*N) with a zero bias (ReLU-epilogue GEMM) and transposed to (nh, N, D)
+        (streaming encoder kernel), encoder_v transposed to
         (nh, N, D) (gated GEMM), decoder (nh*N, D)."""
         key = tuple((p.data_ptr(), p._version) for p in (self.encoder, self.encoder_v, self.decoder))
         hit = self._wcache.get(dt)
@@ -218,6 +234,7 @@ class BDH(nn.Module):
         with torch.no_grad():
             prep = {
                 "enc": self.encoder.permute(1, 0, 2).reshape(D, nh * N).to(dt).contiguous(),
+                "enc_t": self.encoder.transpose(1, 2).to(dt).contiguous(),
                 "zero": torch.zeros(nh * N, dtype=dt, device=self.encoder.device),
                 "encv_t": self.encoder_v.transpose(1, 2).to(dt).contiguous(),
                 "dec": self.decoder.to(dt).contiguous(),
@@ -320,7 +337,7 @@ class BDH(nn.Module):
         prep = self._prepared(_compute_dtype(x)) if fast else None
         for level in range(cfg.n_layer):
             if fast:
-                x_bthn = _encode_relu_epilogue(x, prep["enc"], prep["zero"], nh)
+                x_bthn = _encode_fast(x, prep, nh)
             else:
                 x_bthn = _encode(x, self.encoder)
             x_sparse = x_bthn.permute(0, 2, 1, 3)  # (B, nh, T, N) view

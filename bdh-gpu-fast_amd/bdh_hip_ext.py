@@ -49,6 +49,7 @@ __all__ = [
     "rope_rotate",
     "relu_mul",
     "gated_gemm",
+    "relu_gemm",
     "gated_decoder",
     "small_gemm",
     "layer_norm_rows",
@@ -85,6 +86,7 @@ EXPORTED_SYMBOLS = (
     "bdh_tril_rope_score_v_bwd_saved",
     "bdh_relu_mul",
     "bdh_gated_gemm",
+    "bdh_relu_gemm",
     "bdh_gated_decoder_workspace",
     "bdh_gated_decoder",
     "bdh_small_gemm_workspace",
@@ -151,6 +153,7 @@ def _load():
         "bdh_relu_mul": (ctypes.c_int, [P, P, P, vp]),
         "bdh_layer_norm_rows": (ctypes.c_int, [P, P, P, vp]),
         "bdh_gated_gemm": (ctypes.c_int, [P, P, P, P, vp]),
+        "bdh_relu_gemm": (ctypes.c_int, [P, P, P, vp]),
         "bdh_gated_decoder_workspace": (sz, [i64, i64]),
         "bdh_gated_decoder": (ctypes.c_int, [P, P, P, P, P, vp, sz, vp]),
         "bdh_small_gemm_workspace": (sz, [i64, i64, i64]),
@@ -660,6 +663,22 @@ def gated_gemm(y: torch.Tensor, wt: torch.Tensor, x: torch.Tensor, out: Optional
         rc = _lib.bdh_gated_gemm(ctypes.byref(_t4(y)), ctypes.byref(_t4(wt.unsqueeze(0))), ctypes.byref(_t4(x)),
                                  ctypes.byref(_t4(out)), _stream(dev))
     _check(rc, "gated_gemm")
+    return out
+
+
+def relu_gemm(y: torch.Tensor, wt: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """``relu(y @ wt^T)`` per head, bf16: y (B, nh, T, K) (head stride 0 when the
+    heads share it), wt (nh, N, K) -> (B, T, nh, N)."""
+    dev = _require_device(y, wt, out)
+    if wt.dim() != 3 or y.dim() != 4:
+        raise ValueError(f"relu_gemm: y (B, nh, T, K) and wt (nh, N, K), got {tuple(y.shape)}, {tuple(wt.shape)}")
+    B, nh, T, _ = y.shape
+    if out is None:
+        out = torch.empty(B, T, nh, wt.size(1), dtype=y.dtype, device=dev)
+    with torch.cuda.device(dev):
+        rc = _lib.bdh_relu_gemm(ctypes.byref(_t4(y)), ctypes.byref(_t4(wt.unsqueeze(0))), ctypes.byref(_t4(out)),
+                                _stream(dev))
+    _check(rc, "relu_gemm")
     return out
 
 

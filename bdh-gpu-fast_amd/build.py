@@ -21,7 +21,7 @@ ROOT = HERE.parent
 CSRC = HERE / "csrc"
 BUILD = HERE / "_build"
 LIB = HERE / "libbdh_hip.so"
-SOURCES = ["api.hip", "fwd.hip", "syrk.hip", "bwd.hip", "decode.hip", "rope.hip", "model.hip", "gated_dec.hip"]
+SOURCES = ["api.hip", "fwd.hip", "syrk.hip", "bwd.hip", "decode.hip", "rope.hip", "model.hip", "gated_dec.hip", "enc.hip"]
 ARCH = os.environ.get("BDH_OFFLOAD_ARCH", "gfx950")
 
 

@@ -122,6 +122,7 @@ __device__ __forceinline__ f32x16 mma_bf16(bf16x8 a, bf16x8 b, f32x16 c) {
 }
 __device__ __forceinline__ int g_sw(int row, int c) { return row * 64 + ((c ^ ((row >> 2) & 3)) * 16); }
 
+template <bool kMul>
 __global__ __launch_bounds__(512, 2) void k_gated_gemm(const GatedArgs a) {
   __shared__ __attribute__((aligned(1024))) uint8_t g_lds[kGLds];
   const int bid = blockIdx.x, xcd = bid & 7, kk = bid >> 3;
@@ -202,9 +203,11 @@ __global__ __launch_bounds__(512, 2) void k_gated_gemm(const GatedArgs a) {
     if (s + 2 < nst) issue(s + 2);
     // the epilogue's x chunks go out with the last stage, so their latency
     // runs under its MFMAs
-    if (s == nst - 1) {
+    if constexpr (kMul) {
+      if (s == nst - 1) {
 #pragma unroll
-      for (int e = 0; e < kEp; ++e) load_x(e);
+        for (int e = 0; e < kEp; ++e) load_x(e);
+      }
     }
     const uint8_t* base = g_lds + (s % kGRing) * kGStage;
 #pragma unroll
@@ -245,6 +248,19 @@ __global__ __launch_bounds__(512, 2) void k_gated_gemm(const GatedArgs a) {
         *reinterpret_cast<bf16_t*>(g_lds + row * kGOutRow + col * 2) = f2bf(relu_f(acc[i][c][r]));
       }
   __syncthreads();
+  if constexpr (!kMul) {
+#pragma unroll
+    for (int e = 0; e < kEp; ++e) {
+      const int row = (tid >> 4) + 32 * e;
+      const int m = m0 + row;
+      const uint4 v = *reinterpret_cast<const uint4*>(g_lds + row * kGOutRow + cc * 16);
+      if (m < a.M && n < a.N) {
+        const int b = m / a.T, tt = m - b * a.T;
+        *reinterpret_cast<uint4*>(a.o + b * a.o0 + tt * a.o1 + h * a.o2 + n) = v;
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int e = 0; e < kEp; ++e) {
     const int row = (tid >> 4) + 32 * e;
@@ -581,21 +597,29 @@ extern "C" int bdh_relu_mul(const bdh_tensor4* x, const bdh_tensor4* y, const bd
             : launch_relu_mul<float, float>(a, out->dtype, grid, s);
 }
 
-// out = x * relu(y @ wt^T) per head; see k_gated_gemm.
-extern "C" int bdh_gated_gemm(const bdh_tensor4* y, const bdh_tensor4* wt, const bdh_tensor4* x,
-                              const bdh_tensor4* out, bdh_stream stream) {
+namespace bdh {
+bool relu_enc_takes(int64_t K, int64_t N);
+int relu_enc_launch(const bdh_tensor4* y, const bdh_tensor4* wt, const bdh_tensor4* out, hipStream_t s);
+}  // namespace bdh
+
+// out = [x *] relu(y @ wt^T) per head (x null: the ReLU GEMM alone, k_relu_enc
+// where it takes the shape); see k_gated_gemm.
+static int gated_gemm_launch(const bdh_tensor4* y, const bdh_tensor4* wt, const bdh_tensor4* x,
+                             const bdh_tensor4* out, bdh_stream stream) {
   BDH_TRY(check_view(y));
   BDH_TRY(check_view(wt));
-  BDH_TRY(check_view(x));
+  if (x != nullptr) BDH_TRY(check_view(x));
   BDH_TRY(check_view(out));
-  const int64_t B = x->size[0], T = x->size[1], H = x->size[2], N = x->size[3], K = y->size[3];
-  if (y->dtype != BDH_BF16 || wt->dtype != BDH_BF16 || x->dtype != BDH_BF16 || out->dtype != BDH_BF16)
-    return BDH_ERR_DTYPE;
+  const int64_t B = out->size[0], T = out->size[1], H = out->size[2], N = out->size[3], K = y->size[3];
+  if (y->dtype != BDH_BF16 || wt->dtype != BDH_BF16 || out->dtype != BDH_BF16) return BDH_ERR_DTYPE;
+  if (x != nullptr && x->dtype != BDH_BF16) return BDH_ERR_DTYPE;
   if (y->size[0] != B || y->size[1] != H || y->size[2] != T) return BDH_ERR_SHAPE;
   if (wt->size[0] != 1 || wt->size[1] != H || wt->size[2] != N || wt->size[3] != K) return BDH_ERR_SHAPE;
-  for (int i = 0; i < 4; ++i)
-    if (out->size[i] != x->size[i]) return BDH_ERR_SHAPE;
-  if (views_overlap(out, x) || views_overlap(out, y) || views_overlap(out, wt)) return BDH_ERR_ALIAS;
+  if (x != nullptr)
+    for (int i = 0; i < 4; ++i)
+      if (out->size[i] != x->size[i]) return BDH_ERR_SHAPE;
+  if ((x != nullptr && views_overlap(out, x)) || views_overlap(out, y) || views_overlap(out, wt))
+    return BDH_ERR_ALIAS;
   if (numel4(out) == 0) return BDH_OK;
   if (K < kGK || K % kGK != 0 || N % 8 != 0) return BDH_ERR_SHAPE;
   // 16-byte rows: aligned bases, outer strides multiples of 8 elements
@@ -605,7 +629,7 @@ extern "C" int bdh_gated_gemm(const bdh_tensor4* y, const bdh_tensor4* wt, const
       if (t->size[i] > 1 && t->stride[i] % 8 != 0) return false;
     return true;
   };
-  if (!rows16(y) || !rows16(wt) || !rows16(x) || !rows16(out)) return BDH_ERR_STRIDE;
+  if (!rows16(y) || !rows16(wt) || (x != nullptr && !rows16(x)) || !rows16(out)) return BDH_ERR_STRIDE;
   const int64_t M = B * T;
   if (M >= (int64_t(1) << 31) || T >= (int64_t(1) << 31)) return BDH_ERR_SHAPE;
   // the DMA takes 32-bit byte offsets from the per-head bases of y and wt
@@ -620,10 +644,10 @@ extern "C" int bdh_gated_gemm(const bdh_tensor4* y, const bdh_tensor4* wt, const
   a.w = static_cast<const bf16_t*>(wt->data);
   a.w1 = wt->stride[1];
   a.w2 = wt->stride[2];
-  a.x = static_cast<const bf16_t*>(x->data);
-  a.x0 = x->stride[0];
-  a.x1 = x->stride[1];
-  a.x2 = x->stride[2];
+  a.x = x != nullptr ? static_cast<const bf16_t*>(x->data) : nullptr;
+  a.x0 = x != nullptr ? x->stride[0] : 0;
+  a.x1 = x != nullptr ? x->stride[1] : 0;
+  a.x2 = x != nullptr ? x->stride[2] : 0;
   a.o = static_cast<bf16_t*>(out->data);
   a.o0 = out->stride[0];
   a.o1 = out->stride[1];
@@ -638,8 +662,30 @@ extern "C" int bdh_gated_gemm(const bdh_tensor4* y, const bdh_tensor4* wt, const
   a.per_xcd = (a.total + 7) / 8;
   const int64_t grid = 8 * a.per_xcd;
   if (grid >= (int64_t(1) << 31)) return BDH_ERR_SHAPE;
-  BDH_LAUNCH("k_gated_gemm", k_gated_gemm, dim3(unsigned(grid)), dim3(512), 0, static_cast<hipStream_t>(stream), a);
+  if (x == nullptr && relu_enc_takes(K, N)) {
+    // the encoder chunks: 32-bit byte offsets from the head's base of wt
+    if (((N - 1) * wt->stride[2] + K) * 2 >= (int64_t(1) << 32)) return BDH_ERR_SHAPE;
+    return relu_enc_launch(y, wt, out, static_cast<hipStream_t>(stream));
+  }
+  if (x != nullptr)
+    BDH_LAUNCH("k_gated_gemm", k_gated_gemm<true>, dim3(unsigned(grid)), dim3(512), 0,
+               static_cast<hipStream_t>(stream), a);
+  else
+    BDH_LAUNCH("k_relu_gemm", k_gated_gemm<false>, dim3(unsigned(grid)), dim3(512), 0,
+               static_cast<hipStream_t>(stream), a);
   return BDH_OK;
+}
+
+extern "C" int bdh_gated_gemm(const bdh_tensor4* y, const bdh_tensor4* wt, const bdh_tensor4* x,
+                              const bdh_tensor4* out, bdh_stream stream) {
+  if (x == nullptr) return BDH_ERR_ARG;
+  return gated_gemm_launch(y, wt, x, out, stream);
+}
+
+// out = relu(y @ wt^T) per head as bf16; see k_gated_gemm.
+extern "C" int bdh_relu_gemm(const bdh_tensor4* y, const bdh_tensor4* wt, const bdh_tensor4* out,
+                             bdh_stream stream) {
+  return gated_gemm_launch(y, wt, nullptr, out, stream);
 }
 
 extern "C" size_t bdh_small_gemm_workspace(int64_t M, int64_t K, int64_t D) {

@@ -70,6 +70,7 @@ from .hip_attn import (
     gated_gemm,
     gated_decoder,
     has_hip_kernel,
+    relu_gemm,
     layer_norm_rows,
     relu_mul,
     small_gemm,
@@ -109,6 +110,7 @@ __all__ = [
     "relu_mul",
     "gated_gemm",
     "gated_decoder",
+    "relu_gemm",
     "small_gemm",
     "layer_norm_rows",
     "tril_rope_score_v",

@@ -140,6 +140,14 @@ def gated_gemm(y: torch.Tensor, wt: torch.Tensor, x: torch.Tensor) -> torch.Tens
     return ext.gated_gemm(y, wt, x)
 
 
+def relu_gemm(y: torch.Tensor, wt: torch.Tensor) -> torch.Tensor:
+    """``relu(y @ wt^T)`` per head on the GPU, (B, T, nh, N) bf16 (the encoder and its
+    ReLU, bdh.py:861-912); y (B, nh, T, K) may share one row set over the heads
+    (head stride 0)."""
+    ext = _require(y, wt)
+    return ext.relu_gemm(y, wt)
+
+
 def gated_decoder(y: torch.Tensor, wt: torch.Tensor, x: torch.Tensor, dec: torch.Tensor,
                   out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
     """``(x * relu(y @ wt^T)) @ decoder`` in one pass on the GPU (bdh.py:914-945), the
@@ -274,6 +282,7 @@ __all__ = [
     "relu_mul",
     "gated_gemm",
     "gated_decoder",
+    "relu_gemm",
     "small_gemm",
     "tril_rope_score_v",
     "tril_decode",

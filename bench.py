@@ -80,6 +80,8 @@ CALIB_BYTES = 1 << 29  # reference elementwise pass that scales the HBM byte cou
 MARK_ELEMS = 1 << 16  # the section marker multiply of --pmc-targets (a grid no other target has)
 # the library kernels of the layer's gated product (alone, or chained into the decoder)
 GATED_KERNELS = ("k_gated_gemm", "k_relu_mul", "k_gated_dec", "k_head_sum")
+# the library kernels of the layer's encoder with its ReLU
+ENCODER_KERNELS = ("k_relu_enc", "k_relu_gemm")
 
 
 def log(msg: str) -> None:
@@ -781,11 +783,13 @@ def run_models(torch, ext, dev, only=None) -> dict:
         rec = ext.profile_collect()
         ext.profile_enable(False)
         mlp = GATED_KERNELS
-        leg["hip"]["attention_kernels_ms"] = sum(t for n, t in rec if n not in mlp)
+        leg["hip"]["attention_kernels_ms"] = sum(t for n, t in rec if n not in mlp + ENCODER_KERNELS)
         leg["hip"]["gated_product_kernels_ms"] = sum(t for n, t in rec if n in mlp)
+        leg["hip"]["encoder_kernels_ms"] = sum(t for n, t in rec if n in ENCODER_KERNELS)
         out[name] = leg
         log(f"[bench] {name}: hip {leg['hip']['tok_s']:.0f} tok/s ({leg['hip']['ms']:.2f} ms, attention kernels "
-            f"{leg['hip']['attention_kernels_ms']:.2f} ms, gated product {leg['hip']['gated_product_kernels_ms']:.2f} ms)"
+            f"{leg['hip']['attention_kernels_ms']:.2f} ms, gated product {leg['hip']['gated_product_kernels_ms']:.2f} ms, "
+            f"encoder {leg['hip']['encoder_kernels_ms']:.2f} ms)"
             + (f", eager {leg['eager']['tok_s']:.0f} tok/s" if "eager" in leg else ""))
         del m, idx
         torch.cuda.empty_cache()
@@ -899,7 +903,8 @@ def run_pmc_targets(torch, ext, kernels, dev, reps: int = 3) -> None:
     del q4, v4, d4, sc
     section_end()
     # one C2 layer's gated product (k_gated_gemm): y (B, nh, T, D), encoder_v^T (nh, N, D), x (B, T, nh, N);
-    # then the same product chained into the decoder (k_gated_dec, k_head_sum), dec (nh*N, D)
+    # then the same product chained into the decoder (k_gated_dec, k_head_sum), dec (nh*N, D),
+    # then the encoder with its ReLU (k_relu_enc) on rows shared by the heads
     c = C2
     N2 = c["mult"] * c["D"] // c["nh"]
     y = torch.randn(c["B"], c["nh"], c["T"], c["D"], generator=g, device=dev).to(bf)
@@ -910,7 +915,10 @@ def run_pmc_targets(torch, ext, kernels, dev, reps: int = 3) -> None:
         kernels.gated_gemm(y, wt, xb)
     for _ in range(reps):
         kernels.gated_decoder(y, wt, xb, dec)
-    del y, wt, xb, dec
+    ye = y[:, :1].expand(-1, c["nh"], -1, -1)  # the encoder: one row set shared by the heads
+    for _ in range(reps):
+        kernels.relu_gemm(ye, wt)
+    del y, wt, xb, dec, ye
     section_end()
     # one C2 layer's fused RoPE attention backward, bf16, x_sparse as the
     # model's permuted (B, T, nh, N) view: the route that recomputes the score
@@ -974,7 +982,7 @@ def run_train_step(torch, ext, dev, build) -> dict:
     step()
     rec = ext.profile_collect()
     ext.profile_enable(False)
-    leg["attention_kernels_ms"] = sum(t for n, t in rec if n not in GATED_KERNELS)
+    leg["attention_kernels_ms"] = sum(t for n, t in rec if n not in GATED_KERNELS + ENCODER_KERNELS)
     log(f"[bench] c2_train_step: {ms:.1f} ms, {leg['tok_s']:.0f} tok/s (attention kernels {leg['attention_kernels_ms']:.2f} ms)")
     del m, opt
     torch.cuda.empty_cache()

@@ -270,6 +270,16 @@ int bdh_gated_gemm(const bdh_tensor4* y, const bdh_tensor4* wt, const bdh_tensor
                    const bdh_tensor4* out, bdh_stream stream);
 
 /*
+ * The same GEMM without the gate, the encoder with its ReLU:
+ *   out[b,t,h,n] = max(sum_k y[b,h,t,k] * wt[0,h,n,k], 0)          (bf16)
+ * Replaces `_encoder_relu` (bdh.py:861-912: x @ encoder per head, ReLU) for the
+ * prefill: y (B, nh, T, K), the layer input, with a head stride of 0 when all
+ * heads share it; wt (1, nh, N, K), the encoder transposed; out (B, T, nh, N).
+ * Same sizes, strides and limits as bdh_gated_gemm.
+ */
+int bdh_relu_gemm(const bdh_tensor4* y, const bdh_tensor4* wt, const bdh_tensor4* out, bdh_stream stream);
+
+/*
  * The gated product chained into the decoder product, bf16 operands, fp32
  * accumulation:
  *   out[b,t,0,:] = sum_h sum_n x[b,t,h,n] * max(sum_k y[b,h,t,k] * wt[0,h,n,k], 0)

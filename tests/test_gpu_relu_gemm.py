@@ -1,0 +1,88 @@
+"""GPU checks of the encoder with its ReLU (``bdh_relu_gemm``).
+
+out[b, t, h, n] = relu(sum_k y[b, h, t, k] wt[h, n, k]) as bf16 (bdh.py:861-912,
+`_encoder_relu`), against CPU references on the same bf16 inputs:
+* float64 products rounded once to bf16: within 1e-2 relative Frobenius error,
+  and at least 99 % of the elements bit-identical (fp32 sums in another order
+  move an occasional value across a bf16 rounding boundary);
+* the library's generic tile kernel (k_gated_gemm without the gate), which the
+  entry point takes for shapes the streaming kernel does not: the same bounds.
+Shapes: K = 256 and 512 (the streaming kernel), ragged token blocks (B*T not a
+multiple of 256), one token, heads sharing y through a zero head stride (the
+encoder) and per-head y, N down to one chunk, and a K the streaming kernel
+does not take.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from helpers import rel_fro
+
+pytestmark = pytest.mark.gpu
+
+if not torch.cuda.is_available():
+    pytest.skip("needs a ROCm GPU", allow_module_level=True)
+
+import bdh_hip_ext as ext  # noqa: E402  (fails loudly when the library is missing)
+
+DEV = torch.device("cuda:0")
+BF = torch.bfloat16
+
+
+def _inputs(B, T, nh, N, K, seed, shared):
+    g = torch.Generator().manual_seed(seed)
+    y = torch.randn(B, 1 if shared else nh, T, K, generator=g).to(BF)
+    wt = (0.05 * torch.randn(nh, N, K, generator=g)).to(BF)
+    return y, wt
+
+
+def _want(y, wt, nh):
+    yy = y.double().expand(y.size(0), nh, y.size(2), y.size(3))
+    lin = torch.matmul(yy, wt.double().transpose(1, 2))  # (B, nh, T, N)
+    return torch.relu(lin).permute(0, 2, 1, 3).float().to(BF)
+
+
+@pytest.mark.parametrize("shape", [(2, 300, 4, 1024, 256), (1, 1, 2, 64, 256), (3, 129, 3, 192, 512),
+                                   (1, 512, 8, 8192, 512), (4, 256, 4, 8192, 256), (2, 77, 2, 96, 128)])
+@pytest.mark.parametrize("shared", [True, False])
+def test_relu_gemm_matches_reference(shape, shared):
+    B, T, nh, N, K = shape
+    print(f"relu_gemm {shape} shared={shared}", flush=True)
+    y, wt = _inputs(B, T, nh, N, K, seed=B * 7 + T + N + K, shared=shared)
+    yd = y.to(DEV)
+    yd = yd.expand(B, nh, T, K) if shared else yd
+    got = ext.relu_gemm(yd, wt.to(DEV)).cpu()
+    assert got.shape == (B, T, nh, N) and got.dtype == BF
+    want = _want(y, wt, nh)
+    e = rel_fro(got.float().numpy(), want.float().numpy())
+    same = float((got == want).float().mean())
+    print(f"  rel {e:.2e}, bit-identical {same:.4f}", flush=True)
+    assert e <= 1e-2
+    assert same >= 0.99
+    assert bool((got >= 0).all())
+
+
+def test_relu_gemm_encoder_view_matches_generic_kernel():
+    """At C2's width: the streaming kernel (N a multiple of 64) against the
+    generic tile kernel on the same rows (N = 8184 goes to it), and repeated
+    calls give the same bits."""
+    B, T, nh, K = 4, 512, 4, 256
+    y, wt = _inputs(B, T, nh, 8192, K, seed=11, shared=True)
+    yd = y.to(DEV).expand(B, nh, T, K)
+    wd = wt.to(DEV)
+    got = ext.relu_gemm(yd, wd)
+    assert torch.equal(got, ext.relu_gemm(yd, wd))
+    gen = ext.relu_gemm(yd, wd[:, :8184].contiguous())
+    a, b = got[..., :8184].float().cpu(), gen.float().cpu()
+    assert rel_fro(a.numpy(), b.numpy()) <= 1e-2
+    assert float((got[..., :8184] == gen).float().mean()) >= 0.99
+
+
+def test_relu_gemm_rejects_bad_shapes():
+    y, wt = (t.to(DEV) for t in _inputs(1, 8, 2, 64, 256, seed=3, shared=False))
+    with pytest.raises(RuntimeError):
+        ext.relu_gemm(y, wt[..., :128].contiguous())  # K mismatch
+    with pytest.raises(RuntimeError):
+        ext.relu_gemm(y[:, :1].contiguous(), wt)  # head count
