@@ -6,7 +6,8 @@ partial-tile stores, k_sy_sv's partial, V and output accesses;
 csrc/decode.hip: k_decode_bf16's key, q and partial accesses; the training
 backward's k_dq_sy B loads on x and k_dv_sy; csrc/model.hip: k_gated_gemm's
 LDS-DMA operand loads and epilogue x loads; csrc/gated_dec.hip: k_gated_dec's
-grid, operand DMA, LDS fragment reads and partial stores) are restated here and evaluated over every
+grid, operand DMA, LDS fragment reads and partial stores; csrc/enc.hip: k_relu_enc's grid,
+encoder DMA, fragment and tile accesses and output stores) are restated here and evaluated over every
 work item, with the strides of the views the harness passes (x_sparse as the
 permuted (B, T, nh, N) encoder output, the packed KV cache's
 capacity-strided past views).  Each access must fall inside its buffer and
@@ -415,3 +416,82 @@ def check_gated_dec(B, T, nh, N):
                                       (1, 257, 1, 32)])
 def test_gated_decoder_launches_stay_in_bounds(B, T, nh, N):
     check_gated_dec(B, T, nh, N)
+
+
+def check_relu_enc(B, T, nh, N, K):
+    """csrc/enc.hip k_relu_enc on the harness's operands y (B, 1, T, K) expanded over the heads
+    (head stride 0), wt (nh, N, K), out (B, T, nh, N): the XCD-major grid covers each (head,
+    256-token block) once; each chunk's DMA (instruction i = 4 u + w: K = 256 rows 2 i + l / 32,
+    position l % 32; K = 512 row i, position l; chunk position ^ (row % 32)) reads inside wt with
+    32-bit offsets from the head's base and writes its 1 KB of the 32 KB slot; the fragment
+    reads stay in their slot; the tile writes and reads stay in their tile; the y loads and the
+    output stores (the chunk walk wraps from the block's starting chunk) stay in bounds."""
+    MT, SLOT, RING = 256, 32 * 1024, 3
+    NC = 64 if K == 256 else 32
+    ROWB, NB, KS = K * 2, NC // 32, K // 16
+    TROW = NC * 2
+    TILE, TCH = MT * TROW, TROW // 16
+    SPT, RSTEP = MT * TCH // 256, 256 // TCH
+    assert RING * SLOT + 2 * TILE <= 160 * 1024 and N % NC == 0
+    M = B * T
+    ntb = (M + MT - 1) // MT
+    total = ntb * nh
+    per_xcd = (total + 7) // 8
+    seen = []
+    for bid in range(8 * per_xcd):
+        t = (bid & 7) * per_xcd + (bid >> 3)
+        if (bid >> 3) < per_xcd and t < total:
+            seen.append(divmod(t, ntb))
+    assert sorted(seen) == [(h, tb) for h in range(nh) for tb in range(ntb)]
+    nck = N // NC
+    assert (N - 1) * K * 2 + K * 2 < 2 ** 32
+    for h in {0, nh - 1}:
+        for tb in {0, ntb - 1}:
+            m0 = tb * MT
+            c0 = tb * nck // ntb % nck
+            chunks = {(c + c0) % nck for c in (0, nck - 1)} | {nck - 1}
+            for w in range(4):
+                for lane in (0, 7, 31, 32, 63):
+                    hl, l32 = lane >> 5, lane & 31
+                    for u in range(8):
+                        i = 4 * u + w
+                        r = 2 * i + hl if K == 256 else i
+                        p = l32 if K == 256 else lane
+                        c = p ^ (r & 31)
+                        assert 0 <= r < NC and 0 <= c < K // 8
+                        for slot in range(RING):
+                            lds = slot * SLOT + u * 4096 + w * 1024 + 16 * lane
+                            assert lds == slot * SLOT + i * 1024 + 16 * lane and lds + 16 <= (slot + 1) * SLOT
+                        for cc in chunks:
+                            off = (cc * NC + r) * K + 8 * c
+                            assert off * 2 < 2 ** 32 and h * N * K + off + 8 <= nh * N * K
+                    for j in range(2):
+                        m = min(m0 + 64 * w + 32 * j + l32, M - 1)
+                        b, tt = divmod(m, T)
+                        assert b * T * K + tt * K + 8 * hl + 16 * (KS - 1) + 8 <= B * T * K
+                    for s_ in range(KS):
+                        for i in range(NB):
+                            o = i * 32 * ROWB + l32 * ROWB + 16 * ((2 * s_ + hl) ^ l32)
+                            assert 0 <= o and o + 16 <= SLOT
+                    for it in range(NB * 8):
+                        i, j, q = it // 8, (it // 4) & 1, it & 3
+                        row = 64 * w + 32 * j + l32
+                        o = row * TROW + 16 * ((4 * i + q) ^ (row & (TCH - 1))) + 8 * hl
+                        assert 0 <= o and o + 8 <= TILE
+            for tid in (0, 5, 100, 255):
+                spc = tid % TCH
+                for e in range(SPT):
+                    r = tid // TCH + RSTEP * e
+                    assert r < MT and r * TROW + 16 * (spc ^ (r & (TCH - 1))) + 16 <= TILE
+                    m = m0 + r
+                    if m < M:
+                        b, tt = divmod(m, T)
+                        for cc in chunks:
+                            o = b * T * nh * N + tt * nh * N + h * N + 8 * spc + cc * NC
+                            assert o + 8 <= B * T * nh * N and 8 * spc + cc * NC + 8 <= N
+
+
+@pytest.mark.parametrize("B,T,nh,N,K", [(32, 512, 4, 8192, 256), (4, 2048, 8, 8192, 512), (64, 256, 4, 8192, 256),
+                                        (2, 300, 4, 1024, 256), (3, 129, 3, 192, 512), (1, 1, 2, 64, 256)])
+def test_relu_encoder_launches_stay_in_bounds(B, T, nh, N, K):
+    check_relu_enc(B, T, nh, N, K)
