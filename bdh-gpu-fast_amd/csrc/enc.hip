@@ -1,9 +1,12 @@
-// The BDH encoder with its ReLU, for gfx950:
+// The BDH encoder with its ReLU, and the gated encoder_v product, for gfx950:
 //
 //   out[b, t, h, n] = max(sum_k y[b, h, t, k] * wt[h, n, k], 0)          (bf16)
+//   out[b, t, h, n] = x[b, t, h, n] * max(sum_k y[b, h, t, k] wt[h, n, k], 0)
 //
-// (bdh.py:861-912, `_encoder_relu`: x @ encoder per head, then ReLU), with
-// K = 256 or 512 (the C2 and C5 models), bf16 operands, fp32 accumulation.
+// (bdh.py:861-912, `_encoder_relu`: x @ encoder per head, then ReLU;
+// bdh.py:914-945, `_encoder_v_relu` and the `x_bthn * y_bthn` of _mlp_merge),
+// with K = 256 or 512 (the C2 and C5 models), bf16 operands, fp32
+// accumulation, the GEMM's ReLU rounded to bf16 before the gate.
 // The product has few K steps and a large output (B*T x nh*N: 1.07 GB at C2
 // and C5), so the kernel is built around the output stream:
 //
@@ -23,13 +26,18 @@
 //    groups from a second accumulator set; one chunk later the tile leaves
 //    as 16-byte stores covering whole 128-byte (K = 256) or 64-byte pieces of
 //    output rows.  Two tiles alternate.
+//  * Gated form: each chunk's x pieces land by LDS DMA in the output tile
+//    itself, and the epilogue multiplies in place.
 //  * The token blocks of a head walk the chunks from evenly spread starting
 //    chunks (see c0).
-// Measured (one box, against hipBLASLt's GEMM with a ReLU epilogue on the
-// same operands, bit-identical outputs): C2 (M = 16384, K = 256, 4 x 8192
-// columns) 330 against 430 us, C5 (M = 8192, K = 512, 8 x 8192) 585 against
-// 668 us.  Without the output stores the loop takes 248 / 510 us; the MFMA
-// work alone is 125 / 250 us at 2.1 GHz.
+// Measured (one box; bit-identical outputs): the encoder at C2 (M = 16384,
+// K = 256, 4 x 8192 columns) 330 us against 430 for hipBLASLt's GEMM with a
+// ReLU epilogue, at C5 (M = 8192, K = 512, 8 x 8192) 585 against 668; the
+// gated form 507 / 785 us against 628 / 800 for the tile kernel.  Without the
+// output stores the encoder loop takes 233-248 / 440-510 us, with the MFMAs
+// taken out 232 / 609 us; the MFMA work alone is 125 / 250 us at 2.1 GHz.
+// The LDS (encoder fragments, tile writes and reads, the DMA) and the
+// per-chunk barrier, not the matrix cores, set the pace.
 // The workgroups of one head sit on the same XCD, so the head's encoder
 // chunks stream through that XCD's L2 once for all its token blocks.
 #include "common.h"
@@ -61,6 +69,8 @@ struct EncArgs {
   int64_t y0, y1, y2;  // (B, nh, T, K)
   const bf16_t* w;
   int64_t w1, w2;      // (1, nh, N, K)
+  const bf16_t* x;
+  int64_t x0, x1, x2;  // (B, T, nh, N): the gate (gated form)
   bf16_t* o;
   int64_t o0, o1, o2;  // (B, T, nh, N)
   int T, M, N, ntb;
@@ -80,7 +90,7 @@ __device__ __forceinline__ f32x16 en_mma(bf16x8 a, bf16x8 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
-template <int K>
+template <int K, bool MUL>
 __global__ __launch_bounds__(256, 1) void k_relu_enc(const EncArgs a) {
   using S = EnShape<K>;
   __shared__ __attribute__((aligned(1024))) uint8_t en_lds[S::LDS];
@@ -131,6 +141,38 @@ __global__ __launch_bounds__(256, 1) void k_relu_enc(const EncArgs a) {
     dma16<5 * 4096>(m0b, wbase, goff[5] + kw);
     dma16<6 * 4096>(m0b, wbase, goff[6] + kw);
     dma16<7 * 4096>(m0b, wbase, goff[7] + kw);
+  };
+
+  // ---- gated form: the x pieces of chunk c land by LDS DMA in output tile
+  // c & 1, in the tile's own layout, and the epilogue multiplies in place.
+  // Instruction u of wave w fills tile bytes [i KB, +1 KB), i = 4 u + w:
+  // rows RPI i + l / TCH, the lane's position l % TCH holding piece
+  // (l % TCH) ^ (row % TCH).  Those are the rows the wave's tile reads take
+  // (rows tid / TCH + (256 / TCH) e), so the wave refills only rows it has
+  // itself read.
+  constexpr int RPI = 1024 / S::TROW, XI = S::TILE / 1024 / 4;
+  const bf16_t* xrow[MUL ? XI : 1];
+  if constexpr (MUL) {
+#pragma unroll
+    for (int u = 0; u < XI; ++u) {
+      const int r = RPI * (4 * u + w) + lane / S::TCH;
+      const int m = min(m0 + r, a.M - 1);
+      const int b = m / a.T, tt = m - b * a.T;
+      xrow[u] = a.x + b * a.x0 + tt * a.x1 + int64_t(h) * a.x2 + 8 * ((lane % S::TCH) ^ (r & (S::TCH - 1)));
+    }
+  }
+  const uint32_t tl = lds0 + uint32_t(kEnRing * kEnSlot) + uint32_t(w) * 1024u;
+  auto issue_x = [&](int ck) __attribute__((always_inline)) {
+    const uint32_t m0b = tl + uint32_t((ck & 1) * S::TILE);
+    const int64_t col = int64_t(cmap(ck)) * S::NC;
+#pragma unroll
+    for (int u = 0; u < XI; ++u) {
+      const bf16_t* src = xrow[u] + col;
+      asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off offset:0"
+                   :
+                   : "s"(m0b + uint32_t(u * 4096)), "v"(src)
+                   : "memory", "m0");
+    }
   };
 
   // ---- y fragments in registers: token block j (32 tokens), k16 step s
@@ -200,9 +242,19 @@ __global__ __launch_bounds__(256, 1) void k_relu_enc(const EncArgs a) {
     constexpr int it = decltype(itc)::value;
     constexpr int i = it / 8, j = (it / 4) & 1, q = it & 3;
     const int row = 64 * w + 32 * j + l32;
-    const u32x2 v{pack_bf2(fmaxf(acc[i][j][4 * q], 0.f), fmaxf(acc[i][j][4 * q + 1], 0.f)),
-                  pack_bf2(fmaxf(acc[i][j][4 * q + 2], 0.f), fmaxf(acc[i][j][4 * q + 3], 0.f))};
-    *reinterpret_cast<u32x2*>(tp + row * S::TROW + 16 * ((4 * i + q) ^ (row & (S::TCH - 1))) + 8 * hl) = v;
+    uint8_t* const pp = tp + row * S::TROW + 16 * ((4 * i + q) ^ (row & (S::TCH - 1))) + 8 * hl;
+    u32x2 v{pack_bf2(fmaxf(acc[i][j][4 * q], 0.f), fmaxf(acc[i][j][4 * q + 1], 0.f)),
+            pack_bf2(fmaxf(acc[i][j][4 * q + 2], 0.f), fmaxf(acc[i][j][4 * q + 3], 0.f))};
+    if constexpr (MUL) {
+      // x * relu(S): relu(S) rounded to bf16 (the value the plain GEMM
+      // stores), the product in fp32, rounded once more
+      const u32x2 xv = *reinterpret_cast<const u32x2*>(pp);
+      v.x = pack_bf2(__uint_as_float(xv.x << 16) * __uint_as_float(v.x << 16),
+                     __uint_as_float(xv.x & 0xffff0000u) * __uint_as_float(v.x & 0xffff0000u));
+      v.y = pack_bf2(__uint_as_float(xv.y << 16) * __uint_as_float(v.y << 16),
+                     __uint_as_float(xv.y & 0xffff0000u) * __uint_as_float(v.y & 0xffff0000u));
+    }
+    *reinterpret_cast<u32x2*>(pp) = v;
   };
 
   // One chunk: wait for its operands, then (fenced) the tile reads of chunk
@@ -227,7 +279,10 @@ __global__ __launch_bounds__(256, 1) void k_relu_enc(const EncArgs a) {
     } else {
       read_group(f0, sb, 0);
     }
-    // after the stores: a global store behind the DMA asm would wait for it
+    // after the stores: a global store behind the DMA asm would wait for it.
+    // Gated form: chunk ck's x pieces into tile ck & 1, after this wave's
+    // reads of its rows there (chunk ck - 2's tile, consumed by the stores)
+    if constexpr (MUL) issue_x(ck);
     issue(ck + 2 < nck ? cmap(ck + 2) : nck - 1, slot == 0 ? 2 : slot - 1);  // into the slot of chunk ck - 1
     en_static_for<S::NB>([&](auto ic) {
       en_static_for<2>([&](auto jc) {
@@ -276,6 +331,7 @@ __global__ __launch_bounds__(256, 1) void k_relu_enc(const EncArgs a) {
   // chunk ck - 1's result is in acc0; one chunk may remain
   const bool odd = ck < nck;
   if (odd) chunk(acc1, acc0, ck, slot, true);
+  sy_wait<8>();      // gated form: the x pieces of chunk nck - 1 landed
   __syncthreads();  // chunk nck - 2's tile writes are done
   if (nck >= 2) {
     uint4 tv[S::SPT];
@@ -304,7 +360,8 @@ __global__ __launch_bounds__(256, 1) void k_relu_enc(const EncArgs a) {
 // the chunk width; false when the shape is not one it takes.
 bool relu_enc_takes(int64_t K, int64_t N) { return (K == 256 && N % 64 == 0) || (K == 512 && N % 32 == 0); }
 
-int relu_enc_launch(const bdh_tensor4* y, const bdh_tensor4* wt, const bdh_tensor4* out, hipStream_t s) {
+int relu_enc_launch(const bdh_tensor4* y, const bdh_tensor4* wt, const bdh_tensor4* x, const bdh_tensor4* out,
+                    hipStream_t s) {
   const int64_t B = out->size[0], T = out->size[1], H = out->size[2], N = out->size[3], K = y->size[3];
   EncArgs a;
   a.y = static_cast<const bf16_t*>(y->data);
@@ -314,6 +371,10 @@ int relu_enc_launch(const bdh_tensor4* y, const bdh_tensor4* wt, const bdh_tenso
   a.w = static_cast<const bf16_t*>(wt->data);
   a.w1 = wt->stride[1];
   a.w2 = wt->stride[2];
+  a.x = x != nullptr ? static_cast<const bf16_t*>(x->data) : nullptr;
+  a.x0 = x != nullptr ? x->stride[0] : 0;
+  a.x1 = x != nullptr ? x->stride[1] : 0;
+  a.x2 = x != nullptr ? x->stride[2] : 0;
   a.o = static_cast<bf16_t*>(out->data);
   a.o0 = out->stride[0];
   a.o1 = out->stride[1];
@@ -326,10 +387,17 @@ int relu_enc_launch(const bdh_tensor4* y, const bdh_tensor4* wt, const bdh_tenso
   a.per_xcd = (a.total + 7) / 8;
   const int64_t grid = 8 * a.per_xcd;
   if (grid >= (int64_t(1) << 31)) return BDH_ERR_SHAPE;
-  if (K == 256)
-    BDH_LAUNCH("k_relu_enc", k_relu_enc<256>, dim3(unsigned(grid)), dim3(256), 0, s, a);
-  else
-    BDH_LAUNCH("k_relu_enc", k_relu_enc<512>, dim3(unsigned(grid)), dim3(256), 0, s, a);
+  if (x != nullptr) {
+    if (K == 256)
+      BDH_LAUNCH("k_gated_enc", (k_relu_enc<256, true>), dim3(unsigned(grid)), dim3(256), 0, s, a);
+    else
+      BDH_LAUNCH("k_gated_enc", (k_relu_enc<512, true>), dim3(unsigned(grid)), dim3(256), 0, s, a);
+  } else {
+    if (K == 256)
+      BDH_LAUNCH("k_relu_enc", (k_relu_enc<256, false>), dim3(unsigned(grid)), dim3(256), 0, s, a);
+    else
+      BDH_LAUNCH("k_relu_enc", (k_relu_enc<512, false>), dim3(unsigned(grid)), dim3(256), 0, s, a);
+  }
   return BDH_OK;
 }
 

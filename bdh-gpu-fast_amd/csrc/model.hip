@@ -599,7 +599,8 @@ extern "C" int bdh_relu_mul(const bdh_tensor4* x, const bdh_tensor4* y, const bd
 
 namespace bdh {
 bool relu_enc_takes(int64_t K, int64_t N);
-int relu_enc_launch(const bdh_tensor4* y, const bdh_tensor4* wt, const bdh_tensor4* out, hipStream_t s);
+int relu_enc_launch(const bdh_tensor4* y, const bdh_tensor4* wt, const bdh_tensor4* x, const bdh_tensor4* out,
+                    hipStream_t s);
 }  // namespace bdh
 
 // out = [x *] relu(y @ wt^T) per head (x null: the ReLU GEMM alone, k_relu_enc
@@ -662,11 +663,8 @@ static int gated_gemm_launch(const bdh_tensor4* y, const bdh_tensor4* wt, const 
   a.per_xcd = (a.total + 7) / 8;
   const int64_t grid = 8 * a.per_xcd;
   if (grid >= (int64_t(1) << 31)) return BDH_ERR_SHAPE;
-  if (x == nullptr && relu_enc_takes(K, N)) {
-    // the encoder chunks: 32-bit byte offsets from the head's base of wt
-    if (((N - 1) * wt->stride[2] + K) * 2 >= (int64_t(1) << 32)) return BDH_ERR_SHAPE;
-    return relu_enc_launch(y, wt, out, static_cast<hipStream_t>(stream));
-  }
+  if (relu_enc_takes(K, N) && ((N - 1) * wt->stride[2] + K) * 2 < (int64_t(1) << 32))
+    return relu_enc_launch(y, wt, x, out, static_cast<hipStream_t>(stream));
   if (x != nullptr)
     BDH_LAUNCH("k_gated_gemm", k_gated_gemm<true>, dim3(unsigned(grid)), dim3(512), 0,
                static_cast<hipStream_t>(stream), a);

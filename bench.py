@@ -79,7 +79,7 @@ C3_GEN = dict(n_layer=6, D=256, nh=4, mult=128, B=64, prompt=256, new=256, top_k
 CALIB_BYTES = 1 << 29  # reference elementwise pass that scales the HBM byte counters
 MARK_ELEMS = 1 << 16  # the section marker multiply of --pmc-targets (a grid no other target has)
 # the library kernels of the layer's gated product (alone, or chained into the decoder)
-GATED_KERNELS = ("k_gated_gemm", "k_relu_mul", "k_gated_dec", "k_head_sum")
+GATED_KERNELS = ("k_gated_gemm", "k_gated_enc", "k_relu_mul", "k_gated_dec", "k_head_sum")
 # the library kernels of the layer's encoder with its ReLU
 ENCODER_KERNELS = ("k_relu_enc", "k_relu_gemm")
 

@@ -264,7 +264,10 @@ int bdh_relu_mul(const bdh_tensor4* x, const bdh_tensor4* y, const bdh_tensor4* 
  * attention output; wt: (1, nh, N, K), encoder_v transposed; x, out:
  * (B, T, nh, N).  K a multiple of 32, N of 8, rows 16-byte aligned; one
  * head's view of y and of wt spans at most 4 GiB (else BDH_ERR_SHAPE).  The
- * GEMM result is rounded to bf16 after the ReLU, then multiplied by x.
+ * GEMM result is rounded to bf16 after the ReLU, then multiplied by x.  K =
+ * 256 with N a multiple of 64, and K = 512 with N a multiple of 32, run on the
+ * streaming kernel (one workgroup per head and 256 tokens); other shapes on a
+ * tile kernel.  Both give the same bits.
  */
 int bdh_gated_gemm(const bdh_tensor4* y, const bdh_tensor4* wt, const bdh_tensor4* x,
                    const bdh_tensor4* out, bdh_stream stream);
@@ -275,7 +278,7 @@ int bdh_gated_gemm(const bdh_tensor4* y, const bdh_tensor4* wt, const bdh_tensor
  * Replaces `_encoder_relu` (bdh.py:861-912: x @ encoder per head, ReLU) for the
  * prefill: y (B, nh, T, K), the layer input, with a head stride of 0 when all
  * heads share it; wt (1, nh, N, K), the encoder transposed; out (B, T, nh, N).
- * Same sizes, strides and limits as bdh_gated_gemm.
+ * Same sizes, strides, limits and kernels as bdh_gated_gemm.
  */
 int bdh_relu_gemm(const bdh_tensor4* y, const bdh_tensor4* wt, const bdh_tensor4* out, bdh_stream stream);
 

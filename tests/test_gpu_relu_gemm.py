@@ -1,4 +1,5 @@
-"""GPU checks of the encoder with its ReLU (``bdh_relu_gemm``).
+"""GPU checks of the encoder with its ReLU (``bdh_relu_gemm``) and of the gated form
+(``bdh_gated_gemm``, x * relu(...)) on the same streaming kernel.
 
 out[b, t, h, n] = relu(sum_k y[b, h, t, k] wt[h, n, k]) as bf16 (bdh.py:861-912,
 `_encoder_relu`), against CPU references on the same bf16 inputs:
@@ -86,3 +87,46 @@ def test_relu_gemm_rejects_bad_shapes():
         ext.relu_gemm(y, wt[..., :128].contiguous())  # K mismatch
     with pytest.raises(RuntimeError):
         ext.relu_gemm(y[:, :1].contiguous(), wt)  # head count
+
+
+def _want_gated(y, wt, x):
+    """x * relu(y wt^T): the GEMM in float64, relu rounded to bf16, the product rounded to bf16."""
+    lin = torch.matmul(y.double(), wt.double().transpose(1, 2))  # (B, nh, T, N)
+    r = torch.relu(lin).float().to(BF).permute(0, 2, 1, 3)
+    return (x.float() * r.float()).to(BF)
+
+
+@pytest.mark.parametrize("shape", [(2, 300, 4, 1024, 256), (1, 1, 2, 64, 256), (3, 129, 3, 192, 512),
+                                   (2, 1024, 8, 8192, 512), (2, 77, 2, 96, 128)])
+def test_gated_form_matches_reference(shape):
+    """The gated form (x * relu(y wt^T), the encoder_v product of the layer; the
+    streaming kernel for K = 256 / 512, the generic tile kernel for K = 128)
+    against float64 with the two bf16 roundings: within 1e-2, 99 % bit-identical."""
+    B, T, nh, N, K = shape
+    print(f"gated form {shape}", flush=True)
+    y, wt = _inputs(B, T, nh, N, K, seed=B * 11 + T + N + K, shared=False)
+    g = torch.Generator().manual_seed(N + K)
+    x = torch.relu(torch.randn(B, T, nh, N, generator=g)).to(BF)
+    got = ext.gated_gemm(y.to(DEV), wt.to(DEV), x.to(DEV)).cpu()
+    want = _want_gated(y, wt, x)
+    e = rel_fro(got.float().numpy(), want.float().numpy())
+    same = float((got == want).float().mean())
+    print(f"  rel {e:.2e}, bit-identical {same:.4f}", flush=True)
+    assert got.shape == (B, T, nh, N) and e <= 1e-2 and same >= 0.99
+
+
+def test_gated_form_c5_width_repeats_and_matches_generic():
+    """At C5's width (K = 512, 8 x 8192 columns): repeated calls give the same
+    bits, and the generic tile kernel (N = 8184 goes to it) agrees on the
+    shared columns."""
+    B, T, nh, N, K = 2, 1024, 8, 8192, 512
+    y, wt = (t.to(DEV) for t in _inputs(B, T, nh, N, K, seed=5, shared=False))
+    g = torch.Generator().manual_seed(9)
+    x = torch.relu(torch.randn(B, T, nh, N, generator=g)).to(BF).to(DEV)
+    got = ext.gated_gemm(y, wt, x)
+    for _ in range(3):
+        assert torch.equal(got, ext.gated_gemm(y, wt, x))
+    gen = ext.gated_gemm(y, wt[:, :8184].contiguous(), x[..., :8184].contiguous())
+    a, b = got[..., :8184], gen
+    assert rel_fro(a.float().cpu().numpy(), b.float().cpu().numpy()) <= 1e-2
+    assert float((a == b).float().mean()) >= 0.99
