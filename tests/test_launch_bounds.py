@@ -424,7 +424,8 @@ def check_relu_enc(B, T, nh, N, K):
     256-token block) once; each chunk's DMA (instruction i = 4 u + w: K = 256 rows 2 i + l / 32,
     position l % 32; K = 512 row i, position l; chunk position ^ (row % 32)) reads inside wt with
     32-bit offsets from the head's base and writes its 1 KB of the 32 KB slot; the fragment
-    reads stay in their slot; the tile writes and reads stay in their tile; the y loads and the
+    reads stay in their slot; the tile writes and reads stay in their tile; the gated form's x
+    DMA writes its tile bytes, only rows the same wave reads, from inside x; the y loads and the
     output stores (the chunk walk wraps from the block's starting chunk) stay in bounds."""
     MT, SLOT, RING = 256, 32 * 1024, 3
     NC = 64 if K == 256 else 32
@@ -478,6 +479,24 @@ def check_relu_enc(B, T, nh, N, K):
                         row = 64 * w + 32 * j + l32
                         o = row * TROW + 16 * ((4 * i + q) ^ (row & (TCH - 1))) + 8 * hl
                         assert 0 <= o and o + 8 <= TILE
+            # gated form: x pieces by LDS DMA into the tile, instruction u of wave w
+            # rows RPI (4 u + w) + l / TCH: the same rows as the wave's own tile reads
+            RPI, XI = 1024 // TROW, TILE // 1024 // 4
+            for w in range(4):
+                dma_rows = {RPI * (4 * u + w) + lane // TCH for u in range(XI) for lane in range(64)}
+                read_rows = {(64 * w + lane) // TCH + RSTEP * e for lane in range(64) for e in range(SPT)}
+                assert dma_rows == read_rows
+                for u in range(XI):
+                    for lane in (0, 3, 31, 63):
+                        r = RPI * (4 * u + w) + lane // TCH
+                        piece = (lane % TCH) ^ (r & (TCH - 1))
+                        lds = (4 * u + w) * 1024 + 16 * lane
+                        assert lds + 16 <= TILE and lds == r * TROW + 16 * (lane % TCH)
+                        m = min(m0 + r, M - 1)
+                        b, tt = divmod(m, T)
+                        for cc in chunks:
+                            o = b * T * nh * N + tt * nh * N + h * N + 8 * piece + cc * NC
+                            assert o + 8 <= B * T * nh * N and 8 * piece + cc * NC + 8 <= N
             for tid in (0, 5, 100, 255):
                 spc = tid % TCH
                 for e in range(SPT):
