@@ -140,12 +140,12 @@ def gated_gemm(y: torch.Tensor, wt: torch.Tensor, x: torch.Tensor) -> torch.Tens
     return ext.gated_gemm(y, wt, x)
 
 
-def relu_gemm(y: torch.Tensor, wt: torch.Tensor) -> torch.Tensor:
+def relu_gemm(y: torch.Tensor, wt: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
     """``relu(y @ wt^T)`` per head on the GPU, (B, T, nh, N) bf16 (the encoder and its
     ReLU, bdh.py:861-912); y (B, nh, T, K) may share one row set over the heads
-    (head stride 0)."""
-    ext = _require(y, wt)
-    return ext.relu_gemm(y, wt)
+    (head stride 0); ``out`` may be a strided (B, T, nh, N) view (padded rows)."""
+    ext = _require(y, wt, out)
+    return ext.relu_gemm(y, wt, out)
 
 
 def gated_decoder(y: torch.Tensor, wt: torch.Tensor, x: torch.Tensor, dec: torch.Tensor,

@@ -87,13 +87,17 @@ def test_forward_full_c2_config_matches_oracle():
     assert rel_fro(got.float().cpu().numpy(), M.bdh_forward(p, idx)) <= 2e-2
 
 
-def test_forward_c2_batch_paired_plan_matches_oracle():
+@pytest.mark.parametrize("pad", [0, None])
+def test_forward_c2_batch_paired_plan_matches_oracle(pad, monkeypatch):
     """The C2 configuration at its own batch (B=32, T=512, 6 layers): 128 slabs
-    of two items each fill the chip at one split, and the model's (B, T, nh, N)
-    x_sparse rows are 64 KB apart, so the score pass runs the paired-stage
-    kernel at split 1 (checked in the launch log).  Sequences 0 and 31 against
-    the numpy model oracle within 2e-2."""
-    print("harness C2 batch forward (paired split-1 plan)", flush=True)
+    of two items each fill the chip at one split.  With x_sparse token rows
+    unpadded (64 KB apart) the score pass runs the paired-stage kernel at split
+    1; with the harness's padded rows (the default) the plain one (checked in
+    the launch log).  Sequences 0 and 31 against the numpy model oracle within
+    2e-2, and the two forwards give the same logits."""
+    print(f"harness C2 batch forward (pad {pad})", flush=True)
+    if pad is not None:
+        monkeypatch.setattr(H, "_XS_PAD", pad)
     p = M.init_params(6, 256, 4, 8192, 256, seed=33)
     m = _model(p, mult=128)
     idx = np.random.default_rng(34).integers(0, 256, (32, 512))
@@ -105,7 +109,8 @@ def test_forward_c2_batch_paired_plan_matches_oracle():
         names = {n for n, _ in ext.profile_collect()}
     finally:
         ext.profile_enable(False)
-    assert "k_sy_scores_paired" in names, names
+    assert ("k_sy_scores_paired" if pad == 0 else "k_sy_scores") in names, names
+    assert "k_relu_enc" in names and "k_gated_dec" in names, names
     assert rel_fro(got[[0, 31]].float().cpu().numpy(), M.bdh_forward(p, idx[[0, 31]])) <= 2e-2
 
 
