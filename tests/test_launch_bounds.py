@@ -384,22 +384,29 @@ def check_gated_dec(B, T, nh, N):
                         b, tt = divmod(m, T)
                         yo = b * nh * T * K + h * T * K + tt * K + 8 * hl
                         assert yo + 16 * 15 + 8 <= B * nh * T * K
+                    # the kernel forms these addresses as a per-lane base XOR a compile-time offset
+                    wvb = l32 * 512 + 16 * (hl ^ (l32 & 1)) + 32 * (l32 >> 1)
                     for s in range(16):
                         o = l32 * 512 + 16 * ((2 * s + hl) ^ l32)
+                        assert o == wvb ^ (32 * s)
                         assert 0 <= o and o + 16 <= WV
                     g4, q = lane >> 4, lane & 15
                     drow = 4 * (g4 >> 1) + (q >> 2)
+                    dvb = WV + drow * 512 + 32 * (g4 & 1) + 16 * ((q & 3) >> 1) + 8 * (q & 1) + 64 * (drow & 3)
                     for db in range(8):
                         col = 32 * db + 16 * (g4 & 1) + 4 * (q & 3)
                         o = WV + drow * 512 + (((col >> 3) ^ (4 * (drow & 3))) * 16) + ((col >> 2) & 1) * 8
+                        assert o == dvb ^ (64 * db)
                         for k2 in range(2):
                             for extra in (0, 8 * 512):
                                 p = o + k2 * 16 * 512 + extra
                                 assert WV <= p and p + 8 <= WV + DEC
+                    xvb = WV + DEC + (64 * w + l32) * 64 + 8 * hl + 16 * ((l32 >> 2) & 3)
                     for j in range(2):
                         r = 64 * w + 32 * j + l32
                         for p in range(4):
                             o = WV + DEC + r * 64 + 16 * (p ^ ((r >> 2) & 3)) + 8 * hl
+                            assert o == (xvb + 2048 * j) ^ (16 * p)
                             assert WV + DEC <= o and o + 8 <= SLOT
                         for rr in range(16):
                             m = m0 + 64 * w + 32 * j + 8 * (rr >> 2) + 4 * hl + (rr & 3)
