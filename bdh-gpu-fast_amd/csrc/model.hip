@@ -663,7 +663,10 @@ static int gated_gemm_launch(const bdh_tensor4* y, const bdh_tensor4* wt, const 
   a.per_xcd = (a.total + 7) / 8;
   const int64_t grid = 8 * a.per_xcd;
   if (grid >= (int64_t(1) << 31)) return BDH_ERR_SHAPE;
-  if (relu_enc_takes(K, N) && ((N - 1) * wt->stride[2] + K) * 2 < (int64_t(1) << 32))
+  // The streaming kernel runs one workgroup per (head, 256 tokens) down all N
+  // columns: it needs enough token blocks to fill the chip (a decode step's
+  // few tokens take the tile kernel, whose grid spans the columns too).
+  if (relu_enc_takes(K, N) && (M + 255) / 256 * H >= 128 && ((N - 1) * wt->stride[2] + K) * 2 < (int64_t(1) << 32))
     return relu_enc_launch(y, wt, x, out, static_cast<hipStream_t>(stream));
   if (x != nullptr)
     BDH_LAUNCH("k_gated_gemm", k_gated_gemm<true>, dim3(unsigned(grid)), dim3(512), 0,

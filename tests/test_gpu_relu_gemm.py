@@ -8,10 +8,10 @@ out[b, t, h, n] = relu(sum_k y[b, h, t, k] wt[h, n, k]) as bf16 (bdh.py:861-912,
   move an occasional value across a bf16 rounding boundary);
 * the library's generic tile kernel (k_gated_gemm without the gate), which the
   entry point takes for shapes the streaming kernel does not: the same bounds.
-Shapes: K = 256 and 512 (the streaming kernel), ragged token blocks (B*T not a
-multiple of 256), one token, heads sharing y through a zero head stride (the
-encoder) and per-head y, N down to one chunk, and a K the streaming kernel
-does not take.
+Shapes: K = 256 and 512 on the streaming kernel (ragged last token blocks, N
+down to one chunk), the tile kernel below its workgroup threshold and for K =
+128, one token, heads sharing y through a zero head stride (the encoder) and
+per-head y.
 """
 
 from __future__ import annotations
@@ -45,8 +45,15 @@ def _want(y, wt, nh):
     return torch.relu(lin).permute(0, 2, 1, 3).float().to(BF)
 
 
-@pytest.mark.parametrize("shape", [(2, 300, 4, 1024, 256), (1, 1, 2, 64, 256), (3, 129, 3, 192, 512),
-                                   (1, 512, 8, 8192, 512), (4, 256, 4, 8192, 256), (2, 77, 2, 96, 128)])
+# (B, T, nh, N, K): the streaming kernel takes K = 256 / 512 when (B*T / 256) x nh >= 128
+# workgroups: a ragged last token block (77 and 116 tokens), one chunk (N = 64 at K = 256),
+# two (N = 64 at K = 512); the tile kernel below that (a decode step's 64 tokens, short
+# prompts) and for K = 128.
+STREAM_SHAPES = [(1, 32845, 1, 64, 256), (2, 8250, 2, 64, 512), (4, 8200, 4, 128, 256)]
+TILE_SHAPES = [(2, 300, 4, 1024, 256), (1, 1, 2, 64, 256), (3, 129, 3, 192, 512), (2, 77, 2, 96, 128)]
+
+
+@pytest.mark.parametrize("shape", STREAM_SHAPES + TILE_SHAPES)
 @pytest.mark.parametrize("shared", [True, False])
 def test_relu_gemm_matches_reference(shape, shared):
     B, T, nh, N, K = shape
@@ -66,10 +73,10 @@ def test_relu_gemm_matches_reference(shape, shared):
 
 
 def test_relu_gemm_encoder_view_matches_generic_kernel():
-    """At C2's width: the streaming kernel (N a multiple of 64) against the
-    generic tile kernel on the same rows (N = 8184 goes to it), and repeated
-    calls give the same bits."""
-    B, T, nh, K = 4, 512, 4, 256
+    """At C2's shape (B = 32, T = 512): the streaming kernel (N a multiple of 64)
+    against the generic tile kernel on the same rows (N = 8184 goes to it), and
+    repeated calls give the same bits."""
+    B, T, nh, K = 32, 512, 4, 256
     y, wt = _inputs(B, T, nh, 8192, K, seed=11, shared=True)
     yd = y.to(DEV).expand(B, nh, T, K)
     wd = wt.to(DEV)
@@ -96,8 +103,7 @@ def _want_gated(y, wt, x):
     return (x.float() * r.float()).to(BF)
 
 
-@pytest.mark.parametrize("shape", [(2, 300, 4, 1024, 256), (1, 1, 2, 64, 256), (3, 129, 3, 192, 512),
-                                   (2, 1024, 8, 8192, 512), (2, 77, 2, 96, 128)])
+@pytest.mark.parametrize("shape", STREAM_SHAPES + TILE_SHAPES)
 def test_gated_form_matches_reference(shape):
     """The gated form (x * relu(y wt^T), the encoder_v product of the layer; the
     streaming kernel for K = 256 / 512, the generic tile kernel for K = 128)
@@ -116,10 +122,10 @@ def test_gated_form_matches_reference(shape):
 
 
 def test_gated_form_c5_width_repeats_and_matches_generic():
-    """At C5's width (K = 512, 8 x 8192 columns): repeated calls give the same
-    bits, and the generic tile kernel (N = 8184 goes to it) agrees on the
-    shared columns."""
-    B, T, nh, N, K = 2, 1024, 8, 8192, 512
+    """At C5's shape (B = 4, T = 2048, K = 512, 8 x 8192 columns): repeated
+    calls give the same bits, and the generic tile kernel (N = 8184 goes to it)
+    agrees on the shared columns."""
+    B, T, nh, N, K = 4, 2048, 8, 8192, 512
     y, wt = (t.to(DEV) for t in _inputs(B, T, nh, N, K, seed=5, shared=False))
     g = torch.Generator().manual_seed(9)
     x = torch.relu(torch.randn(B, T, nh, N, generator=g)).to(BF).to(DEV)
@@ -130,3 +136,27 @@ def test_gated_form_c5_width_repeats_and_matches_generic():
     a, b = got[..., :8184], gen
     assert rel_fro(a.float().cpu().numpy(), b.float().cpu().numpy()) <= 1e-2
     assert float((a == b).float().mean()) >= 0.99
+
+
+@pytest.mark.parametrize("tokens", [64, 4096])
+def test_few_tokens_take_the_tile_kernel(tokens):
+    """The streaming kernel needs (tokens / 256) x heads >= 128 workgroups; a
+    decode step's few tokens (64 here, C3's batch) take the tile kernel, a
+    prefill's the streaming one (checked in the launch log); both against
+    float64."""
+    B, T, nh, N, K = tokens, 1, 4, 8192, 256
+    if tokens == 4096:
+        B, T, nh = 8, 512, 8
+    y, wt = _inputs(B, T, nh, N, K, seed=tokens, shared=False)
+    g = torch.Generator().manual_seed(tokens)
+    x = torch.relu(torch.randn(B, T, nh, N, generator=g)).to(BF)
+    ext.profile_enable(True)
+    try:
+        got = ext.gated_gemm(y.to(DEV), wt.to(DEV), x.to(DEV))
+        torch.cuda.synchronize()
+        names = {n for n, _ in ext.profile_collect()}
+    finally:
+        ext.profile_enable(False)
+    assert names == ({"k_gated_gemm"} if tokens == 64 else {"k_gated_enc"}), names
+    want = _want_gated(y, wt, x)
+    assert rel_fro(got.float().cpu().numpy(), want.float().numpy()) <= 1e-2
