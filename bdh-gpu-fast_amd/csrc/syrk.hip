@@ -1293,6 +1293,11 @@ __global__ __launch_bounds__(kSyThreads, 1) void k_dq_sy(const DqsArgs a) {
 // first's through LDS at the end.  Two groups halve the longest workgroup's
 // chain of items (the row block j0 = 0 has H * T / 64 of them) and keep two
 // items' loads in flight per CU.
+// Every row block of one (b, hv) reads the same dO rows, so those workgroups
+// share an XCD (its L2): units u = (b Hv + hv) nrb + rb go to the XCDs in
+// contiguous ranges of per_xcd, and each workgroup walks its i chunks from the
+// last one down, the heads inside, so they read each dO chunk at about the
+// same time.
 struct DvsArgs {
   const bf16_t* part;  // [slab][ntl][nsplit][256*256]
   int ntl, nsplit;
@@ -1302,6 +1307,7 @@ struct DvsArgs {
   int64_t o0, o1, o2;
   int H, Hv, T, D;
   int rel = 0;  // the tiles came from the relative-RoPE score kernel (fragment slot order)
+  int nrb = 0, nbv = 0, per_xcd = 0;  // row blocks, B Hv, units per XCD (grid 8 per_xcd)
 };
 
 template <typename TO, int NS>
@@ -1310,7 +1316,10 @@ __global__ __launch_bounds__(512) void k_dv_sy(const DvsArgs a) {
   // M [i][j] (16-byte chunk c at c ^ 2 (i & 3)) and dO [i][d] (chunk c at c ^ 4 (i & 3))
   constexpr int kBlk = 64 * 128 + 64 * 512;
   __shared__ __attribute__((aligned(16))) uint8_t dv_lds[2 * kBlk];
-  const int rb = blockIdx.x, bv = blockIdx.y;
+  // workgroup L runs on XCD L % 8 (round robin by linear id)
+  const int L = blockIdx.x, u = (L & 7) * a.per_xcd + (L >> 3);
+  if (u >= a.nrb * a.nbv) return;
+  const int bv = u / a.nrb, rb = u - bv * a.nrb;
   const int b = bv / a.Hv, hv = bv - b * a.Hv;
   const int j0 = rb * 64;
   const int tid = threadIdx.x, grp = tid >> 8, gt = tid & 255, w = gt >> 6, lane = tid & 63;
@@ -1319,11 +1328,12 @@ __global__ __launch_bounds__(512) void k_dv_sy(const DvsArgs a) {
   const int h_lo = a.Hv == 1 ? 0 : hv, h_hi = a.Hv == 1 ? a.H : hv + 1;
   const int ic0 = j0 / 64, nic = (a.T + 63) / 64;  // chunks of i: i >= j0 (i > j)
   const int tj = j0 >> 8;
-  // items it = (head h_lo + it / per_h, chunk ic0 + it % per_h); group g takes
+  // items it = (chunk nic - 1 - it / nhv, head h_lo + it % nhv); group g takes
   // items g, g + 2, ... (ng of them), both groups step together (nk steps)
-  const int per_h = nic - ic0;
-  const int total = per_h * (h_hi - h_lo);
+  const int nhv = h_hi - h_lo;
+  const int total = (nic - ic0) * nhv;
   const int ng = (total - grp + 1) / 2, nk = (total + 1) / 2;
+  auto item_ic = [&](int it) { return nic - 1 - it / nhv; };
 
   // builder roles: M pieces (fragment-ordered partial tiles, see sy_piece):
   // piece e of this thread is 32 x 32 block mbi = (gt + 256 e) / 128 of the
@@ -1336,7 +1346,7 @@ __global__ __launch_bounds__(512) void k_dv_sy(const DvsArgs a) {
   // L2 hit, not used); splits past nsplit re-read the last split (not summed).
   auto load_chunk = [&](int itq) {
     const int it = min(itq, total - 1);
-    const int h = h_lo + it / per_h, ic = ic0 + it % per_h;
+    const int ic = item_ic(it), h = h_lo + it - (nic - 1 - ic) * nhv;
     const int i0 = ic * 64;
     const int ti = i0 >> 8;
     const int slab = b * a.H + h;
@@ -1362,7 +1372,7 @@ __global__ __launch_bounds__(512) void k_dv_sy(const DvsArgs a) {
     }
   };
   auto store_chunk = [&](int it, bool live) {
-    const int ic = ic0 + min(it, total - 1) % per_h;
+    const int ic = item_ic(min(it, total - 1));
 #pragma unroll
     for (int e = 0; e < 2; ++e) {
       float sacc[8];
@@ -1467,6 +1477,181 @@ __global__ __launch_bounds__(512) void k_dv_sy(const DvsArgs a) {
       }
 }
 
+// dV from score tiles of one split through an LDS ring: the k_dv_sy work
+// (64 rows j of dV[b, hv] per workgroup, all D <= 256 columns; the same
+// units per XCD and the same item order) with every operand moved by DMA.
+// Per item the four 32 x 32 blocks of M, as the score kernel stored them
+// (MFMA accumulator order, 2 KB a block), and the 64 dO rows (512-byte rows,
+// 16-byte chunk c at c ^ 4 (i & 3)) go to a ring of three stages, two items
+// in flight while one is multiplied.  A stored accumulator half (1 KB) is an A
+// operand of M^T as it stands: lane l holds column j = l % 32 and rows
+// 16 hf + 8 (t / 4) + 4 (l / 32) + t % 4 of the block for t = 0..7, so the
+// MFMA's contraction index 8 (l / 32) + t runs over those rows, and the B
+// operand (dO) is read in the same row order (two transposing reads eight
+// rows apart).  Waves 0-3 contract rows 0-31 of each item, waves 4-7 rows
+// 32-63; wave w & 3 owns columns [64 (w & 3), +64) and both 32-row halves of
+// j.  Entries with i <= j (the diagonal chunk, whose block above the diagonal
+// is not stored: the diagonal block is read in its place) or i >= T are
+// zeroed in the A registers.  At the end the two halves' sums meet in LDS and
+// the 64 x D tile leaves in 16-byte stores.
+constexpr int kDvStage = 8192 + 64 * 512;  // M blocks + dO rows
+constexpr int kDvRing = 3;
+constexpr int kDvPitch = 1056;  // output tile row pitch in bytes (rows 4 apart on other banks)
+
+template <typename TO>
+__global__ __launch_bounds__(512, 1) void k_dv_dma(const DvsArgs a) {
+  __shared__ __attribute__((aligned(1024))) uint8_t dv_ring[kDvRing * kDvStage];
+  const int L = blockIdx.x, u = (L & 7) * a.per_xcd + (L >> 3);
+  if (u >= a.nrb * a.nbv) return;
+  const int bv = u / a.nrb, rb = u - bv * a.nrb;
+  const int b = bv / a.Hv, hv = bv - b * a.Hv;
+  const int j0 = rb * 64, tj = j0 >> 8;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int h_lo = a.Hv == 1 ? 0 : hv, nhv = a.Hv == 1 ? a.H : 1;
+  const int nic = (a.T + 63) / 64;
+  const int total = (nic - rb) * nhv;
+  const uint32_t lds0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_u8*)dv_ring);
+
+  // DMA roles: wave w moves half w & 1 of M block (ib, jb) = (w >> 2, (w >> 1) & 1)
+  // and dO rows 8 w + 2 v + lane / 32 (v = 0..3); chunks past D re-read the last one
+  const int mhf = w & 1, cbk = ((j0 & 255) >> 5) + ((w >> 1) & 1), mib = w >> 2;
+  int drow[4];
+  uint32_t dcol[4];
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    const int r = 8 * w + 2 * v + (lane >> 5);
+    drow[v] = r;
+    dcol[v] = uint32_t(min((lane & 31) ^ (4 * (r & 3)), a.D / 8 - 1) * 16);
+  }
+  auto issue = [&](int it, int slot) __attribute__((always_inline)) {
+    const int c = it / nhv, ic = nic - 1 - c, h = h_lo + it - c * nhv;
+    const int i0 = ic * 64, ti = i0 >> 8;
+    const bool dt = ti == tj;
+    const int rbk = ((i0 & 255) >> 5) + mib;
+    const bf16_t* tile = a.part + (int64_t(b * a.H + h) * a.ntl + ti * (ti + 1) / 2 + tj) * kSyTileElems;
+    const int off = sy_piece(dt, a.rel, rbk, dt && cbk > rbk ? rbk : cbk, lane, mhf);
+    const uint32_t sb = lds0 + uint32_t(slot * kDvStage);
+    dma16<0>(sb + uint32_t(w) * 1024u, sgpr_ptr(tile), uint32_t(off * 2));
+    const void* dob = sgpr_ptr(a.dO + b * a.d0 + h * a.d1);
+    const uint32_t dm0 = sb + 8192u + uint32_t(w) * 4096u;
+    dma16<0>(dm0, dob, uint32_t(min(i0 + drow[0], a.T - 1)) * uint32_t(a.d2 * 2) + dcol[0]);
+    dma16<1024>(dm0, dob, uint32_t(min(i0 + drow[1], a.T - 1)) * uint32_t(a.d2 * 2) + dcol[1]);
+    dma16<2048>(dm0, dob, uint32_t(min(i0 + drow[2], a.T - 1)) * uint32_t(a.d2 * 2) + dcol[2]);
+    dma16<3072>(dm0, dob, uint32_t(min(i0 + drow[3], a.T - 1)) * uint32_t(a.d2 * 2) + dcol[3]);
+  };
+
+  // fragments: A (M^T) halves of blocks (kq, jb); B (dO) rows 16 ks + 4 (l / 32)
+  // + q / 4 and 8 below, columns 64 wc + 32 c + 16 ((l / 16) & 1) + 4 (q % 4)
+  const int kq = w >> 2, wc = w & 3;
+  const int g4 = lane >> 4, q = lane & 15;
+  uint32_t boff[2];
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+    const int row = 4 * (g4 >> 1) + (q >> 2);
+    const int col = 64 * wc + 32 * c + 16 * (g4 & 1) + 4 * (q & 3);
+    boff[c] = uint32_t(8192 + row * 512 + (((col >> 3) ^ (4 * (row & 3))) * 16) + ((col >> 2) & 1) * 8);
+  }
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][c][r] = 0.f;
+
+  issue(0, 0);
+  if (total > 1) issue(1, 1);
+  int slot = 0;
+  for (int k = 0; k < total; ++k) {
+    if (k + 1 < total) sy_wait<5>();  // item k landed, item k + 1 in flight
+    else sy_wait<0>();
+    __syncthreads();  // item k in every wave's view; item k - 1's stage is free
+    if (k + 2 < total) issue(k + 2, slot == 0 ? 2 : slot - 1);
+    const int ic = nic - 1 - k / nhv;
+    const bool msk = ic == rb || ic * 64 + 64 > a.T;  // uniform
+    const uint32_t sb = lds0 + uint32_t(slot * kDvStage);
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+      const int ks = 2 * kq + hf;
+      bf16x8 fa[2], fb[2];
+#pragma unroll
+      for (int jb = 0; jb < 2; ++jb) {
+        fa[jb] = *reinterpret_cast<const lds_bf16x8*>(lds_at(sb + uint32_t(((2 * kq + jb) * 2 + hf) * 1024 + lane * 16)));
+        if (msk) {
+          u32x4 wv = __builtin_bit_cast(u32x4, fa[jb]);
+          const int ib0 = ic * 64 + 16 * ks + 4 * (lane >> 5);
+          const int gj = j0 + 32 * jb + (lane & 31);
+#pragma unroll
+          for (int p = 0; p < 4; ++p) {
+            const int il = ib0 + 8 * (p >> 1) + 2 * (p & 1);
+            const uint32_t keep = ((il > gj && il < a.T) ? 0xffffu : 0u) | ((il + 1 > gj && il + 1 < a.T) ? 0xffff0000u : 0u);
+            wv[p] &= keep;
+          }
+          fa[jb] = __builtin_bit_cast(bf16x8, wv);
+        }
+      }
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        const lds_u8* pb = lds_at(sb + boff[c] + uint32_t(ks * 16 * 512));
+        fb[c] = __builtin_shufflevector(lds_tr4(pb), lds_tr4(pb + 8 * 512), 0, 1, 2, 3, 4, 5, 6, 7);
+      }
+#pragma unroll
+      for (int jb = 0; jb < 2; ++jb)
+#pragma unroll
+        for (int c = 0; c < 2; ++c) acc[jb][c] = mma(fa[jb], fb[c], acc[jb][c]);
+    }
+    slot = slot == 2 ? 0 : slot + 1;
+  }
+
+  // the two row halves' sums into one fp32 tile [64 j][pitch], then 16-byte stores
+  __syncthreads();  // every wave's last fragment reads are done (its DMA waited above)
+  float* const tl = reinterpret_cast<float*>(dv_ring);
+  constexpr int PF = kDvPitch / 4;
+  auto tile_idx = [&](int jb, int c, int r) {
+    return (32 * jb + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)) * PF + 64 * wc + 32 * c + (lane & 31);
+  };
+  if (kq == 1) {
+#pragma unroll
+    for (int jb = 0; jb < 2; ++jb)
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) tl[tile_idx(jb, c, r)] = acc[jb][c][r];
+  }
+  __syncthreads();
+  if (kq == 0) {
+#pragma unroll
+    for (int jb = 0; jb < 2; ++jb)
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) tl[tile_idx(jb, c, r)] += acc[jb][c][r];
+  }
+  __syncthreads();
+  TO* o = static_cast<TO*>(a.o) + b * a.o0 + hv * a.o1;
+  if constexpr (sizeof(TO) == 2) {
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int e = tid + 512 * v, row = e >> 5, cc = e & 31;
+      if (j0 + row < a.T && 8 * cc < a.D) {
+        const f32x4 x0 = *reinterpret_cast<const f32x4*>(tl + row * PF + 8 * cc);
+        const f32x4 x1 = *reinterpret_cast<const f32x4*>(tl + row * PF + 8 * cc + 4);
+        *reinterpret_cast<u32x4*>(o + int64_t(j0 + row) * a.o2 + 8 * cc) =
+            u32x4{pack_bf2(x0[0], x0[1]), pack_bf2(x0[2], x0[3]), pack_bf2(x1[0], x1[1]), pack_bf2(x1[2], x1[3])};
+      }
+    }
+  } else {
+#pragma unroll
+    for (int v = 0; v < 8; ++v) {
+      const int e = tid + 512 * v, row = e >> 6, cc = e & 63;
+      if (j0 + row < a.T && 4 * cc < a.D)
+        *reinterpret_cast<f32x4*>(o + int64_t(j0 + row) * a.o2 + 4 * cc) =
+            *reinterpret_cast<const f32x4*>(tl + row * PF + 4 * cc);
+    }
+  }
+}
+
 // ------------------------------------------------------------- score x V
 // out rows [64 rb, +64) of one (b,h) slab, all D (<= 256) columns.  Keys go
 // in chunks of 64.  The 512 threads first stage the chunk in LDS: the score
@@ -1505,15 +1690,16 @@ __global__ __launch_bounds__(512, 1) void k_sy_sv(const SvArgs a) {
   uint8_t* const vblk = sv_lds + 64 * 128;   // 64 x 512 bytes
   float* const red = reinterpret_cast<float*>(sv_lds);
   constexpr int VL = sizeof(TV) == 2 ? 1 : 2;  // 16-byte loads per 8 V elements
-  // Workgroups go to the XCDs round robin by linear id L.  The row blocks of
-  // slab s run on XCD s % 8, the XCD whose L2 took the slab's partial tiles
-  // in the score kernel.  On each XCD the row blocks go longest first (block
-  // rb has rb + 1 key chunks): the k-th workgroup of XCD x is slab
-  // 8 (k % nsx) + x, block nrbk - 1 - k / nsx, so when the grid takes more than
-  // one round of the CUs the last workgroups to start are the short ones.
+  // Workgroups go to the XCDs round robin by linear id L.  XCD x takes the
+  // slabs [x nsx, (x + 1) nsx), consecutive heads of one batch element, which
+  // read the same V rows (one L2 holds them).  On each XCD the row blocks go
+  // longest first (block rb has rb + 1 key chunks): the k-th workgroup of XCD
+  // x is slab x nsx + k % nsx, block nrbk - 1 - k / nsx, so when the grid takes
+  // more than one round of the CUs the last workgroups to start are the short
+  // ones.
   const int nrbk = a.nrbk, nsx = (a.nslab + 7) / 8;
   const int L = blockIdx.x, xcdv = L & 7, kk = L >> 3;
-  const int slab = (kk % nsx) * 8 + xcdv;
+  const int slab = xcdv * nsx + kk % nsx;
   if (slab >= a.nslab) return;
   const int rb = nrbk - 1 - kk / nsx + a.rb0;
   const int b = slab / a.H, h = slab - b * a.H, hv = a.Hv == 1 ? 0 : h;
@@ -2251,9 +2437,16 @@ int sy_bwd_dv(const bdh_tensor4* q, const bdh_tensor4* v, const bdh_tensor4* dou
   d.T = int(T);
   d.D = int(D);
   d.rel = saved != nullptr ? rel : 0;
-  const dim3 gd(unsigned((T + 63) / 64), unsigned(B * Hv));
+  d.nrb = int((T + 63) / 64);
+  d.nbv = int(B * Hv);
+  d.per_xcd = int((int64_t(d.nrb) * d.nbv + 7) / 8);
+  const dim3 gd(unsigned(8 * d.per_xcd));
   const bool o16 = dv->dtype == BDH_BF16;
-  if (p.nsplit == 1) {
+  // one split, 16-byte output rows and dO offsets within 32 bits: the DMA ring
+  if (p.nsplit == 1 && rows16(dv) && ((T - 1) * dout->stride[2] + D) * 2 < (int64_t(1) << 32)) {
+    if (o16) BDH_LAUNCH("k_dv_dma", (k_dv_dma<bf16_t>), gd, dim3(512), 0, s, d);
+    else BDH_LAUNCH("k_dv_dma", (k_dv_dma<float>), gd, dim3(512), 0, s, d);
+  } else if (p.nsplit == 1) {
     if (o16) BDH_LAUNCH("k_dv_sy", (k_dv_sy<bf16_t, 1>), gd, dim3(512), 0, s, d);
     else BDH_LAUNCH("k_dv_sy", (k_dv_sy<float, 1>), gd, dim3(512), 0, s, d);
   } else if (p.nsplit <= 2) {

@@ -892,7 +892,7 @@ def run_pmc_targets(torch, ext, kernels, dev, reps: int = 3) -> None:
         kernels.bdh_attn_rope(x5, v5, f5, 0, impl="hip")
     del x5, v5
     section_end()
-    # C4 training op (k_sy_scores, k_dv_sy, G, k_dq_sy)
+    # C4 training op (k_sy_scores, k_sy_sv, k_dv_dma, G, k_dq_sy)
     B4, n4, T4, N4, D4 = (C4[k] for k in ("B", "nh", "T", "N", "D"))
     q4 = torch.relu(0.32 * torch.randn(B4, n4, T4, N4, generator=g, device=dev)).to(bf)
     v4 = torch.randn(B4, 1, T4, D4, generator=g, device=dev).to(bf)

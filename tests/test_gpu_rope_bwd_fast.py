@@ -69,7 +69,7 @@ def test_rope_backward_mfma_route_matches_oracle(shape):
     xd, vd, dd = to_dev(x, BF), to_dev(v, BF), to_dev(dO, BF)
     fd = torch.from_numpy(f).to(DEV)
     (dx, dv), names = _names(lambda: ext.tril_rope_score_v_bwd(xd, vd, dd, fd, start))
-    assert "k_dq_sy" in names and "k_dv_sy" in names, names
+    assert "k_dq_sy" in names and names & {"k_dv_sy", "k_dv_dma"}, names
     wx, wv = O.tril_rope_score_v_backward(x, v, dO, f, start)
     ex, ev = rel_fro(np_of(dx), wx), rel_fro(np_of(dv), wv)
     print(f"  dx rel {ex:.3e}, dv rel {ev:.3e}", flush=True)
@@ -161,7 +161,7 @@ def test_rope_backward_from_saved_tiles(shape):
     assert scores is not None
     assert torch.equal(out, ext.tril_rope_score_v(xd, vd, fd, start))
     (sx, sv), names = _names(lambda: ext.tril_rope_score_v_bwd_saved(xd, vd, dd, fd, start, scores))
-    assert "k_dq_sy" in names and "k_dv_sy" in names, names
+    assert "k_dq_sy" in names and names & {"k_dv_sy", "k_dv_dma"}, names
     assert "k_rope_table" not in names, names
     assert not any(n.startswith("k_sy_scores") and n != "k_sy_scores_g" for n in names), names
     rx, rv = ext.tril_rope_score_v_bwd(xd, vd, dd, fd, start)
@@ -217,7 +217,7 @@ def test_rope_backward_from_saved_tiles_absolute_layout():
     assert scores is not None
     assert torch.equal(out, ext.tril_rope_score_v(xd, vd, fd, start))
     (sx, sv), names = _names(lambda: ext.tril_rope_score_v_bwd_saved(xd, vd, dd, fd, start, scores))
-    assert "k_dq_sy" in names and "k_dv_sy" in names, names
+    assert "k_dq_sy" in names and names & {"k_dv_sy", "k_dv_dma"}, names
     rx, rv = ext.tril_rope_score_v_bwd(xd, vd, dd, fd, start)
     assert torch.equal(sx, rx)
     assert rel_fro(np_of(sv), np_of(rv)) <= TOL

@@ -4,7 +4,7 @@ CPU only: the launch plans and index formulas of the kernels the harness's
 HIP legs run (csrc/syrk.hip: k_sy_scores work items, their x loads and
 partial-tile stores, k_sy_sv's partial, V and output accesses;
 csrc/decode.hip: k_decode_bf16's key, q and partial accesses; the training
-backward's k_dq_sy B loads on x and k_dv_sy; csrc/model.hip: k_gated_gemm's
+backward's k_dq_sy B loads on x, k_dv_sy and k_dv_dma; csrc/model.hip: k_gated_gemm's
 LDS-DMA operand loads and epilogue x loads; csrc/gated_dec.hip: k_gated_dec's
 grid, operand DMA, LDS fragment reads and partial stores; csrc/enc.hip: k_relu_enc's grid,
 encoder DMA, fragment and tile accesses and output stores) are restated here and evaluated over every
@@ -14,6 +14,7 @@ capacity-strided past views).  Each access must fall inside its buffer and
 every score tile must be computed exactly once.
 """
 
+import numpy as np
 import pytest
 
 TILE, TILE_ELEMS = 256, 256 * 256
@@ -117,7 +118,7 @@ def sv_grid(nslab, nrb):
     nsx = (nslab + 7) // 8
     for L in range(8 * nsx * nrb):
         xcd, kk = L & 7, L >> 3
-        slab = (kk % nsx) * 8 + xcd
+        slab = xcd * nsx + kk % nsx
         out.append(None if slab >= nslab else (nrb - 1 - kk // nsx, slab))
     return out
 
@@ -128,11 +129,13 @@ def check_sv(B, nh, T, D, p, v_strides, v_numel):
     nrb = (T + 63) // 64
     S, ntl = p["nsplit"], p["ntl"]
     part_elems = nslab * ntl * S * TILE_ELEMS
-    # the 1-D grid visits each (row block, slab) once; slab s sits on XCD s % 8
+    # the 1-D grid visits each (row block, slab) once; XCD x holds the slabs
+    # [x nsx, (x + 1) nsx), row blocks longest first
     grid = sv_grid(nslab, nrb)
     live = [g for g in grid if g is not None]
     assert sorted(live) == sorted((rb, s) for s in range(nslab) for rb in range(nrb))
-    assert all(g[1] % 8 == L % 8 for L, g in enumerate(grid) if g is not None)
+    nsx = (nslab + 7) // 8
+    assert all(g[1] // nsx == L % 8 for L, g in enumerate(grid) if g is not None)
     # on each XCD the row blocks (rb + 1 key chunks each) start longest first
     for x in range(8):
         rbs = [g[0] for L, g in enumerate(grid) if L % 8 == x and g is not None]
@@ -236,31 +239,122 @@ def check_dq_rot(B, nh, T, N, x_strides, x_numel, tpad):
 
 
 def check_dv(B, nh, Hv, T, N, D, p):
-    """csrc/syrk.hip k_dv_sy: grid (T / 64, B Hv), two groups taking items g, g + 2, ...
-    of (head, 64-row chunk ic >= rb); loads of item min(it, total - 1); M pieces of tile
+    """csrc/syrk.hip k_dv_sy: 1-D grid of 8 per_xcd workgroups, workgroup L the unit
+    u = (L % 8) per_xcd + L / 8 = bv nrb + rb (units past nrb B Hv return), every unit
+    taken once; two groups taking items g, g + 2, ... of (64-row chunk nrb - 1 - it / nhv
+    >= rb, head h_lo + it % nhv); loads of item min(it, total - 1); M pieces of tile
     (ti, tj), ti >= tj, splits < nsplit; dO rows < T (others zero); dV rows < T."""
     nrb = (T + 63) // 64
+    nbv = B * Hv
+    per_xcd = (nrb * nbv + 7) // 8
+    units = [(L % 8) * per_xcd + L // 8 for L in range(8 * per_xcd)]
+    units = [u for u in units if u < nrb * nbv]
+    assert sorted(units) == list(range(nrb * nbv))
     S, ntl = p["nsplit"], p["ntl"]
     part_elems = B * nh * ntl * S * TILE_ELEMS
-    for rb in range(nrb):
-        for bv in range(B * Hv):
-            b, hv = divmod(bv, Hv)
-            h_lo, h_hi = (0, nh) if Hv == 1 else (hv, hv + 1)
-            per_h = nrb - rb
-            total = per_h * (h_hi - h_lo)
-            assert total >= 1
-            for grp in (0, 1):
-                nk = (total + 1) // 2
-                for k in range(nk + 1):  # steps plus the load issued after the last one
-                    it = min(grp + 2 * k, total - 1)
-                    h, ic = h_lo + it // per_h, rb + it % per_h
-                    assert h_lo <= h < h_hi and rb <= ic < nrb
-                    ti, tj = (ic * 64) >> 8, (rb * 64) >> 8
-                    assert tj <= ti
-                    slab = b * nh + h
-                    tile = ti * (ti + 1) // 2 + tj
-                    top = ((slab * ntl + tile) * S + S - 1) * TILE_ELEMS + 63 * 1024 + 512 + 63 * 8 + 8
-                    assert top <= part_elems
+    for u in units:
+        bv, rb = divmod(u, nrb)
+        b, hv = divmod(bv, Hv)
+        h_lo, h_hi = (0, nh) if Hv == 1 else (hv, hv + 1)
+        nhv = h_hi - h_lo
+        total = (nrb - rb) * nhv
+        assert total >= 1
+        seen = set()
+        for grp in (0, 1):
+            nk = (total + 1) // 2
+            for k in range(nk + 1):  # steps plus the load issued after the last one
+                it = min(grp + 2 * k, total - 1)
+                ic = nrb - 1 - it // nhv
+                h = h_lo + it - (nrb - 1 - ic) * nhv
+                assert h_lo <= h < h_hi and rb <= ic < nrb
+                if grp + 2 * k < total:
+                    seen.add((h, ic))
+                ti, tj = (ic * 64) >> 8, (rb * 64) >> 8
+                assert tj <= ti
+                slab = b * nh + h
+                tile = ti * (ti + 1) // 2 + tj
+                top = ((slab * ntl + tile) * S + S - 1) * TILE_ELEMS + 63 * 1024 + 512 + 63 * 8 + 8
+                assert top <= part_elems
+        assert seen == {(h, ic) for h in range(h_lo, h_hi) for ic in range(rb, nrb)}
+
+
+DV_STAGE, DV_RING, DV_PITCH = 8192 + 64 * 512, 3, 1056
+
+
+def check_dv_dma(B, nh, Hv, T, N, D, p, d_strides, d_numel):
+    """csrc/syrk.hip k_dv_dma (one split): the units and items of k_dv_sy; per item
+    wave w moves half w & 1 of M block (w >> 2, (w >> 1) & 1) (one 1 KB DMA inside its
+    tile) and dO rows 8 w + 2 v + lane / 32, clamped to T - 1, chunk (lane % 32) ^
+    4 (row & 3) clamped to D / 8 - 1, into stage slot (item % 3) of the 120 KB ring;
+    fragment reads and the 64 x 1056-byte output tile stay in the ring; the A operand's
+    rows (16 hf + 8 (t / 4) + 4 (l / 32) + t % 4) are the stored accumulator rows."""
+    assert p["nsplit"] == 1
+    nrb = (T + 63) // 64
+    nbv = B * Hv
+    per_xcd = (nrb * nbv + 7) // 8
+    units = sorted(u for u in ((L % 8) * per_xcd + L // 8 for L in range(8 * per_xcd)) if u < nrb * nbv)
+    assert units == list(range(nrb * nbv))
+    ntl = p["ntl"]
+    part_bytes = B * nh * ntl * TILE_ELEMS * 2
+    lane = np.arange(64)
+    for u in units:
+        bv, rb = divmod(u, nrb)
+        b, hv = divmod(bv, Hv)
+        h_lo, nhv = (0, nh) if Hv == 1 else (hv, 1)
+        total = (nrb - rb) * nhv
+        for it in range(total):
+            c = it // nhv
+            ic, h = nrb - 1 - c, h_lo + it - c * nhv
+            assert rb <= ic < nrb
+            ti, tj = (ic * 64) >> 8, (rb * 64) >> 8
+            assert tj <= ti
+            tile = ((b * nh + h) * ntl + ti * (ti + 1) // 2 + tj) * TILE_ELEMS * 2
+            # slot index < 64, half < 2: the 1 KB piece ends inside the tile
+            assert tile + 63 * 2048 + 1024 + 63 * 16 + 16 <= part_bytes
+            slot = it % DV_RING
+            for w in range(8):
+                assert slot * DV_STAGE + w * 1024 + 1024 <= slot * DV_STAGE + 8192
+                for v in range(4):
+                    r = 8 * w + 2 * v + lane // 32
+                    row = np.minimum(ic * 64 + r, T - 1)
+                    cc = np.minimum((lane % 32) ^ (4 * (r & 3)), D // 8 - 1)
+                    off = row * d_strides[2] + 8 * cc
+                    assert int((b * d_strides[0] + h * d_strides[1] + off + 8).max()) <= d_numel
+                    assert int((off * 2 + 16).max()) < 2 ** 32
+                    assert slot * DV_STAGE + 8192 + 4096 * w + 1024 * v + 64 * 16 <= (slot + 1) * DV_STAGE
+    # fragment reads inside a stage: A halves, B transposing reads (row 4 g + q / 4, 8 below)
+    for w in range(8):
+        kq, wc = w >> 2, w & 3
+        for hf in (0, 1):
+            ks = 2 * kq + hf
+            for jb in (0, 1):
+                assert ((2 * kq + jb) * 2 + hf) * 1024 + 63 * 16 + 16 <= 8192
+            for c in (0, 1):
+                g4, q = lane >> 4, lane & 15
+                row = 4 * (g4 >> 1) + (q >> 2)
+                col = 64 * wc + 32 * c + 16 * (g4 & 1) + 4 * (q & 3)
+                boff = 8192 + row * 512 + (((col >> 3) ^ (4 * (row & 3))) * 16) + ((col >> 2) & 1) * 8
+                assert int((boff + ks * 16 * 512 + 8 * 512 + 8).max()) <= DV_STAGE
+                # the B rows of lane l, value t are the A rows of the same (l / 32, t)
+                for t in range(8):
+                    brow = 16 * ks + 4 * (lane >> 5) + 8 * (t >> 2) + (t & 3)
+                    arow = 32 * kq + 16 * hf + 8 * (t >> 2) + 4 * (lane >> 5) + (t & 3)
+                    assert (brow == arow).all()
+    # the stored accumulator rows of value t = 2 qq + e of half hf, lane l
+    for l in range(64):
+        for hf in (0, 1):
+            for t in range(8):
+                r = 2 * (4 * hf + t // 2) + t % 2
+                stored = 8 * (r >> 2) + 4 * (l >> 5) + (r & 3)
+                assert stored == 16 * hf + 8 * (t >> 2) + 4 * (l >> 5) + (t & 3)
+    assert 64 * DV_PITCH <= DV_RING * DV_STAGE and DV_PITCH % 16 == 0
+
+
+@pytest.mark.parametrize("B,nh,Hv,T,N,D", [(16, 4, 1, 1024, 256, 256), (8, 4, 1, 1000, 256, 192), (8, 4, 4, 700, 256, 64),
+                                            (130, 1, 1, 33, 256, 128), (32, 4, 1, 512, 8192, 256)])
+def test_dv_ring_launches_stay_in_bounds(B, nh, Hv, T, N, D):
+    p = sy_plan(B * nh, T, N)
+    check_dv_dma(B, nh, Hv, T, N, D, p, (nh * T * D, T * D, D), B * nh * T * D)
 
 
 @pytest.mark.parametrize("B,nh,T,N,D", [(32, 4, 512, 8192, 256), (3, 2, 300, 512, 64), (1, 3, 700, 768, 256)])
