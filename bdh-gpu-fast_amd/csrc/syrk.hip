@@ -1927,6 +1927,193 @@ __global__ __launch_bounds__(512, 1) void k_sy_sv(const SvArgs a) {
   }
 }
 
+// score x V from score tiles of one split through an LDS ring, V in bf16:
+// the k_sy_sv work (64 output rows of one slab per workgroup, all D <= 256
+// columns, key chunks of 64, the same grid) with every operand moved by DMA,
+// in the stage layout of k_dv_dma: per chunk the four 32 x 32 blocks of M as
+// the score kernel stored them (MFMA accumulator order) and the 64 V rows
+// (512-byte rows, chunk c at c ^ 4 (j & 3)), three chunks in the ring.  The
+// A operand (M, rows i, contracting over keys j) comes out of the stored
+// accumulator order by transposing reads: within a group of 16 lanes, lane
+// s = 4 e + m reads the 8 bytes that hold rows 4 m .. 4 m + 3 (of the group's
+// 16) of key jbase + e, which sit in stored lane jbase + e + 32 (m & 1), bytes
+// 8 (m >> 1) ..; the read hands lane q row q's four consecutive keys.  Stored
+// lane L' of half hf lands in LDS slot L' ^ 4 (L' / 32) ^ 8 hf (the DMA lane
+// loads the stored lane that belongs in its slot), which puts the two 64-byte
+// runs of a group and the two halves on different banks.  Waves 0-3 contract
+// the chunk's keys 0-31, waves 4-7 keys 32-63; wave w & 3 owns columns
+// [64 (w & 3), +64) and both 32-row halves.  Entries with j >= i or i >= T are
+// zeroed in the A registers; the two key halves' sums meet in LDS and leave in
+// 16-byte stores (rows below past not stored, row i at i - past).
+template <typename TO>
+__global__ __launch_bounds__(512, 1) void k_sv_dma(const SvArgs a) {
+  __shared__ __attribute__((aligned(1024))) uint8_t sv_ring[kDvRing * kDvStage];
+  const int nrbk = a.nrbk, nsx = (a.nslab + 7) / 8;
+  const int L = blockIdx.x, xcdv = L & 7, kk = L >> 3;
+  const int slab = xcdv * nsx + kk % nsx;
+  if (slab >= a.nslab) return;
+  const int rb = nrbk - 1 - kk / nsx + a.rb0;
+  const int b = slab / a.H, h = slab - b * a.H, hv = a.Hv == 1 ? 0 : h;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r0 = rb * 64, ti = r0 >> 8;
+  const int nch = (min(a.T, r0 + 64) + 63) / 64;
+  const bf16_t* pslab = a.part + int64_t(slab) * a.ntl * kSyTileElems;
+  const void* vbase = sgpr_ptr(static_cast<const bf16_t*>(a.v.p) + b * a.v.s0 + hv * a.v.s1);
+  const uint32_t lds0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_u8*)sv_ring);
+
+  // DMA roles: wave w moves half w & 1 of M block (ib, jb) = (w >> 2, (w >> 1) & 1)
+  // (DMA lane l takes stored lane l ^ 4 (l / 32) ^ 8 hf) and V rows 8 w + 2 v + lane / 32
+  const int mhf = w & 1, mjb = (w >> 1) & 1;
+  const int rbk = ((r0 & 255) >> 5) + (w >> 2);
+  const int mlane = lane ^ (4 * (lane >> 5)) ^ (8 * mhf);
+  int vrow[4];
+  uint32_t vcol[4];
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    const int r = 8 * w + 2 * v + (lane >> 5);
+    vrow[v] = r;
+    vcol[v] = uint32_t(min((lane & 31) ^ (4 * (r & 3)), a.D / 8 - 1) * 16);
+  }
+  const uint32_t vpitch = uint32_t(a.v.s2 * 2);
+  auto issue = [&](int ck, int slot) __attribute__((always_inline)) {
+    const int j0 = ck * 64, tj = j0 >> 8;
+    const bool dt = a.self && ti == tj;
+    const int cbk = ((j0 & 255) >> 5) + mjb;
+    const bf16_t* tile = pslab + int64_t(ti * (ti + 1) / 2 + tj - a.t0) * kSyTileElems;
+    const int off = sy_piece(dt, a.rel, rbk, dt && cbk > rbk ? rbk : cbk, mlane, mhf);
+    const uint32_t sb = lds0 + uint32_t(slot * kDvStage);
+    dma16<0>(sb + uint32_t(w) * 1024u, sgpr_ptr(tile), uint32_t(off * 2));
+    const uint32_t vm0 = sb + 8192u + uint32_t(w) * 4096u;
+    dma16<0>(vm0, vbase, uint32_t(min(j0 + vrow[0], a.T - 1)) * vpitch + vcol[0]);
+    dma16<1024>(vm0, vbase, uint32_t(min(j0 + vrow[1], a.T - 1)) * vpitch + vcol[1]);
+    dma16<2048>(vm0, vbase, uint32_t(min(j0 + vrow[2], a.T - 1)) * vpitch + vcol[2]);
+    dma16<3072>(vm0, vbase, uint32_t(min(j0 + vrow[3], a.T - 1)) * vpitch + vcol[3]);
+  };
+
+  // fragment reads: A (M) transposing reads of stored blocks (ib, kh), key
+  // steps kk, halves r of the eight keys; B (V) rows 16 ks + 8 (l / 32) + q / 4
+  // and 4 below, columns 64 wc + 32 c + 16 ((l / 16) & 1) + 4 (q % 4)
+  const int kh = w >> 2, wc = w & 3;
+  const int g4 = lane >> 4, q = lane & 15;
+  uint32_t aoff[2][2];
+#pragma unroll
+  for (int k2 = 0; k2 < 2; ++k2)
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const int hf = g4 & 1;
+      const int sl = 16 * k2 + 8 * (g4 >> 1) + 4 * r + (q >> 2) + 32 * (q & 1);
+      const int slot = sl ^ (4 * (sl >> 5)) ^ (8 * hf);
+      aoff[k2][r] = uint32_t(kh * 2048 + hf * 1024 + slot * 16 + 8 * ((q >> 1) & 1));
+    }
+  uint32_t boff[2];
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+    const int row = 8 * (g4 >> 1) + (q >> 2);
+    const int col = 64 * wc + 32 * c + 16 * (g4 & 1) + 4 * (q & 3);
+    boff[c] = uint32_t(8192 + row * 512 + (((col >> 3) ^ (4 * (row & 3))) * 16) + ((col >> 2) & 1) * 8);
+  }
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][c][r] = 0.f;
+
+  issue(0, 0);
+  if (nch > 1) issue(1, 1);
+  int slot = 0;
+  for (int ck = 0; ck < nch; ++ck) {
+    if (ck + 1 < nch) sy_wait<5>();  // chunk ck landed, chunk ck + 1 in flight
+    else sy_wait<0>();
+    __syncthreads();  // chunk ck in every wave's view; chunk ck - 1's stage is free
+    if (ck + 2 < nch) issue(ck + 2, slot == 0 ? 2 : slot - 1);
+    const bool msk = ck == rb || r0 + 64 > a.T;  // uniform
+    const uint32_t sb = lds0 + uint32_t(slot * kDvStage);
+#pragma unroll
+    for (int k2 = 0; k2 < 2; ++k2) {
+      const int ks = 2 * kh + k2;
+      bf16x8 fa[2], fb[2];
+#pragma unroll
+      for (int ib = 0; ib < 2; ++ib) {
+        const lds_u8* pa = lds_at(sb + uint32_t(ib * 4096));
+        fa[ib] = __builtin_shufflevector(lds_tr4(pa + aoff[k2][0]), lds_tr4(pa + aoff[k2][1]), 0, 1, 2, 3, 4, 5, 6, 7);
+        if (msk) {
+          u32x4 wv = __builtin_bit_cast(u32x4, fa[ib]);
+          const int gi = r0 + 32 * ib + 16 * (g4 & 1) + q;
+          const int jb0 = ck * 64 + 16 * ks + 8 * (g4 >> 1);
+#pragma unroll
+          for (int p = 0; p < 4; ++p) {
+            const int jl = jb0 + 4 * (p >> 1) + 2 * (p & 1);
+            const bool iok = gi < a.T;
+            const uint32_t keep = ((iok && jl < gi) ? 0xffffu : 0u) | ((iok && jl + 1 < gi) ? 0xffff0000u : 0u);
+            wv[p] &= keep;
+          }
+          fa[ib] = __builtin_bit_cast(bf16x8, wv);
+        }
+      }
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        const lds_u8* pb = lds_at(sb + boff[c] + uint32_t(ks * 16 * 512));
+        fb[c] = __builtin_shufflevector(lds_tr4(pb), lds_tr4(pb + 4 * 512), 0, 1, 2, 3, 4, 5, 6, 7);
+      }
+#pragma unroll
+      for (int ib = 0; ib < 2; ++ib)
+#pragma unroll
+        for (int c = 0; c < 2; ++c) acc[ib][c] = mma(fa[ib], fb[c], acc[ib][c]);
+    }
+    slot = slot == 2 ? 0 : slot + 1;
+  }
+
+  // the two key halves' sums into one fp32 tile [64 i][pitch], then 16-byte stores
+  __syncthreads();  // every wave's last fragment reads are done (its DMA waited above)
+  float* const tl = reinterpret_cast<float*>(sv_ring);
+  constexpr int PF = kDvPitch / 4;
+  auto tile_idx = [&](int ib, int c, int r) {
+    return (32 * ib + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)) * PF + 64 * wc + 32 * c + (lane & 31);
+  };
+  if (kh == 1) {
+#pragma unroll
+    for (int ib = 0; ib < 2; ++ib)
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) tl[tile_idx(ib, c, r)] = acc[ib][c][r];
+  }
+  __syncthreads();
+  if (kh == 0) {
+#pragma unroll
+    for (int ib = 0; ib < 2; ++ib)
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) tl[tile_idx(ib, c, r)] += acc[ib][c][r];
+  }
+  __syncthreads();
+  TO* o = static_cast<TO*>(const_cast<void*>(a.o.p)) + b * a.o.s0 + h * a.o.s1;
+  if constexpr (sizeof(TO) == 2) {
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int e = tid + 512 * v, row = e >> 5, cc = e & 31, gi = r0 + row;
+      if (gi >= a.past && gi < a.T && 8 * cc < a.D) {
+        const f32x4 x0 = *reinterpret_cast<const f32x4*>(tl + row * PF + 8 * cc);
+        const f32x4 x1 = *reinterpret_cast<const f32x4*>(tl + row * PF + 8 * cc + 4);
+        *reinterpret_cast<u32x4*>(o + int64_t(gi - a.past) * a.o.s2 + 8 * cc) =
+            u32x4{pack_bf2(x0[0], x0[1]), pack_bf2(x0[2], x0[3]), pack_bf2(x1[0], x1[1]), pack_bf2(x1[2], x1[3])};
+      }
+    }
+  } else {
+#pragma unroll
+    for (int v = 0; v < 8; ++v) {
+      const int e = tid + 512 * v, row = e >> 6, cc = e & 63, gi = r0 + row;
+      if (gi >= a.past && gi < a.T && 4 * cc < a.D)
+        *reinterpret_cast<f32x4*>(o + int64_t(gi - a.past) * a.o.s2 + 4 * cc) =
+            *reinterpret_cast<const f32x4*>(tl + row * PF + 4 * cc);
+    }
+  }
+}
+
 template <typename TO, typename TV>
 int launch_sy_sv(const SvArgs& sa, dim3 grid, hipStream_t s) {
   const int ns = sa.nsplit;
@@ -2201,6 +2388,13 @@ int sy_run(const bdh_tensor4* q, const bdh_tensor4* k, const bdh_tensor4* v, con
     sc.v.p = static_cast<const char*>(v->data) + d0 * esize(v->dtype);
     sc.o.p = static_cast<const char*>(out->data) + d0 * esize(out->dtype);
     sc.D = int(std::min<int64_t>(256, Dv - d0));
+    // one split, bf16 V in 16-byte rows, 16-byte output rows, V offsets within
+    // 32 bits: the DMA ring
+    if (sc.nsplit == 1 && v16 && sc.o16 && rows16(v) && ((T - 1) * v->stride[2] + 256) * 2 < (int64_t(1) << 32)) {
+      if (o16) BDH_LAUNCH("k_sv_dma", (k_sv_dma<bf16_t>), gsv, dim3(512), 0, s, sc);
+      else BDH_LAUNCH("k_sv_dma", (k_sv_dma<float>), gsv, dim3(512), 0, s, sc);
+      continue;
+    }
     const int rc = o16 ? (v16 ? launch_sy_sv<bf16_t, bf16_t>(sc, gsv, s) : launch_sy_sv<bf16_t, float>(sc, gsv, s))
                        : (v16 ? launch_sy_sv<float, bf16_t>(sc, gsv, s) : launch_sy_sv<float, float>(sc, gsv, s));
     if (rc != BDH_OK) return rc;

@@ -4,7 +4,7 @@ CPU only: the launch plans and index formulas of the kernels the harness's
 HIP legs run (csrc/syrk.hip: k_sy_scores work items, their x loads and
 partial-tile stores, k_sy_sv's partial, V and output accesses;
 csrc/decode.hip: k_decode_bf16's key, q and partial accesses; the training
-backward's k_dq_sy B loads on x, k_dv_sy and k_dv_dma; csrc/model.hip: k_gated_gemm's
+backward's k_dq_sy B loads on x, k_dv_sy and k_dv_dma, the forward's k_sv_dma; csrc/model.hip: k_gated_gemm's
 LDS-DMA operand loads and epilogue x loads; csrc/gated_dec.hip: k_gated_dec's
 grid, operand DMA, LDS fragment reads and partial stores; csrc/enc.hip: k_relu_enc's grid,
 encoder DMA, fragment and tile accesses and output stores) are restated here and evaluated over every
@@ -348,6 +348,89 @@ def check_dv_dma(B, nh, Hv, T, N, D, p, d_strides, d_numel):
                 stored = 8 * (r >> 2) + 4 * (l >> 5) + (r & 3)
                 assert stored == 16 * hf + 8 * (t >> 2) + 4 * (l >> 5) + (t & 3)
     assert 64 * DV_PITCH <= DV_RING * DV_STAGE and DV_PITCH % 16 == 0
+
+
+def check_sv_dma(B, nh, Hv, T, N, D, p, v_strides, v_numel):
+    """csrc/syrk.hip k_sv_dma (one split, bf16 V): the k_sy_sv grid; per key chunk wave w
+    moves half w & 1 of M block (w >> 2, (w >> 1) & 1) (DMA lane l loads stored lane
+    l ^ 4 (l / 32) ^ 8 hf, a permutation of the 64) and V rows 8 w + 2 v + lane / 32
+    (clamped to T - 1, chunk (lane % 32) ^ 4 (row & 3) clamped to Dc / 8 - 1) into stage
+    (chunk % 3) of the 120 KB ring; the transposing A reads find, for every lane and key,
+    the stored element (row i, key j) in its LDS slot; B reads and the output tile stay
+    in the ring."""
+    assert p["nsplit"] == 1
+    nslab = B * nh
+    nrb = (T + 63) // 64
+    ntl = p["ntl"]
+    part_bytes = nslab * ntl * TILE_ELEMS * 2
+    lane = np.arange(64)
+    for hf in (0, 1):
+        perm = lane ^ (4 * (lane >> 5)) ^ (8 * hf)
+        assert sorted(perm) == list(range(64))
+    # element (i, j) of a stored 32 x 32 block: half i >> 4, stored lane j + 32 ((i >> 2) & 1),
+    # value 4 ((i >> 3) & 1) + (i & 3); LDS slot of stored lane L' in half hf: L' ^ 4 (L' >> 5) ^ 8 hf
+    def lds_byte(i, j):
+        hf = i >> 4
+        lp = j + 32 * ((i >> 2) & 1)
+        slot = lp ^ (4 * (lp >> 5)) ^ (8 * hf)
+        return hf * 1024 + slot * 16 + 2 * (4 * ((i >> 3) & 1) + (i & 3))
+    # ds_read_b64_tr_b16 within a group of 16 lanes: result lane q, value e is element q & 3
+    # of the 8 bytes read by lane 4 e + q / 4
+    for k2 in (0, 1):
+        for r in (0, 1):
+            for l in range(64):
+                g4, q = l >> 4, l & 15
+                for e in range(4):
+                    s = 4 * e + (q >> 2)
+                    sl = 16 * k2 + 8 * (g4 >> 1) + 4 * r + (s >> 2) + 32 * (s & 1)
+                    slot = sl ^ (4 * (sl >> 5)) ^ (8 * (g4 & 1))
+                    addr = (g4 & 1) * 1024 + slot * 16 + 8 * ((s >> 1) & 1) + 2 * (q & 3)
+                    i = 16 * (g4 & 1) + q
+                    j = 16 * k2 + 8 * (g4 >> 1) + 4 * r + e
+                    assert addr == lds_byte(i, j), (k2, r, l, e)
+    for d0 in range(0, D, 256):
+        Dc = min(256, D - d0)
+        for slab in sorted({0, nslab - 1}):  # the V base of the first and last slab
+            b, h = divmod(slab, nh)
+            hv = 0 if Hv == 1 else h
+            for rb in range(nrb):
+                r0 = rb * 64
+                nch = (min(T, r0 + 64) + 63) // 64
+                ti = r0 >> 8
+                for ck in range(nch):
+                    tj = (ck * 64) >> 8
+                    assert tj <= ti
+                    tile = (slab * ntl + ti * (ti + 1) // 2 + tj) * TILE_ELEMS * 2
+                    assert tile + 63 * 2048 + 1024 + 63 * 16 + 16 <= part_bytes
+                    slot = ck % DV_RING
+                    for w in range(8):
+                        for v in range(4):
+                            rr = 8 * w + 2 * v + lane // 32
+                            row = np.minimum(ck * 64 + rr, T - 1)
+                            cc = np.minimum((lane % 32) ^ (4 * (rr & 3)), Dc // 8 - 1)
+                            off = row * v_strides[2] + d0 + 8 * cc
+                            assert int((b * v_strides[0] + hv * v_strides[1] + off + 8).max()) <= v_numel
+                            assert int(((row * v_strides[2] + 8 * cc) * 2 + 16).max()) < 2 ** 32
+                            assert slot * DV_STAGE + 8192 + 4096 * w + 1024 * v + 64 * 16 <= (slot + 1) * DV_STAGE
+    for w in range(8):
+        kh, wc = w >> 2, w & 3
+        for k2 in (0, 1):
+            ks = 2 * kh + k2
+            for c in (0, 1):
+                g4, q = lane >> 4, lane & 15
+                row = 8 * (g4 >> 1) + (q >> 2)
+                col = 64 * wc + 32 * c + 16 * (g4 & 1) + 4 * (q & 3)
+                boff = 8192 + row * 512 + (((col >> 3) ^ (4 * (row & 3))) * 16) + ((col >> 2) & 1) * 8
+                assert int((boff + ks * 16 * 512 + 4 * 512 + 8).max()) <= DV_STAGE
+            for ib in (0, 1):
+                assert ib * 4096 + kh * 2048 + 1024 + 63 * 16 + 16 <= 8192
+
+
+@pytest.mark.parametrize("B,nh,Hv,T,N,D", [(16, 4, 1, 1024, 256, 256), (8, 4, 1, 1000, 256, 192), (8, 4, 4, 700, 256, 64),
+                                            (130, 1, 1, 33, 256, 128), (8, 4, 1, 520, 256, 512)])
+def test_sv_ring_launches_stay_in_bounds(B, nh, Hv, T, N, D):
+    p = sy_plan(B * nh, T, N)
+    check_sv_dma(B, nh, Hv, T, N, D, p, (Hv * T * D, T * D, D), B * Hv * T * D)
 
 
 @pytest.mark.parametrize("B,nh,Hv,T,N,D", [(16, 4, 1, 1024, 256, 256), (8, 4, 1, 1000, 256, 192), (8, 4, 4, 700, 256, 64),
