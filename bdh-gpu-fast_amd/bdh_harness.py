@@ -354,7 +354,12 @@ class BDH(nn.Module):
             else:
                 x_bthn = _encode(x, self.encoder)
             x_sparse = x_bthn.permute(0, 2, 1, 3)  # (B, nh, T, N) view
-            y_kv = self._attention(level, x_sparse, x.unsqueeze(1), rope_start, cache, impl, cos_sin)
+            v_tok = x.unsqueeze(1)
+            if fast and cache is None and x_sparse.dtype == torch.bfloat16 and v_tok.dtype == torch.float32:
+                # the bf16 product rounds V to bf16 (autocast's matmul, bdh.py:405-412);
+                # rounded once here, the score x V pass streams half the bytes
+                v_tok = v_tok.to(torch.bfloat16)
+            y_kv = self._attention(level, x_sparse, v_tok, rope_start, cache, impl, cos_sin)
             if fast:
                 y_ln = _ln_fast(y_kv, dt=_compute_dtype(x_bthn))
                 if _chains_decoder(x_bthn, y_ln, prep["dec"]):
