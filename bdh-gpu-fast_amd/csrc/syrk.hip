@@ -1690,16 +1690,16 @@ __global__ __launch_bounds__(512, 1) void k_sy_sv(const SvArgs a) {
   uint8_t* const vblk = sv_lds + 64 * 128;   // 64 x 512 bytes
   float* const red = reinterpret_cast<float*>(sv_lds);
   constexpr int VL = sizeof(TV) == 2 ? 1 : 2;  // 16-byte loads per 8 V elements
-  // Workgroups go to the XCDs round robin by linear id L.  XCD x takes the
-  // slabs [x nsx, (x + 1) nsx), consecutive heads of one batch element, which
-  // read the same V rows (one L2 holds them).  On each XCD the row blocks go
-  // longest first (block rb has rb + 1 key chunks): the k-th workgroup of XCD
-  // x is slab x nsx + k % nsx, block nrbk - 1 - k / nsx, so when the grid takes
-  // more than one round of the CUs the last workgroups to start are the short
-  // ones.
+  // Workgroups go to the XCDs round robin by linear id L.  The row blocks of
+  // slab s run on XCD s % 8, the XCD whose L2 took the slab's partial tiles
+  // in the score kernel (this kernel serves the few-slab shapes that split K,
+  // whose tiles fit the L2s).  On each XCD the row blocks go longest first
+  // (block rb has rb + 1 key chunks): the k-th workgroup of XCD x is slab
+  // 8 (k % nsx) + x, block nrbk - 1 - k / nsx, so when the grid takes more than
+  // one round of the CUs the last workgroups to start are the short ones.
   const int nrbk = a.nrbk, nsx = (a.nslab + 7) / 8;
   const int L = blockIdx.x, xcdv = L & 7, kk = L >> 3;
-  const int slab = xcdv * nsx + kk % nsx;
+  const int slab = (kk % nsx) * 8 + xcdv;
   if (slab >= a.nslab) return;
   const int rb = nrbk - 1 - kk / nsx + a.rb0;
   const int b = slab / a.H, h = slab - b * a.H, hv = a.Hv == 1 ? 0 : h;

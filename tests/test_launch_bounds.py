@@ -112,13 +112,14 @@ def check_scores(B, nh, T, N, strides, numel):
     return p
 
 
-def sv_grid(nslab, nrb):
-    """csrc/syrk.hip k_sy_sv: (rb, slab) of each linear workgroup id (None past the slabs)."""
+def sv_grid(nslab, nrb, contiguous=False):
+    """csrc/syrk.hip k_sy_sv (slab s on XCD s % 8) and k_sv_dma (XCD x holds slabs
+    [x nsx, (x + 1) nsx)): (rb, slab) of each linear workgroup id (None past the slabs)."""
     out = []
     nsx = (nslab + 7) // 8
     for L in range(8 * nsx * nrb):
         xcd, kk = L & 7, L >> 3
-        slab = xcd * nsx + kk % nsx
+        slab = xcd * nsx + kk % nsx if contiguous else (kk % nsx) * 8 + xcd
         out.append(None if slab >= nslab else (nrb - 1 - kk // nsx, slab))
     return out
 
@@ -129,13 +130,15 @@ def check_sv(B, nh, T, D, p, v_strides, v_numel):
     nrb = (T + 63) // 64
     S, ntl = p["nsplit"], p["ntl"]
     part_elems = nslab * ntl * S * TILE_ELEMS
-    # the 1-D grid visits each (row block, slab) once; XCD x holds the slabs
-    # [x nsx, (x + 1) nsx), row blocks longest first
-    grid = sv_grid(nslab, nrb)
-    live = [g for g in grid if g is not None]
-    assert sorted(live) == sorted((rb, s) for s in range(nslab) for rb in range(nrb))
+    # the 1-D grid visits each (row block, slab) once; slab s sits on XCD s % 8
+    # (k_sy_sv) or XCD s / nsx (k_sv_dma), row blocks longest first
     nsx = (nslab + 7) // 8
-    assert all(g[1] // nsx == L % 8 for L, g in enumerate(grid) if g is not None)
+    for contiguous in (False, True):
+        grid = sv_grid(nslab, nrb, contiguous)
+        live = [g for g in grid if g is not None]
+        assert sorted(live) == sorted((rb, s) for s in range(nslab) for rb in range(nrb))
+        assert all((g[1] // nsx if contiguous else g[1] % 8) == L % 8 for L, g in enumerate(grid) if g is not None)
+    grid = sv_grid(nslab, nrb)
     # on each XCD the row blocks (rb + 1 key chunks each) start longest first
     for x in range(8):
         rbs = [g[0] for L, g in enumerate(grid) if L % 8 == x and g is not None]
