@@ -103,16 +103,21 @@ def _ln_rows_ok(t: torch.Tensor) -> bool:
     return t.dtype in (torch.float32, torch.bfloat16) and d % 64 == 0 and d <= 1024 and (d // 64) & (d // 64 - 1) == 0
 
 
-def _ln_fast(y: torch.Tensor, x: Optional[torch.Tensor] = None, dt: Optional[torch.dtype] = None) -> torch.Tensor:
+def _ln_fast(y: torch.Tensor, x: Optional[torch.Tensor] = None, dt: Optional[torch.dtype] = None,
+             out_bf16: Optional[torch.Tensor] = None) -> torch.Tensor:
     """``LN(y)`` (in ``dt``) or ``LN(x + LN(y))`` (in x's dtype) as one HIP pass: the
     LayerNorm of the reference's _ln / _residual_ln (bdh.py:565-574, 731-750), fp32
-    arithmetic as under autocast."""
+    arithmetic as under autocast.  ``out_bf16`` also receives the result in bf16."""
     if _ln_rows_ok(y) and (x is None or _ln_rows_ok(x)):
-        return kernels.layer_norm_rows(y, x, out_dtype=x.dtype if x is not None else dt)
+        return kernels.layer_norm_rows(y, x, out_dtype=x.dtype if x is not None else dt, out_bf16=out_bf16)
     if x is None:
         out = _ln(y.float())
-        return out.to(dt) if dt is not None else out
-    return _ln(x + _ln(y.float()))
+        out = out.to(dt) if dt is not None else out
+    else:
+        out = _ln(x + _ln(y.float()))
+    if out_bf16 is not None:
+        out_bf16.copy_(out)
+    return out
 
 
 # The dense products are 2-D matrix products (hipBLASLt GEMMs) on contiguous
@@ -308,7 +313,8 @@ class BDH(nn.Module):
             return kernels.bdh_attn(qr, qr, v_tok, impl="eager")
         S = cache.seq_len
         slot_kr, slot_v = cache.slot(level, T)
-        slot_v.copy_(v_tok)
+        if not (v_tok.data_ptr() == slot_v.data_ptr() and v_tok.shape == slot_v.shape and v_tok.stride() == slot_v.stride()):
+            slot_v.copy_(v_tok)  # (the residual LayerNorm may have written the slot already)
         if impl == "hip" and S == 0 and T > 1:
             # cold prefill into an empty cache: RoPE(x) lands in the KR slot from the fused kernel
             return kernels.bdh_attn_rope(x_sparse, slot_v, self.freqs, 0, out_kr=slot_kr, impl="hip")
@@ -348,17 +354,27 @@ class BDH(nn.Module):
         fast = impl == "hip" and not torch.is_grad_enabled()
         x = _ln(self.embed(idx))  # (B, T, D)
         prep = self._prepared(_compute_dtype(x)) if fast else None
+        # Under bf16 compute the encoder and the attention's V take the fp32 residual
+        # stream x rounded to bf16 (autocast's matmuls, bdh.py:396-413, 861-912).  From
+        # layer 1 on the residual LayerNorm writes that copy (xb) beside x; into the KV
+        # cache's V slot when the cache stores bf16, so a decode step makes neither a
+        # cast nor a slot copy.  The bits are those of x.to(bf16).
+        xb = None
+        v_bf16 = fast and (cache is None or (isinstance(cache, KVCache) and cache.dtype == torch.bfloat16))
         for level in range(cfg.n_layer):
             if fast:
-                x_bthn = _encode_fast(x, prep, nh)
+                x_bthn = _encode_fast(x if xb is None else xb, prep, nh)
             else:
                 x_bthn = _encode(x, self.encoder)
             x_sparse = x_bthn.permute(0, 2, 1, 3)  # (B, nh, T, N) view
             v_tok = x.unsqueeze(1)
-            if fast and cache is None and x_sparse.dtype == torch.bfloat16 and v_tok.dtype == torch.float32:
-                # the bf16 product rounds V to bf16 (autocast's matmul, bdh.py:405-412);
-                # rounded once here, the score x V pass streams half the bytes
-                v_tok = v_tok.to(torch.bfloat16)
+            if v_bf16 and x_sparse.dtype == torch.bfloat16 and v_tok.dtype == torch.float32:
+                # rounded once, the score x V pass streams half the bytes
+                if xb is not None:
+                    # (with a cache: the V slot the residual LayerNorm wrote, as the slot's own view)
+                    v_tok = cache.slot(level, T)[1] if cache is not None else xb.unsqueeze(1)
+                elif cache is None:
+                    v_tok = v_tok.to(torch.bfloat16)
             y_kv = self._attention(level, x_sparse, v_tok, rope_start, cache, impl, cos_sin)
             if fast:
                 y_ln = _ln_fast(y_kv, dt=_compute_dtype(x_bthn))
@@ -375,7 +391,16 @@ class BDH(nn.Module):
             else:
                 xy = x_bthn * _encode_heads(_ln(y_kv), self.encoder_v)
                 y_mlp = xy.view(B, T, nh * N) @ self.decoder
-            x = _ln_fast(y_mlp, x) if fast else _ln(x + _ln(y_mlp))
+            if fast:
+                xb = None
+                if level + 1 < cfg.n_layer and x_bthn.dtype == torch.bfloat16 and x.dtype == torch.float32:
+                    if v_bf16 and cache is not None:
+                        xb = cache.slot(level + 1, T)[1][:, 0]  # (B, T, D) view of the next layer's V rows
+                    else:
+                        xb = torch.empty(B, T, x.size(-1), dtype=torch.bfloat16, device=x.device)
+                x = _ln_fast(y_mlp, x, out_bf16=xb)
+            else:
+                x = _ln(x + _ln(y_mlp))
         if isinstance(cache, CacheManager):
             cache.commit()
         elif cache is not None:

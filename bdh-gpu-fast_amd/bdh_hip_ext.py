@@ -92,6 +92,7 @@ EXPORTED_SYMBOLS = (
     "bdh_small_gemm_workspace",
     "bdh_small_gemm",
     "bdh_layer_norm_rows",
+    "bdh_layer_norm_rows2",
     "bdh_profile_enable",
     "bdh_profile_collect",
 )
@@ -152,6 +153,7 @@ def _load():
         "bdh_tril_rope_score_v_bwd_saved": (ctypes.c_int, [P, P, P, fp, i64, P, P, vp, sz, vp, sz, vp]),
         "bdh_relu_mul": (ctypes.c_int, [P, P, P, vp]),
         "bdh_layer_norm_rows": (ctypes.c_int, [P, P, P, vp]),
+        "bdh_layer_norm_rows2": (ctypes.c_int, [P, P, P, P, vp]),
         "bdh_gated_gemm": (ctypes.c_int, [P, P, P, P, vp]),
         "bdh_relu_gemm": (ctypes.c_int, [P, P, P, vp]),
         "bdh_gated_decoder_workspace": (sz, [i64, i64]),
@@ -632,11 +634,12 @@ def relu_mul(x: torch.Tensor, y: torch.Tensor, out: Optional[torch.Tensor] = Non
 
 
 def layer_norm_rows(y: torch.Tensor, x: Optional[torch.Tensor] = None, out_dtype: Optional[torch.dtype] = None,
-                    out: Optional[torch.Tensor] = None) -> torch.Tensor:
+                    out: Optional[torch.Tensor] = None, out_bf16: Optional[torch.Tensor] = None) -> torch.Tensor:
     """LayerNorm over the last dim (no affine, eps 1e-5): ``LN(y)``, or ``LN(x + LN(y))``
     with ``x``; 1- to 4-D tensors of one shape, fp32 or bf16; ``out`` defaults to a
-    contiguous tensor in ``out_dtype`` (y's dtype)."""
-    dev = _require_device(y, x, out)
+    contiguous tensor in ``out_dtype`` (y's dtype).  ``out_bf16`` (bf16, y's shape, any
+    strides) also receives the result rounded once to bf16."""
+    dev = _require_device(y, x, out, out_bf16)
     if x is not None and x.shape != y.shape:
         raise ValueError(f"layer_norm_rows: x {tuple(x.shape)} and y {tuple(y.shape)} differ")
     if out is None:
@@ -646,8 +649,15 @@ def layer_norm_rows(y: torch.Tensor, x: Optional[torch.Tensor] = None, out_dtype
         return t.reshape((1,) * (4 - t.dim()) + tuple(t.shape)) if t.dim() < 4 else t
 
     with torch.cuda.device(dev):
-        rc = _lib.bdh_layer_norm_rows(ctypes.byref(_t4(v4(x))) if x is not None else None, ctypes.byref(_t4(v4(y))),
-                                      ctypes.byref(_t4(v4(out))), _stream(dev))
+        if out_bf16 is None:
+            rc = _lib.bdh_layer_norm_rows(ctypes.byref(_t4(v4(x))) if x is not None else None,
+                                          ctypes.byref(_t4(v4(y))), ctypes.byref(_t4(v4(out))), _stream(dev))
+        else:
+            if out_bf16.shape != y.shape:
+                raise ValueError(f"layer_norm_rows: out_bf16 {tuple(out_bf16.shape)} and y {tuple(y.shape)} differ")
+            rc = _lib.bdh_layer_norm_rows2(ctypes.byref(_t4(v4(x))) if x is not None else None,
+                                           ctypes.byref(_t4(v4(y))), ctypes.byref(_t4(v4(out))),
+                                           ctypes.byref(_t4(v4(out_bf16))), _stream(dev))
     _check(rc, "layer_norm_rows")
     return out
 

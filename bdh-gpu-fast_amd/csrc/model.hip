@@ -414,6 +414,7 @@ __global__ __launch_bounds__(256) void k_small_gemm_reduce(const float* part, in
 // three dims of 4-D strided views.
 struct LnArgs {
   View x, y, o;
+  View o2 = {nullptr, 0, 0, 0};  // optional second output, bf16 (the same values rounded once)
   int64_t d1, d2, rows;
   int D;
 };
@@ -459,6 +460,11 @@ __global__ __launch_bounds__(256) void k_ln_rows(const LnArgs a) {
   TO* o = static_cast<TO*>(const_cast<void*>(a.o.p)) + i0 * a.o.s0 + i1 * a.o.s1 + i2 * a.o.s2;
 #pragma unroll
   for (int e = 0; e < E; ++e) o[lane + 64 * e] = from_f<TO>(v[e]);
+  if (a.o2.p != nullptr) {
+    bf16_t* o2 = static_cast<bf16_t*>(const_cast<void*>(a.o2.p)) + i0 * a.o2.s0 + i1 * a.o2.s1 + i2 * a.o2.s2;
+#pragma unroll
+    for (int e = 0; e < E; ++e) o2[lane + 64 * e] = f2bf(v[e]);
+  }
 }
 
 struct SmallGemmPlan {
@@ -514,14 +520,23 @@ int launch_ln_rows_o(const LnArgs& a, int32_t odt, dim3 grid, hipStream_t s) {
 
 using namespace bdh;
 
-extern "C" int bdh_layer_norm_rows(const bdh_tensor4* x, const bdh_tensor4* y, const bdh_tensor4* out,
-                                   bdh_stream stream) {
+namespace {
+int layer_norm_rows(const bdh_tensor4* x, const bdh_tensor4* y, const bdh_tensor4* out, const bdh_tensor4* out2,
+                    bdh_stream stream) {
   BDH_TRY(check_view(y));
   BDH_TRY(check_view(out));
   if (x != nullptr) BDH_TRY(check_view(x));
   for (int i = 0; i < 4; ++i)
     if (out->size[i] != y->size[i] || (x != nullptr && x->size[i] != y->size[i])) return BDH_ERR_SHAPE;
   if (views_overlap(out, y) || (x != nullptr && views_overlap(out, x))) return BDH_ERR_ALIAS;
+  if (out2 != nullptr) {
+    BDH_TRY(check_view(out2));
+    if (out2->dtype != BDH_BF16) return BDH_ERR_DTYPE;
+    for (int i = 0; i < 4; ++i)
+      if (out2->size[i] != y->size[i]) return BDH_ERR_SHAPE;
+    if (views_overlap(out2, y) || views_overlap(out2, out) || (x != nullptr && views_overlap(out2, x)))
+      return BDH_ERR_ALIAS;
+  }
   if (numel4(out) == 0) return BDH_OK;
   const int64_t D = y->size[3];
   if (D % 64 != 0 || D > 1024 || ((D / 64) & (D / 64 - 1)) != 0) return BDH_ERR_SHAPE;
@@ -539,6 +554,7 @@ extern "C" int bdh_layer_norm_rows(const bdh_tensor4* x, const bdh_tensor4* y, c
   a.x = x != nullptr ? view(x) : View{nullptr, 0, 0, 0};
   a.y = view(y);
   a.o = view(out);
+  if (out2 != nullptr) a.o2 = view(out2);
   a.d1 = y->size[1];
   a.d2 = y->size[2];
   a.rows = rows;
@@ -551,6 +567,18 @@ extern "C" int bdh_layer_norm_rows(const bdh_tensor4* x, const bdh_tensor4* y, c
               : launch_ln_rows_o<bf16_t, float>(a, out->dtype, grid, s);
   return yb ? launch_ln_rows_o<float, bf16_t>(a, out->dtype, grid, s)
             : launch_ln_rows_o<float, float>(a, out->dtype, grid, s);
+}
+}  // namespace
+
+extern "C" int bdh_layer_norm_rows(const bdh_tensor4* x, const bdh_tensor4* y, const bdh_tensor4* out,
+                                   bdh_stream stream) {
+  return layer_norm_rows(x, y, out, nullptr, stream);
+}
+
+extern "C" int bdh_layer_norm_rows2(const bdh_tensor4* x, const bdh_tensor4* y, const bdh_tensor4* out,
+                                    const bdh_tensor4* out_bf16, bdh_stream stream) {
+  if (out_bf16 == nullptr) return BDH_ERR_ARG;
+  return layer_norm_rows(x, y, out, out_bf16, stream);
 }
 
 extern "C" int bdh_relu_mul(const bdh_tensor4* x, const bdh_tensor4* y, const bdh_tensor4* out,

@@ -157,10 +157,12 @@ def gated_decoder(y: torch.Tensor, wt: torch.Tensor, x: torch.Tensor, dec: torch
 
 
 def layer_norm_rows(y: torch.Tensor, x: Optional[torch.Tensor] = None,
-                    out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
-    """``LN(y)`` or ``LN(x + LN(y))`` over the last dim on the GPU (bdh.py:565-574, 731-750)."""
-    ext = _require(y, x)
-    return ext.layer_norm_rows(_last_dim_unit(y), _last_dim_unit(x) if x is not None else None, out_dtype)
+                    out_dtype: Optional[torch.dtype] = None, out_bf16: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """``LN(y)`` or ``LN(x + LN(y))`` over the last dim on the GPU (bdh.py:565-574, 731-750);
+    ``out_bf16`` (bf16, y's shape) also receives the result rounded once to bf16."""
+    ext = _require(y, x, out_bf16)
+    return ext.layer_norm_rows(_last_dim_unit(y), _last_dim_unit(x) if x is not None else None, out_dtype,
+                               out_bf16=out_bf16)
 
 
 def small_gemm(a: torch.Tensor, b: torch.Tensor, out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:

@@ -329,6 +329,19 @@ int bdh_layer_norm_rows(const bdh_tensor4* x, const bdh_tensor4* y,
                         const bdh_tensor4* out, bdh_stream stream);
 
 /*
+ * bdh_layer_norm_rows that also writes the result rounded once to bf16 into
+ * out_bf16 (one shape with y, bf16, any strides, overlapping no other
+ * operand).  The model's bf16 forward feeds the next layer's encoder and
+ * attention V (bdh.py:396-413, 861-912, under autocast both take the residual
+ * stream in bf16) from it without a cast pass; a decode step writes it
+ * straight into the KV cache's V slot.  The two outputs hold the same values:
+ * out_bf16 equals out converted to bf16 (round to nearest even).
+ */
+int bdh_layer_norm_rows2(const bdh_tensor4* x, const bdh_tensor4* y,
+                         const bdh_tensor4* out, const bdh_tensor4* out_bf16,
+                         bdh_stream stream);
+
+/*
  * Per-kernel timing (measurement support; no counterpart in the reference).
  * While enabled, every kernel the library launches is bracketed by HIP events
  * on its stream.  bdh_profile_collect() waits for the recorded events and

@@ -440,3 +440,26 @@ def test_layer_norm_rows_matches_reference(D, dy, dx, do):
     assert got.shape == want.shape and got.dtype == do
     tol = 1e-5 if do == torch.float32 else 2.0 ** -8
     assert rel_fro(got.float().cpu().numpy(), want.numpy()) <= tol
+
+
+@pytest.mark.parametrize("D", [256, 512])
+@pytest.mark.parametrize("dy", [torch.bfloat16, torch.float32])
+def test_layer_norm_rows_bf16_second_output(D, dy):
+    """``bdh_layer_norm_rows2``: the residual LN's fp32 output and its bf16 copy,
+    the copy written into a strided view (a KV cache's V slot, rows capacity
+    apart): the copy equals the fp32 output rounded to bf16 bit for bit, and the
+    fp32 output equals the one-output entry point's.  Rows outside the view are
+    untouched."""
+    g = torch.Generator().manual_seed(D + 1)
+    B, T, cap = 5, 3, 11
+    y = torch.randn(B, T, D, generator=g).to(dy).to(DEV)
+    x = torch.randn(B, T, D, generator=g).to(DEV)
+    cache = torch.full((B, 1, cap, D), 7.0, dtype=torch.bfloat16, device=DEV)
+    slot = cache[:, 0].narrow(1, 4, T)  # (B, T, D), rows cap * D apart
+    out = ext.layer_norm_rows(y, x, out_dtype=torch.float32, out_bf16=slot)
+    assert torch.equal(out, ext.layer_norm_rows(y, x, out_dtype=torch.float32))
+    assert torch.equal(slot, out.to(torch.bfloat16))
+    rest = torch.cat([cache[:, 0, :4], cache[:, 0, 4 + T:]], dim=1)
+    assert bool((rest == 7.0).all())
+    with pytest.raises(RuntimeError):
+        ext.layer_norm_rows(y, x, out_dtype=torch.float32, out_bf16=torch.empty(B, T, D, device=DEV))  # fp32
